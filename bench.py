@@ -1,0 +1,260 @@
+"""Headline benchmark of the MI355X int8 weight-only decode path.
+
+Workload: one talker decode step's GEMV chain at
+batch 1 -- 28 layers, hidden 2048, each layer = fused QKV 2048->4096 with the
+input RMSNorm fused as prologue, O 2048->2048 + residual, gate+up 2048->12288
+with the post-attention RMSNorm prologue and SiLU-gate epilogue, down
+6144->2048 + residual -- on synthetic int8 weights (uniform [-127,127],
+per-row scales uniform [1e-3,2e-2]) distinct per layer (1.41 GB, far above the
+256 MB last-level cache), x ~ N(0,1).  A step is one pass of the chain,
+replayed as a hipGraph; inputs are resident in HBM before timing.
+
+value = algorithmic bytes per step / time per step (GB/s).  The JSON line
+also carries the roofline of the dominant kernel (the gate/up GEMV, timed
+alone over its 28 per-layer launches with hipEvents on the launching
+stream), the CPU baseline (the oracle's multithreaded exact-order GEMV on
+this host), and the full codec frame step (talker + 15-step code predictor,
+config 5) through the C ABI as frames/s and real-time factor.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "qwen3-tts-native_amd"))
+
+HBM_PEAK_GBS = 8000.0
+LAYERS, HIDDEN, INTER, QW, KW = 28, 2048, 6144, 2048, 1024
+
+
+def step_benchmark(hip, steps, warmup, kernel_filter=0, use_graph=1, rows=1, mode=1):
+    b = hip.StepBenchmarkV1()
+    b.struct_size = C.sizeof(hip.StepBenchmarkV1)
+    b.layers, b.hidden, b.intermediate, b.query_width, b.key_value_width = LAYERS, HIDDEN, INTER, QW, KW
+    b.rows, b.mode, b.warmup, b.steps, b.use_graph, b.kernel_filter = rows, mode, warmup, steps, use_graph, kernel_filter
+    hip.call("qwen3_tts_benchmark_talker_step_gemvs", 0, C.byref(b))
+    return b
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """Oracle exact-order int8 GEMV chain on the host cores (bounded sample)."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(0)
+    sample_layers = 2
+    mats = []
+    for _ in range(sample_layers):
+        for out_f, in_f in ((QW + 2 * KW, HIDDEN), (HIDDEN, QW), (2 * INTER, HIDDEN), (HIDDEN, INTER)):
+            w = rng.integers(-127, 128, size=(out_f, in_f), dtype=np.int8)
+            s = rng.uniform(1e-3, 2e-2, out_f).astype(np.float32)
+            x = oracle.f32_to_bf16(rng.standard_normal(in_f).astype(np.float32))
+            mats.append((w, s, x))
+    per_layer = sum(w.nbytes + 4 * w.shape[0] + 2 * w.shape[1] + 2 * w.shape[0] for w, _, _ in mats) / sample_layers
+    t0 = time.perf_counter()
+    layers_done = 0
+    while True:
+        for w, s, x in mats:
+            oracle.int8_gemm_rows_mt(w, s, x, threads)
+        layers_done += sample_layers
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(per_layer * layers_done / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{layers_done} talker-layer GEMV chains (QKV, O, gate+up, down; {sample_layers} distinct "
+                  f"layers cycled) in {dt:.1f} s with the oracle's exact-order int8 GEMV on {threads} threads",
+    }
+
+
+def frame_benchmark(hip, frames: int = 200, prompt: int = 824, max_seq: int = 1024):
+    """Config 5 through the reference C ABI: VoiceDesign geometry, synthetic
+    bf16 weights quantized to int8 at finalize, prompt of `prompt` tokens,
+    then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed."""
+    import numpy as np
+
+    lib = hip.load()
+    cfg = hip.default_config()
+    model = C.c_void_p()
+    hip.call("qwen3_tts_model_create", 0, C.byref(model))
+    scratch = []
+    try:
+        T, P = (cfg.talker_hidden, cfg.talker_intermediate, cfg.talker_query_heads * 128,
+                cfg.talker_key_value_heads * 128), \
+               (cfg.predictor_hidden, cfg.predictor_intermediate, cfg.predictor_query_heads * 128,
+                cfg.predictor_key_value_heads * 128)
+        tensors = []
+
+        def layer(prefix, d):
+            h, i, qw, kw = d
+            return [(f"{prefix}.input_layernorm.weight", (h,), 1.0), (f"{prefix}.self_attn.q_proj.weight", (qw, h), 0),
+                    (f"{prefix}.self_attn.k_proj.weight", (kw, h), 0), (f"{prefix}.self_attn.v_proj.weight", (kw, h), 0),
+                    (f"{prefix}.self_attn.o_proj.weight", (h, qw), 0), (f"{prefix}.self_attn.q_norm.weight", (128,), 1.0),
+                    (f"{prefix}.self_attn.k_norm.weight", (128,), 1.0),
+                    (f"{prefix}.post_attention_layernorm.weight", (h,), 1.0),
+                    (f"{prefix}.mlp.gate_proj.weight", (i, h), 0), (f"{prefix}.mlp.up_proj.weight", (i, h), 0),
+                    (f"{prefix}.mlp.down_proj.weight", (h, i), 0)]
+
+        H = T[0]
+        tensors += [("talker.model.codec_embedding.weight", (cfg.talker_vocabulary, H), 0),
+                    ("talker.model.text_embedding.weight", (cfg.text_vocabulary, H), 0),
+                    ("talker.text_projection.linear_fc1.weight", (H, H), 0),
+                    ("talker.text_projection.linear_fc1.bias", (H,), 0),
+                    ("talker.text_projection.linear_fc2.weight", (H, H), 0),
+                    ("talker.text_projection.linear_fc2.bias", (H,), 0),
+                    ("talker.model.norm.weight", (H,), 1.0),
+                    ("talker.codec_head.weight", (cfg.talker_vocabulary, H), 0),
+                    ("talker.code_predictor.small_to_mtp_projection.weight", (P[0], H), 0),
+                    ("talker.code_predictor.small_to_mtp_projection.bias", (P[0],), 0),
+                    ("talker.code_predictor.model.norm.weight", (P[0],), 1.0)]
+        for l in range(cfg.talker_layers):
+            tensors += layer(f"talker.model.layers.{l}", T)
+        for l in range(cfg.predictor_layers):
+            tensors += layer(f"talker.code_predictor.model.layers.{l}", P)
+        for g in range(15):
+            tensors += [(f"talker.code_predictor.model.codec_embedding.{g}.weight", (cfg.predictor_vocabulary, H), 0),
+                        (f"talker.code_predictor.lm_head.{g}.weight", (cfg.predictor_vocabulary, P[0]), 0)]
+        biggest = max(int(np.prod(s)) for _, s, _ in tensors)
+        buf = hip.DeviceArray(biggest, np.uint16)
+        scratch.append(buf)
+        for seed, (name, shape, mean) in enumerate(tensors):
+            n = int(np.prod(shape))
+            std = 0.05 if mean else (1.0 if "embedding" in name else 0.02)
+            hip.call("qwen3_tts_device_fill_bf16_normal", buf.ptr, n, 1000 + seed, C.c_float(mean), C.c_float(std), None)
+            hip.synchronize()
+            shp = (C.c_uint64 * len(shape))(*shape)
+            hip.call("qwen3_tts_model_upload_tensor", model, name.encode(), buf.ptr, 2 * n, len(shape), shp)
+        mem = hip.ModelMemory()
+        hip.call("qwen3_tts_model_finalize", model, C.byref(mem))
+        session = C.c_void_p()
+        smem = hip.SessionMemory()
+        hip.call("qwen3_tts_session_create", model, max_seq, 42, C.byref(session), C.byref(smem))
+        try:
+            rng = np.random.default_rng(1)
+            text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
+            codec = rng.integers(0, 2048, prompt).astype(np.int32)
+            ts = hip.sampling(1, 50, 1.0, 0.9, 1.05)
+            ps = hip.sampling(1, 50, 1.0, 0.9, 1.0)
+            pre = hip.PrefillResult()
+            t0 = time.perf_counter()
+            hip.call("qwen3_tts_session_prefill", session, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                     codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(pre))
+            prefill_s = time.perf_counter() - t0
+            semantic = C.c_uint16(pre.first_semantic_token)
+            codes = (C.c_uint16 * 16)()
+            info = hip.CodecFrameInfo()
+            nxt = C.c_uint16()
+            trailing = rng.integers(0, cfg.text_vocabulary, frames + 8).astype(np.int32)
+            warm = 3
+            done = 0
+            pred_ms = talk_ms = 0.0
+            eos = 0
+            t_start = None
+            for f in range(frames + warm):
+                if f == warm:
+                    hip.synchronize()
+                    t_start = time.perf_counter()
+                if semantic.value == cfg.codec_eos_token:
+                    eos += 1
+                    break
+                hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts, ps, codes, 16,
+                         C.byref(nxt), C.byref(info))
+                semantic = C.c_uint16(nxt.value)
+                if f >= warm:
+                    done += 1
+                    pred_ms += info.predictor_gpu_milliseconds
+                    talk_ms += info.talker_gpu_milliseconds
+            wall = time.perf_counter() - t_start
+            frame_ms = wall * 1000.0 / max(done, 1)
+            return {
+                "frames": done, "prompt_tokens": prompt, "max_sequence_length": max_seq,
+                "frames_per_second": round(1000.0 / frame_ms, 2),
+                "ms_per_frame": round(frame_ms, 3),
+                "rtf": round(frame_ms / 80.0, 4),
+                "predictor_gpu_ms_per_frame": round(pred_ms / max(done, 1), 3),
+                "talker_gpu_ms_per_frame": round(talk_ms / max(done, 1), 3),
+                "prefill_seconds": round(prefill_s, 3),
+                "ended_by_eos_early": bool(eos),
+                "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9; seed 42",
+            }
+        finally:
+            lib.qwen3_tts_session_destroy(session)
+    finally:
+        lib.qwen3_tts_model_destroy(model)
+        for b in scratch:
+            b.free()
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--frames", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-frames", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the decode path on a single MI355X "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        return 2
+    import qwen3_tts_hip as hip
+
+    hip.load()
+    main_run = step_benchmark(hip, args.steps, args.warmup)
+    ms = main_run.milliseconds_per_step
+    value = main_run.algorithmic_bytes_per_step / (ms * 1e-3) / 1e9
+    # dominant kernel: the gate/up GEMV (25.2 MB int8 per launch), alone
+    dom = step_benchmark(hip, args.steps, args.warmup, kernel_filter=3)
+    launch_us = dom.milliseconds_per_step * 1000.0 / LAYERS
+    launch_bytes = dom.algorithmic_bytes_per_step / LAYERS
+    achieved = launch_bytes / (launch_us * 1e-6) / 1e9
+    line = {
+        "metric": "int8 GEMV achieved HBM GB/s (talker decode step, batch 1)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xbf16->fp32",
+        "data": "synthetic int8 weights U[-127,127], scales U[1e-3,2e-2], x ~ N(0,1); distinct weights per layer",
+        "config": {"workload": "talker decode step GEMVs, batch 1, 28 layers, hidden 2048 (configs[1])",
+                   "layers": LAYERS, "hidden": HIDDEN, "intermediate": INTER, "qkv_out": QW + 2 * KW,
+                   "rows": 1, "graph": True,
+                   "algorithmic_bytes_per_step": int(main_run.algorithmic_bytes_per_step),
+                   "weight_bytes_per_step": int(main_run.weight_bytes)},
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_exact_fixed<4, SiluRounded, norm> (gate+up 12288x2048)",
+                     "bytes_per_launch": int(launch_bytes), "us_per_launch": round(launch_us, 3)},
+    }
+    if not args.no_frames:
+        try:
+            line["frame_step"] = frame_benchmark(hip, frames=args.frames)
+        except Exception as e:  # report, never hide
+            line["frame_step"] = {"error": str(e)}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

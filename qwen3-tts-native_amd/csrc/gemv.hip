@@ -1,0 +1,639 @@
+// int8 weight-only dequantizing GEMV / skinny GEMM for gfx950.
+//
+// Semantics follow native/qwen3-tts-native/native/src/int8_gemv.cu:58-293:
+//   y[r][c] = scale[c] * sum_k float(W[c][k]) * float(x[r][k])
+// with int8 W [out][in] row-major, bf16 x, fp32 accumulation and a per-output
+// channel fp32 scale.
+//
+// Exact mode (rows == 1 by default) reproduces the reference's summation order
+// bit-for-bit: every output channel is owned by 32 lanes (half of a wave64);
+// lane l owns the 16-byte weight vectors l, l+32, l+64, ...; each vector is a
+// fresh 16-term fmaf chain that is added to the lane accumulator, and the 32
+// lane sums are folded by shuffle-down with offsets 16, 8, 4, 2, 1.  Because
+// the lane -> k mapping does not depend on the channel, each lane keeps its
+// slice of x in VGPRs for the whole kernel and the weight stream is the only
+// HBM traffic: two half-waves read two 512-byte contiguous segments per
+// 128-bit load instruction.  int8 -> fp32 is one SDWA sign-extending convert.
+//
+// Optional RMSNorm prologue (talker_kernels.cu:27-48 semantics, double bf16
+// rounding): every wave recomputes inv_rms from x with the reference's
+// 256-thread reduction tree emulated exactly (4 virtual threads per lane),
+// then normalizes the x slice it holds.  This removes the separate RMSNorm
+// launch and the normalized-activation round trip through memory.
+//
+// MFMA mode (rows 2..8): weights are dequantized int8 -> bf16 (exact) in
+// registers and fed to v_mfma_f32_16x16x32_bf16 with the session rows padded
+// to 16; the per-channel scale is applied after accumulation.
+#include "q3_common.hpp"
+#include "q3_math.h"
+
+namespace q3 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kHalfWaves = kThreads / 32;
+
+__device__ __forceinline__ float byte_f(int word, int b) {
+    return static_cast<float>(static_cast<int8_t>(word >> (8 * b)));
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming 128-bit weight load (nontemporal: weights are read once per step).
+__device__ __forceinline__ int4 stream_load(const void* p) {
+    const i32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
+// Reference 32-lane shuffle-down fold, offsets 16..1 (int8_gemv.cu:114-118).
+__device__ __forceinline__ float fold32(float value) {
+#pragma unroll
+    for (int offset = 16; offset > 0; offset >>= 1) {
+        value += __shfl_down(value, offset, 32);
+    }
+    return value;
+}
+
+// inv_rms of x[0..width) with the exact 256-thread tree of the reference's
+// block_sum (talker_kernels.cu:14-25,36-41), computed by one wave64.
+__device__ float wave_inverse_rms(const bf16_t* x, int width, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.0f;
+        for (int i = lane + 64 * j; i < width; i += 256) {
+            const float v = bf2f(x[i]);
+            s = fmaf(v, v, s);
+        }
+        part[j] = s;
+    }
+    part[0] += part[2];
+    part[1] += part[3];
+    float value = part[0] + part[1];
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        value += __shfl_down(value, offset, 64);
+    }
+    const float total = __shfl(value, 0, 64);
+    return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
+}
+
+__device__ __forceinline__ float normalize_one(float x, float inverse, float gain) {
+    return round_bf(round_bf(x * inverse) * gain);
+}
+
+// Load the 16 activations of vector `v` (bf16) as fp32, normalized if needed.
+template <bool kNorm>
+__device__ __forceinline__ void load_x16(const bf16_t* x, const bf16_t* gain, int v,
+                                         float inverse, float* out) {
+    const uint4* p = reinterpret_cast<const uint4*>(x + static_cast<size_t>(v) * 16);
+    const uint4 a = p[0];
+    const uint4 b = p[1];
+    const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        out[2 * i] = __uint_as_float(words[i] << 16);
+        out[2 * i + 1] = __uint_as_float(words[i] & 0xffff0000u);
+    }
+    if constexpr (kNorm) {
+        const uint4* g = reinterpret_cast<const uint4*>(gain + static_cast<size_t>(v) * 16);
+        const uint4 ga = g[0];
+        const uint4 gb = g[1];
+        const uint32_t gw[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            out[2 * i] = normalize_one(out[2 * i], inverse, __uint_as_float(gw[i] << 16));
+            out[2 * i + 1] =
+                normalize_one(out[2 * i + 1], inverse, __uint_as_float(gw[i] & 0xffff0000u));
+        }
+    }
+}
+
+// One 16-byte weight vector against 16 fp32 activations: the reference's
+// fresh fmaf chain (int8_gemv.cu:99-112).
+__device__ __forceinline__ float chain16(const int4 w, const float* x) {
+    const int words[4] = {w.x, w.y, w.z, w.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            sum = fmaf(byte_f(words[i], b), x[4 * i + b], sum);
+        }
+    }
+    return sum;
+}
+
+// Packed-activation variant: x as 8 words of bf16 pairs.
+__device__ __forceinline__ float chain16_packed(const int4 w, const uint32_t* xp) {
+    const int words[4] = {w.x, w.y, w.z, w.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t pair = xp[(4 * i + b) >> 1];
+            const float xv = ((b & 1) == 0) ? __uint_as_float(pair << 16)
+                                            : __uint_as_float(pair & 0xffff0000u);
+            sum = fmaf(byte_f(words[i], b), xv, sum);
+        }
+    }
+    return sum;
+}
+
+// Half-wave lane 0 epilogue for the plain / residual epilogues.
+template <int kEpi>
+__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
+    const float scale = a.scales[channel];
+    if constexpr (kEpi == kEpiStore) {
+        const float y = value * scale;
+        if (a.out32 != nullptr) a.out32[channel] = y;
+        if (a.out16 != nullptr) a.out16[channel] = f2bf(y);
+    } else if constexpr (kEpi == kEpiAddFma) {
+        a.out16[channel] = f2bf(fmaf(value, scale, bf2f(a.out16[channel])));
+    } else if constexpr (kEpi == kEpiAddRounded) {
+        const float projected = round_bf(value * scale);
+        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
+    } else if constexpr (kEpi == kEpiBias) {
+        a.out16[channel] = f2bf(round_bf(value * scale) + bf2f(a.bias[channel]));
+    } else if constexpr (kEpi == kEpiBiasSilu) {
+        float v = round_bf(value * scale) + bf2f(a.bias[channel]);
+        v *= 1.0f / (1.0f + q3_expf(-v));
+        a.out16[channel] = f2bf(v);
+    } else if constexpr (kEpi == kEpiBiasAdd) {
+        const float projected = round_bf(round_bf(value * scale) + bf2f(a.bias[channel]));
+        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
+    }
+}
+
+template <int kEpi>
+__device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
+    const float gate = g * a.scales[channel];
+    const float up = u * a.scales[a.out_features + channel];
+    if constexpr (kEpi == kEpiSiluFused) {
+        const float activated = gate / (1.0f + q3_expf(-gate));
+        a.out16[channel] = f2bf(activated * up);
+    } else {
+        const float gate16 = round_bf(gate);
+        const float up16 = round_bf(up);
+        const float activated = round_bf(gate16 / (1.0f + q3_expf(-gate16)));
+        a.out16[channel] = f2bf(activated * up16);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Exact-order GEMV, one activation row, K = kVpl * 512 known at compile time.
+// Each half-wave processes a unit of two weight rows per iteration:
+//   plain/residual epilogues: channels 2u and 2u+1;
+//   SiLU epilogues: gate row u and up row out+u.
+// ---------------------------------------------------------------------------
+template <int kVpl, int kEpi, bool kNorm>
+__global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
+    if (a.input_row_index != nullptr) {
+        a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
+    }
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    constexpr bool kPacked = kVpl > 6;
+    constexpr int kIn = kVpl * 512;
+    const int lane = threadIdx.x & 31;
+    float inverse = 1.0f;
+    if constexpr (kNorm) {
+        inverse = wave_inverse_rms(a.input, kIn, a.norm_epsilon);
+    }
+    // Activation slice of this lane: vectors lane + 32*i.
+    float xf[kPacked ? 1 : kVpl][16];
+    uint32_t xp[kPacked ? kVpl : 1][8];
+#pragma unroll
+    for (int i = 0; i < kVpl; ++i) {
+        float tmp[16];
+        load_x16<kNorm>(a.input, a.norm_weight, lane + 32 * i, inverse, tmp);
+        if constexpr (kPacked) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xp[i][j] = (__float_as_uint(tmp[2 * j]) >> 16) |
+                           (__float_as_uint(tmp[2 * j + 1]) & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xf[i][j] = tmp[j];
+        }
+    }
+
+    const int units = kSilu ? a.out_features : (a.out_features + 1) / 2;
+    const int stride = gridDim.x * kHalfWaves;
+    for (int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5); unit < units; unit += stride) {
+        const int row0 = kSilu ? unit : 2 * unit;
+        const int row1 = kSilu ? a.out_features + unit : 2 * unit + 1;
+        const bool has1 = kSilu || row1 < a.out_features;
+        const int4* w0 = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row0) * kIn);
+        const int4* w1 = reinterpret_cast<const int4*>(
+            a.weight + static_cast<size_t>(has1 ? row1 : row0) * kIn);
+        int4 r0[kVpl];
+        int4 r1[kVpl];
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) {
+            r0[i] = stream_load(w0 + lane + 32 * i);
+            r1[i] = stream_load(w1 + lane + 32 * i);
+        }
+        float acc0 = 0.0f;
+        float acc1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) {
+            if constexpr (kPacked) {
+                acc0 += chain16_packed(r0[i], xp[i]);
+                acc1 += chain16_packed(r1[i], xp[i]);
+            } else {
+                acc0 += chain16(r0[i], xf[i]);
+                acc1 += chain16(r1[i], xf[i]);
+            }
+        }
+        acc0 = fold32(acc0);
+        acc1 = fold32(acc1);
+        if (lane == 0) {
+            if constexpr (kSilu) {
+                store_gate_up<kEpi>(a, unit, acc0, acc1);
+            } else {
+                store_channel<kEpi>(a, row0, acc0);
+                if (has1) store_channel<kEpi>(a, row1, acc1);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Exact-order GEMV/GEMM for any in_features % 16 == 0 and rows 1..8.  The
+// activation vectors are re-read per weight vector (they stay in L1/L2).
+// ---------------------------------------------------------------------------
+template <int kRows, int kEpi, bool kNorm>
+__global__ __launch_bounds__(kThreads) void gemv_exact_generic(GemvArgs a) {
+    if (a.input_row_index != nullptr) {
+        a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
+    }
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    const int lane = threadIdx.x & 31;
+    const int in = a.in_features;
+    const int vectors = in / 16;
+    float inverse[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        inverse[r] = 1.0f;
+        if constexpr (kNorm) {
+            inverse[r] = wave_inverse_rms(a.input + static_cast<size_t>(r) * in, in,
+                                          a.norm_epsilon);
+        }
+    }
+    const int units = kSilu ? a.out_features : a.out_features;
+    const int stride = gridDim.x * kHalfWaves;
+    for (int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5); unit < units; unit += stride) {
+        const int row0 = unit;
+        const int row1 = kSilu ? a.out_features + unit : unit;
+        const int4* w0 = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row0) * in);
+        const int4* w1 = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row1) * in);
+        float acc0[kRows];
+        float acc1[kRows];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            acc0[r] = 0.0f;
+            acc1[r] = 0.0f;
+        }
+        for (int v = lane; v < vectors; v += 32) {
+            const int4 q0 = stream_load(w0 + v);
+            int4 q1 = q0;
+            if constexpr (kSilu) q1 = stream_load(w1 + v);
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                float xv[16];
+                load_x16<kNorm>(a.input + static_cast<size_t>(r) * in, a.norm_weight, v,
+                                inverse[r], xv);
+                acc0[r] += chain16(q0, xv);
+                if constexpr (kSilu) acc1[r] += chain16(q1, xv);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const float g = fold32(acc0[r]);
+            float u = 0.0f;
+            if constexpr (kSilu) u = fold32(acc1[r]);
+            if (lane == 0) {
+                GemvArgs row = a;
+                row.out16 = a.out16 ? a.out16 + static_cast<size_t>(r) * a.out_features : nullptr;
+                row.out32 = a.out32 ? a.out32 + static_cast<size_t>(r) * a.out_features : nullptr;
+                if constexpr (kSilu) {
+                    store_gate_up<kEpi>(row, unit, g, u);
+                } else {
+                    store_channel<kEpi>(row, unit, g);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA skinny GEMM for rows 2..8 (rows padded to 16 columns of B).
+//   A (16 x 32): lane i holds W[c0 + i%16][k-group i/16]   (int8 -> bf16)
+//   B (32 x 16): lane i holds x[i%16][k-group i/16]         (zero if i%16 >= rows)
+//   D (16 x 16): lane i holds D[4*(i/16) + j][i%16], j < 4
+// Each lane streams 16 contiguous weight bytes per step; bytes 0-7 feed the
+// first MFMA and bytes 8-15 the second, with the matching activations on the
+// B side, so every product pairs the right (W, x) elements.
+// A block owns 16 channels (two rows for SiLU: gate tile + up tile); its four
+// waves split K and fold their partial tiles through LDS.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t bytes_to_bf16x8(uint32_t lo, uint32_t hi) {
+    // int8 values are exactly representable in bf16: convert via fp32 and
+    // keep the upper half (exact, no rounding needed).
+    union {
+        uint32_t u[4];
+        bf16x8_t v;
+    } r;
+    const uint32_t words[2] = {lo, hi};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t a = __float_as_uint(byte_f(static_cast<int>(words[w]), 2 * p));
+            const uint32_t b = __float_as_uint(byte_f(static_cast<int>(words[w]), 2 * p + 1));
+            r.u[2 * w + p] = (a >> 16) | (b & 0xffff0000u);
+        }
+    }
+    return r.v;
+}
+
+__device__ __forceinline__ bf16x8_t load_bf16x8(const bf16_t* p) {
+    union {
+        uint4 q;
+        bf16x8_t v;
+    } r;
+    r.q = *reinterpret_cast<const uint4*>(p);
+    return r.v;
+}
+
+template <int kEpi, bool kNorm>
+__global__ __launch_bounds__(kThreads) void gemv_mfma(GemvArgs a) {
+    if (a.input_row_index != nullptr) {
+        a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
+    }
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    constexpr int kTiles = kSilu ? 2 : 1;
+    __shared__ float fold[4][kTiles][16][16];
+    __shared__ bf16_t xs_norm[kNorm ? 8 : 1][kNorm ? 6144 : 1];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int in = a.in_features;
+    const int rows = a.rows;
+    const int c0 = blockIdx.x * 16;
+    const bf16_t* x = a.input;
+    int x_stride = in;
+    if constexpr (kNorm) {
+        // Normalized rows staged once in LDS (in <= 6144 checked on launch).
+        for (int r = wave; r < rows; r += 4) {
+            const bf16_t* xr = a.input + static_cast<size_t>(r) * in;
+            const float inverse = wave_inverse_rms(xr, in, a.norm_epsilon);
+            for (int k = lane; k < in; k += 64) {
+                xs_norm[r][k] = f2bf(normalize_one(bf2f(xr[k]), inverse, bf2f(a.norm_weight[k])));
+            }
+        }
+        __syncthreads();
+        x = &xs_norm[0][0];
+        x_stride = 6144;
+    }
+    const int m = lane & 15;
+    const int group = lane >> 4;
+    const bool real_col = m < rows;
+    floatx4_t acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    const int slice = in / 4;  // in % 256 == 0 checked on launch
+    const int k_begin = wave * slice;
+    const int k_end = k_begin + slice;
+    const int channel = c0 + m;
+    const bool valid_channel = channel < a.out_features;
+    const int8_t* wrow[kTiles];
+    wrow[0] = a.weight + static_cast<size_t>(valid_channel ? channel : 0) * in;
+    if constexpr (kSilu) {
+        wrow[kTiles - 1] =
+            a.weight + static_cast<size_t>(a.out_features + (valid_channel ? channel : 0)) * in;
+    }
+    for (int k = k_begin + 16 * group; k < k_end; k += 64) {
+        int4 wq[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            wq[t] = stream_load(wrow[t] + k);
+        }
+        bf16x8_t b0 = {};
+        bf16x8_t b1 = {};
+        if (real_col) {
+            b0 = load_bf16x8(x + static_cast<size_t>(m) * x_stride + k);
+            b1 = load_bf16x8(x + static_cast<size_t>(m) * x_stride + k + 8);
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const bf16x8_t a0 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t].x), static_cast<uint32_t>(wq[t].y));
+            const bf16x8_t a1 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t].z), static_cast<uint32_t>(wq[t].w));
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[t], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            fold[wave][t][4 * group + j][m] = acc[t][j];  // [channel row][session col]
+        }
+    }
+    __syncthreads();
+    // 256 threads: thread -> (channel row, session col) of the 16x16 tile.
+    const int row = threadIdx.x >> 4;
+    const int col = threadIdx.x & 15;
+    const int ch = c0 + row;
+    if (col < rows && ch < a.out_features) {
+        float value[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            value[t] = ((fold[0][t][row][col] + fold[1][t][row][col]) + fold[2][t][row][col]) +
+                       fold[3][t][row][col];
+        }
+        GemvArgs r = a;
+        r.out16 = a.out16 ? a.out16 + static_cast<size_t>(col) * a.out_features : nullptr;
+        r.out32 = a.out32 ? a.out32 + static_cast<size_t>(col) * a.out_features : nullptr;
+        if constexpr (kSilu) {
+            store_gate_up<kEpi>(r, ch, value[0], value[kTiles - 1]);
+        } else {
+            store_channel<kEpi>(r, ch, value[0]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-row symmetric quantizer (int8_gemv.cu:20-52): absmax -> scale ->
+// lrint(clamp(w / scale)).  One 256-thread block per output row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const bf16_t* weight,
+                                                                 int8_t* quantized, float* scales,
+                                                                 int in_features) {
+    __shared__ float partial[kThreads];
+    const size_t offset = static_cast<size_t>(blockIdx.x) * in_features;
+    const bf16_t* row = weight + offset;
+    float maximum = 0.0f;
+    for (int i = threadIdx.x; i < in_features; i += kThreads) {
+        maximum = fmaxf(maximum, fabsf(bf2f(row[i])));
+    }
+    partial[threadIdx.x] = maximum;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) partial[threadIdx.x] = fmaxf(partial[threadIdx.x], partial[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const float scale = partial[0] > 0.0f ? partial[0] / 127.0f : 1.0f;
+    const float inverse = 1.0f / scale;
+    if (threadIdx.x == 0) scales[blockIdx.x] = scale;
+    int8_t* out = quantized + offset;
+    for (int i = threadIdx.x; i < in_features; i += kThreads) {
+        const float clamped = fminf(fmaxf(bf2f(row[i]) * inverse, -127.0f), 127.0f);
+        out[i] = static_cast<int8_t>(__float2int_rn(clamped));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch
+// ---------------------------------------------------------------------------
+int device_cu_count() {
+    static int count = [] {
+        int device = 0;
+        hipDeviceProp_t props{};
+        if (hipGetDevice(&device) != hipSuccess || hipGetDeviceProperties(&props, device) != hipSuccess) {
+            return 256;
+        }
+        return props.multiProcessorCount > 0 ? props.multiProcessorCount : 256;
+    }();
+    return count;
+}
+
+template <int kEpi, bool kNorm>
+hipError_t dispatch_fixed(const GemvArgs& a, int vpl, int grid, hipStream_t s) {
+    switch (vpl) {
+        case 2: gemv_exact_fixed<2, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 4: gemv_exact_fixed<4, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 6: gemv_exact_fixed<6, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 12: gemv_exact_fixed<12, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int kEpi, bool kNorm>
+hipError_t dispatch_generic(const GemvArgs& a, int grid, hipStream_t s) {
+    switch (a.rows) {
+        case 1: gemv_exact_generic<1, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 2: gemv_exact_generic<2, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 3: gemv_exact_generic<3, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 4: gemv_exact_generic<4, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 5: gemv_exact_generic<5, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 6: gemv_exact_generic<6, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 7: gemv_exact_generic<7, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 8: gemv_exact_generic<8, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int kEpi, bool kNorm>
+hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    const bool mfma = a.mode == kModeMfma || (a.mode == kModeAuto && a.rows >= 2);
+    if (mfma) {
+        if (a.in_features % 256 != 0 || (kNorm && a.in_features > 6144)) {
+            return hipErrorInvalidValue;
+        }
+        const int grid = (a.out_features + 15) / 16;
+        gemv_mfma<kEpi, kNorm><<<grid, kThreads, 0, s>>>(a);
+        return hipGetLastError();
+    }
+    const int units = kSilu ? a.out_features : (a.out_features + 1) / 2;
+    if (a.rows == 1 && a.in_features % 512 == 0) {
+        const int vpl = a.in_features / 512;
+        if (vpl == 2 || vpl == 4 || vpl == 6 || vpl == 12) {
+            const int grid = (units + kHalfWaves - 1) / kHalfWaves;
+            return dispatch_fixed<kEpi, kNorm>(a, vpl, grid, s);
+        }
+    }
+    const int generic_units = a.out_features;
+    int grid = (generic_units + kHalfWaves - 1) / kHalfWaves;
+    const int cap = device_cu_count() * 16;
+    if (grid > cap) grid = cap;
+    return dispatch_generic<kEpi, kNorm>(a, grid, s);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_int8_gemv(const GemvArgs& a, hipStream_t stream) {
+    if (a.weight == nullptr || a.scales == nullptr || a.input == nullptr) return hipErrorInvalidValue;
+    if (a.in_features <= 0 || a.in_features % 16 != 0 || a.out_features <= 0) return hipErrorInvalidValue;
+    if (a.rows < 1 || a.rows > 8) return hipErrorInvalidValue;
+    if (!aligned16(a.weight) || !aligned16(a.input)) return hipErrorInvalidValue;
+    if (a.norm_weight != nullptr && !aligned16(a.norm_weight)) return hipErrorInvalidValue;
+    if (a.epilogue != kEpiStore && a.out16 == nullptr) return hipErrorInvalidValue;
+    if (a.epilogue == kEpiStore && a.out16 == nullptr && a.out32 == nullptr) return hipErrorInvalidValue;
+    if (a.epilogue >= kEpiBias && a.bias == nullptr) return hipErrorInvalidValue;
+    if (a.input_row_index != nullptr && a.rows != 1) return hipErrorInvalidValue;
+    const bool norm = a.norm_weight != nullptr;
+    switch (a.epilogue) {
+        case kEpiStore: return norm ? dispatch<kEpiStore, true>(a, stream) : dispatch<kEpiStore, false>(a, stream);
+        case kEpiAddFma: return norm ? dispatch<kEpiAddFma, true>(a, stream) : dispatch<kEpiAddFma, false>(a, stream);
+        case kEpiAddRounded: return norm ? dispatch<kEpiAddRounded, true>(a, stream) : dispatch<kEpiAddRounded, false>(a, stream);
+        case kEpiSiluFused: return norm ? dispatch<kEpiSiluFused, true>(a, stream) : dispatch<kEpiSiluFused, false>(a, stream);
+        case kEpiSiluRounded: return norm ? dispatch<kEpiSiluRounded, true>(a, stream) : dispatch<kEpiSiluRounded, false>(a, stream);
+        case kEpiBias: return norm ? dispatch<kEpiBias, true>(a, stream) : dispatch<kEpiBias, false>(a, stream);
+        case kEpiBiasSilu: return norm ? dispatch<kEpiBiasSilu, true>(a, stream) : dispatch<kEpiBiasSilu, false>(a, stream);
+        case kEpiBiasAdd: return norm ? dispatch<kEpiBiasAdd, true>(a, stream) : dispatch<kEpiBiasAdd, false>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,
+                                       int in_features, int out_features, hipStream_t stream) {
+    if (in_features % 16 != 0 || in_features <= 0 || out_features <= 0) return hipErrorInvalidValue;
+    quantize_rows_kernel<<<out_features, kThreads, 0, stream>>>(weight, quantized, scales, in_features);
+    return hipGetLastError();
+}
+
+namespace {
+hipError_t reference_style(const int8_t* w, const float* s, const bf16_t* x, bf16_t* y, int in,
+                           int out, int rows, int epi, hipStream_t stream) {
+    if (in % 16 != 0 || rows < 1 || rows > 8) return hipErrorInvalidValue;
+    GemvArgs a;
+    a.weight = w;
+    a.scales = s;
+    a.input = x;
+    a.out16 = y;
+    a.in_features = in;
+    a.out_features = out;
+    a.rows = rows;
+    a.epilogue = epi;
+    a.mode = kModeExact;
+    return launch_int8_gemv(a, stream);
+}
+}  // namespace
+
+hipError_t launch_int8_gemm_rows(const int8_t* w, const float* s, const bf16_t* x, bf16_t* y,
+                                 int in, int out, int rows, hipStream_t stream) {
+    return reference_style(w, s, x, y, in, out, rows, kEpiStore, stream);
+}
+
+hipError_t launch_int8_gemm_rows_add(const int8_t* w, const float* s, const bf16_t* x, bf16_t* y,
+                                     int in, int out, int rows, hipStream_t stream) {
+    return reference_style(w, s, x, y, in, out, rows, kEpiAddFma, stream);
+}
+
+hipError_t launch_int8_gate_up_silu_rows(const int8_t* w, const float* s, const bf16_t* x,
+                                         bf16_t* y, int in, int out, int rows, hipStream_t stream) {
+    return reference_style(w, s, x, y, in, out, rows, kEpiSiluFused, stream);
+}
+
+}  // namespace q3

@@ -1,0 +1,503 @@
+// Decode-step transformer primitives around the int8 GEMVs, gfx950.
+//
+// Arithmetic follows native/qwen3-tts-native/native/src/talker_kernels.cu
+// (cited per kernel) with its operation order reproduced exactly, so results
+// are bit-identical to the CPU restatement; the layouts and launch shapes are
+// this build's own (wave64 reductions, one wave per head, device-resident
+// positions so a frame can be replayed as a hipGraph).
+#include "q3_common.hpp"
+#include "q3_math.h"
+
+namespace q3 {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Exact emulation of the reference's 256-thread block_sum tree
+// (talker_kernels.cu:14-25) by one wave64: `part[j]` is virtual thread
+// lane + 64*j.  Result is broadcast to every lane.
+__device__ __forceinline__ float wave_tree256(float p0, float p1, float p2, float p3) {
+    p0 += p2;
+    p1 += p3;
+    float value = p0 + p1;
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        value += __shfl_down(value, offset, 64);
+    }
+    return __shfl(value, 0, 64);
+}
+
+// rms_norm_kernel (talker_kernels.cu:27-48), one wave64 per row.
+__global__ __launch_bounds__(64) void rms_norm_rows_kernel(const bf16_t* input, const bf16_t* weight,
+                                                           bf16_t* output, int width, float epsilon) {
+    const bf16_t* in = input + static_cast<size_t>(blockIdx.x) * width;
+    bf16_t* out = output + static_cast<size_t>(blockIdx.x) * width;
+    const int lane = threadIdx.x;
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.0f;
+        for (int i = lane + 64 * j; i < width; i += 256) {
+            const float v = bf2f(in[i]);
+            s = fmaf(v, v, s);
+        }
+        part[j] = s;
+    }
+    const float total = wave_tree256(part[0], part[1], part[2], part[3]);
+    const float inverse = 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
+    for (int i = lane; i < width; i += 64) {
+        const float normalized = round_bf(bf2f(in[i]) * inverse);
+        out[i] = f2bf(normalized * bf2f(weight[i]));
+    }
+}
+
+// Fused QKV epilogue, one wave64 per head:
+//   q/k heads: head RMSNorm (talker_kernels.cu:50-70) then rotate-half RoPE
+//   (talker_kernels.cu:72-114) with cos/sin read from a bf16 table built on
+//   the host with the same float formula; k heads are then appended to the
+//   cache, v heads are copied to the cache (the reference's two D2D copies,
+//   talker.cu:3343-3364).  Supports head_dimension == 128.
+// rope_table: [max_positions][head_dim/2][2] bf16 (cos, sin).
+__global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
+    bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, bf16_t* const* key_bases,
+    bf16_t* const* value_bases, const int* positions, const bf16_t* rope_table, int query_heads,
+    int key_value_heads, float epsilon) {
+    constexpr int kDim = 128;
+    constexpr int kHalf = 64;
+    const int heads = query_heads + 2 * key_value_heads;
+    const int row = blockIdx.x / heads;
+    const int head = blockIdx.x % heads;
+    const int lane = threadIdx.x;
+    const int q_width = query_heads * kDim;
+    const int kv_width = key_value_heads * kDim;
+    bf16_t* base = qkv + static_cast<size_t>(row) * (q_width + 2 * kv_width) +
+                   static_cast<size_t>(head) * kDim;
+    const int position = positions[row];
+    if (head >= query_heads + key_value_heads) {
+        const int vh = head - query_heads - key_value_heads;
+        bf16_t* dst = value_bases[row] + static_cast<size_t>(position) * kv_width +
+                      static_cast<size_t>(vh) * kDim;
+        dst[lane] = base[lane];
+        dst[lane + kHalf] = base[lane + kHalf];
+        return;
+    }
+    const bool is_query = head < query_heads;
+    const bf16_t* gain = is_query ? q_norm : k_norm;
+    const float x0 = bf2f(base[lane]);
+    const float x1 = bf2f(base[lane + kHalf]);
+    // 256-thread tree over 128 squares; virtual threads 128..255 hold 0.
+    const float total = wave_tree256(fmaf(x0, x0, 0.0f), fmaf(x1, x1, 0.0f), 0.0f, 0.0f);
+    const float inverse = 1.0f / sqrtf(total / static_cast<float>(kDim) + epsilon);
+    const float first = round_bf(round_bf(x0 * inverse) * bf2f(gain[lane]));
+    const float second = round_bf(round_bf(x1 * inverse) * bf2f(gain[lane + kHalf]));
+    const bf16_t* cs = rope_table + (static_cast<size_t>(position) * kHalf + lane) * 2;
+    const float c = bf2f(cs[0]);
+    const float s = bf2f(cs[1]);
+    const float fc = round_bf(first * c);
+    const float ss = round_bf(second * s);
+    const float sc = round_bf(second * c);
+    const float fs = round_bf(first * s);
+    const bf16_t out0 = f2bf(fc - ss);
+    const bf16_t out1 = f2bf(sc + fs);
+    if (is_query) {
+        base[lane] = out0;
+        base[lane + kHalf] = out1;
+    } else {
+        const int kh = head - query_heads;
+        bf16_t* dst = key_bases[row] + static_cast<size_t>(position) * kv_width +
+                      static_cast<size_t>(kh) * kDim;
+        dst[lane] = out0;
+        dst[lane + kHalf] = out1;
+    }
+}
+
+// Head RMSNorm alone (talker_kernels.cu:50-70), one wave per head, d = 128.
+__global__ __launch_bounds__(64) void head_rms_norm_kernel(bf16_t* values, const bf16_t* weight,
+                                                           float epsilon) {
+    bf16_t* head = values + static_cast<size_t>(blockIdx.x) * 128;
+    const int lane = threadIdx.x;
+    const float x0 = bf2f(head[lane]);
+    const float x1 = bf2f(head[lane + 64]);
+    const float total = wave_tree256(fmaf(x0, x0, 0.0f), fmaf(x1, x1, 0.0f), 0.0f, 0.0f);
+    const float inverse = 1.0f / sqrtf(total / 128.0f + epsilon);
+    head[lane] = f2bf(round_bf(x0 * inverse) * bf2f(weight[lane]));
+    head[lane + 64] = f2bf(round_bf(x1 * inverse) * bf2f(weight[lane + 64]));
+}
+
+// RoPE alone (talker_kernels.cu:72-114) with the reference's in-kernel
+// powf/cosf/sinf angle.  Used only by the primitive self-test export; the
+// decode path uses the host-built table above.
+__global__ void rope_kernel(bf16_t* values, int rows, int heads, int head_dimension,
+                            const int* positions, int first_position, float theta) {
+    const int half = head_dimension / 2;
+    const int pair = blockIdx.x * blockDim.x + threadIdx.x;
+    const int row_pairs = heads * half;
+    if (pair >= rows * row_pairs) return;
+    const int row = pair / row_pairs;
+    const int head = (pair % row_pairs) / half;
+    const int d = pair % half;
+    const int position = positions ? positions[row] : first_position + row;
+    bf16_t* base = values + (static_cast<size_t>(row) * heads + head) * head_dimension;
+    const float exponent = static_cast<float>(2 * d) / static_cast<float>(head_dimension);
+    const float angle = static_cast<float>(position) * powf(theta, -exponent);
+    const float c = round_bf(cosf(angle));
+    const float s = round_bf(sinf(angle));
+    const float first = bf2f(base[d]);
+    const float second = bf2f(base[d + half]);
+    const float fc = round_bf(first * c);
+    const float ss = round_bf(second * s);
+    const float sc = round_bf(second * c);
+    const float fs = round_bf(first * s);
+    base[d] = f2bf(fc - ss);
+    base[d + half] = f2bf(sc + fs);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention, one 256-thread block per (row, query head), d = 128.
+//
+// kExact reproduces causal_gqa_attention_kernel (talker_kernels.cu:287-357):
+//   dot = 256-thread tree of the 128 exact products, rounded to bf16;
+//   score = bf16(dot * scale); softmax sequential in fp32 with bf16 probs;
+//   out[d] = bf16(sequential fmaf over positions).
+// !kExact reproduces batch_causal_gqa_attention_fast_kernel (:506-595):
+//   fp32 scores from a sequential fmaf over d; 256-thread max and sum trees
+//   over per-thread strided partials; out[d] = bf16(chain * (1/sum)).
+// Scores, each computed by one lane over a whole key row (no per-position
+// block barrier), live in LDS.  The sequential chains are the reference's
+// own order and are kept.
+// ---------------------------------------------------------------------------
+template <bool kExact>
+__global__ __launch_bounds__(kThreads) void attention_kernel(
+    const bf16_t* query, int query_stride, bf16_t* const* key_bases, bf16_t* const* value_bases,
+    const bf16_t* key_cache, const bf16_t* value_cache, const int* positions,
+    int fixed_sequence_length, bf16_t* output, int query_heads, int key_value_heads,
+    float scale) {
+    constexpr int kDim = 128;
+    extern __shared__ float scores[];
+    __shared__ float q_shared[kDim];
+    __shared__ float reduction[kThreads];
+    __shared__ float broadcast[2];
+    const int row = blockIdx.x / query_heads;
+    const int qh = blockIdx.x % query_heads;
+    const int kvh = qh / (query_heads / key_value_heads);
+    const int tid = threadIdx.x;
+    const int length = positions ? positions[row] + 1 : fixed_sequence_length;
+    const bf16_t* keys = key_bases ? key_bases[row] : key_cache;
+    const bf16_t* values = value_bases ? value_bases[row] : value_cache;
+    const int kv_width = key_value_heads * kDim;
+    const bf16_t* q = query + static_cast<size_t>(row) * query_stride + static_cast<size_t>(qh) * kDim;
+    if (tid < kDim) q_shared[tid] = bf2f(q[tid]);
+    __syncthreads();
+
+    float local_max = -INFINITY;
+    for (int p = tid; p < length; p += kThreads) {
+        const uint4* k4 = reinterpret_cast<const uint4*>(keys + static_cast<size_t>(p) * kv_width +
+                                                         static_cast<size_t>(kvh) * kDim);
+        float score;
+        if constexpr (kExact) {
+            // s[t] = (q[t]k[t] + 0) + (q[t+64]k[t+64] + 0), t < 64; then halves.
+            float s[64];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                const uint4 lo = k4[v];
+                const uint4 hi = k4[v + 8];
+                const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
+                const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        const int t = 8 * v + 2 * i + b;
+                        const float kl = b ? __uint_as_float(lw[i] & 0xffff0000u) : __uint_as_float(lw[i] << 16);
+                        const float kh = b ? __uint_as_float(hw[i] & 0xffff0000u) : __uint_as_float(hw[i] << 16);
+                        const float a = fmaf(q_shared[t], kl, 0.0f) + 0.0f;
+                        const float c = fmaf(q_shared[t + 64], kh, 0.0f) + 0.0f;
+                        s[t] = a + c;
+                    }
+                }
+            }
+#pragma unroll
+            for (int w = 32; w > 0; w >>= 1) {
+#pragma unroll
+                for (int t = 0; t < w; ++t) s[t] += s[t + w];
+            }
+            score = round_bf(round_bf(s[0]) * scale);
+        } else {
+            float dot = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint4 w4 = k4[v];
+                const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    dot = fmaf(q_shared[8 * v + 2 * i], __uint_as_float(w[i] << 16), dot);
+                    dot = fmaf(q_shared[8 * v + 2 * i + 1], __uint_as_float(w[i] & 0xffff0000u), dot);
+                }
+            }
+            score = dot * scale;
+        }
+        scores[p] = score;
+        local_max = fmaxf(local_max, score);
+    }
+    // Maximum (order independent).
+    reduction[tid] = local_max;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (tid < s) reduction[tid] = fmaxf(reduction[tid], reduction[tid + s]);
+        __syncthreads();
+    }
+    const float maximum = reduction[0];
+    __syncthreads();
+    float inverse;
+    if constexpr (kExact) {
+        for (int p = tid; p < length; p += kThreads) scores[p] = q3_expf(scores[p] - maximum);
+        __syncthreads();
+        if (tid == 0) {
+            float denominator = 0.0f;
+            for (int p = 0; p < length; ++p) denominator += scores[p];
+            broadcast[0] = 1.0f / denominator;
+        }
+        __syncthreads();
+        inverse = broadcast[0];
+        for (int p = tid; p < length; p += kThreads) scores[p] = round_bf(scores[p] * inverse);
+        __syncthreads();
+    } else {
+        float local_sum = 0.0f;
+        for (int p = tid; p < length; p += kThreads) {
+            const float w = q3_expf(scores[p] - maximum);
+            scores[p] = w;
+            local_sum += w;
+        }
+        reduction[tid] = local_sum;
+        __syncthreads();
+        for (int s = kThreads / 2; s > 0; s >>= 1) {
+            if (tid < s) reduction[tid] += reduction[tid + s];
+            __syncthreads();
+        }
+        inverse = 1.0f / reduction[0];
+        __syncthreads();
+    }
+    if (tid < kDim) {
+        const bf16_t* vcol = values + static_cast<size_t>(kvh) * kDim + tid;
+        float acc = 0.0f;
+        int p = 0;
+        for (; p + 8 <= length; p += 8) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vv[u] = bf2f(vcol[static_cast<size_t>(p + u) * kv_width]);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fmaf(scores[p + u], vv[u], acc);
+        }
+        for (; p < length; ++p) acc = fmaf(scores[p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
+        bf16_t* out = output + (static_cast<size_t>(row) * query_heads + qh) * kDim;
+        out[tid] = kExact ? f2bf(acc) : f2bf(acc * inverse);
+    }
+}
+
+__global__ void kv_scatter_rows_kernel(const bf16_t* rows_data, bf16_t* const* cache_bases,
+                                       const int* positions, int rows, int width, int row_stride) {
+    const int index = blockIdx.x * blockDim.x + threadIdx.x;
+    if (index >= rows * width) return;
+    const int row = index / width;
+    const int column = index % width;
+    cache_bases[row][static_cast<size_t>(positions[row]) * width + column] =
+        rows_data[static_cast<size_t>(row) * row_stride + column];
+}
+
+__global__ void add_in_place_kernel(bf16_t* destination, const bf16_t* source, int width) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < width) destination[i] = f2bf(bf2f(destination[i]) + bf2f(source[i]));
+}
+
+__global__ void bias_activation_rows_kernel(bf16_t* values, const bf16_t* bias, int total,
+                                            int width, bool silu) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    float value = bf2f(values[i]) + bf2f(bias[i % width]);
+    if (silu) value *= 1.0f / (1.0f + q3_expf(-value));
+    values[i] = f2bf(value);
+}
+
+__global__ void silu_gate_kernel(bf16_t* gate, const bf16_t* up, int width) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= width) return;
+    const float g = bf2f(gate[i]);
+    const float activated = round_bf(g / (1.0f + q3_expf(-g)));
+    gate[i] = f2bf(activated * bf2f(up[i]));
+}
+
+__global__ void fill_zero_kernel(bf16_t* values, int width) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < width) values[i] = 0;
+}
+
+__global__ void increment_kernel(int* counter) {
+    if (threadIdx.x == 0) *counter += 1;
+}
+
+// Deterministic N(mean, stddev) bf16 fill: Box-Muller on two 24-bit uniforms
+// taken from a splitmix64 hash of (seed, index).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_kernel(bf16_t* out, uint64_t count, uint64_t seed, float mean,
+                                   float stddev) {
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < count;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t h = splitmix64(seed * 0x100000001b3ULL + i);
+        const float u1 = (static_cast<float>(h >> 40) + 1.0f) * (1.0f / 16777217.0f);
+        const float u2 = static_cast<float>((h >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+        const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+        out[i] = f2bf(mean + stddev * z);
+    }
+}
+
+int blocks_for(int n) { return (n + kThreads - 1) / kThreads; }
+
+}  // namespace
+
+hipError_t launch_increment(int* counter, hipStream_t stream) {
+    increment_kernel<<<1, 64, 0, stream>>>(counter);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_bf16_normal(bf16_t* destination, uint64_t count, uint64_t seed, float mean,
+                                   float stddev, hipStream_t stream) {
+    if (count == 0) return hipSuccess;
+    uint64_t blocks = (count + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    fill_normal_kernel<<<static_cast<int>(blocks), kThreads, 0, stream>>>(destination, count, seed,
+                                                                          mean, stddev);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_rows(const bf16_t* input, const bf16_t* weight, bf16_t* output, int rows,
+                                int width, float epsilon, hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    rms_norm_rows_kernel<<<rows, 64, 0, stream>>>(input, weight, output, width, epsilon);
+    return hipGetLastError();
+}
+
+hipError_t launch_head_rms_norm_rows(bf16_t* values, const bf16_t* weight, int rows, int heads,
+                                     int head_dimension, float epsilon, hipStream_t stream) {
+    if (head_dimension != 128 || rows <= 0 || heads <= 0) return hipErrorInvalidValue;
+    head_rms_norm_kernel<<<rows * heads, 64, 0, stream>>>(values, weight, epsilon);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows(bf16_t* values, int rows, int heads, int head_dimension,
+                            int first_position, float theta, hipStream_t stream) {
+    if (head_dimension % 2 != 0 || rows <= 0) return hipErrorInvalidValue;
+    const int pairs = rows * heads * head_dimension / 2;
+    rope_kernel<<<blocks_for(pairs), kThreads, 0, stream>>>(values, rows, heads, head_dimension,
+                                                            nullptr, first_position, theta);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows_at(bf16_t* values, int rows, int heads, int head_dimension,
+                               const int* positions, float theta, hipStream_t stream) {
+    if (head_dimension % 2 != 0 || rows <= 0) return hipErrorInvalidValue;
+    const int pairs = rows * heads * head_dimension / 2;
+    rope_kernel<<<blocks_for(pairs), kThreads, 0, stream>>>(values, rows, heads, head_dimension,
+                                                            positions, 0, theta);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm,
+                                         bf16_t* const* key_bases, bf16_t* const* value_bases,
+                                         const int* positions, const bf16_t* rope_table, int rows,
+                                         int query_heads, int key_value_heads, int head_dimension,
+                                         float epsilon, hipStream_t stream) {
+    if (head_dimension != 128 || rows <= 0 || key_value_heads <= 0) return hipErrorInvalidValue;
+    const int heads = query_heads + 2 * key_value_heads;
+    qk_norm_rope_kv_kernel<<<rows * heads, 64, 0, stream>>>(qkv, q_norm, k_norm, key_bases,
+                                                            value_bases, positions, rope_table,
+                                                            query_heads, key_value_heads, epsilon);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
+                            bf16_t* const* key_bases, bf16_t* const* value_bases,
+                            const bf16_t* key_cache, const bf16_t* value_cache,
+                            const int* positions, int fixed_sequence_length, bf16_t* output,
+                            int rows, int query_heads, int key_value_heads, int head_dimension,
+                            int max_sequence_length, hipStream_t stream) {
+    if (head_dimension != 128 || query_heads % key_value_heads != 0 || rows <= 0 ||
+        max_sequence_length <= 0 || max_sequence_length > 16384) {
+        return hipErrorInvalidValue;
+    }
+    const float scale = 1.0f / sqrtf(static_cast<float>(head_dimension));
+    const size_t shared = static_cast<size_t>(max_sequence_length) * sizeof(float);
+    if (exact) {
+        attention_kernel<true><<<rows * query_heads, kThreads, shared, stream>>>(
+            query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
+            fixed_sequence_length, output, query_heads, key_value_heads, scale);
+    } else {
+        attention_kernel<false><<<rows * query_heads, kThreads, shared, stream>>>(
+            query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
+            fixed_sequence_length, output, query_heads, key_value_heads, scale);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_causal_gqa_attention(const bf16_t* query, const bf16_t* key_cache,
+                                       const bf16_t* value_cache, bf16_t* output, int query_heads,
+                                       int key_value_heads, int head_dimension,
+                                       int sequence_length, int query_stride, hipStream_t stream) {
+    return launch_attention(true, query, query_stride, nullptr, nullptr, key_cache, value_cache,
+                            nullptr, sequence_length, output, 1, query_heads, key_value_heads,
+                            head_dimension, sequence_length, stream);
+}
+
+hipError_t launch_batch_causal_gqa_attention_fast(const bf16_t* query, bf16_t* const* key_bases,
+                                                  bf16_t* const* value_bases, const int* positions,
+                                                  bf16_t* output, int rows, int query_heads,
+                                                  int key_value_heads, int head_dimension,
+                                                  int max_sequence_length, int query_stride,
+                                                  hipStream_t stream) {
+    return launch_attention(false, query, query_stride, key_bases, value_bases, nullptr, nullptr,
+                            positions, 0, output, rows, query_heads, key_value_heads,
+                            head_dimension, max_sequence_length, stream);
+}
+
+hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,
+                                  const int* positions, int rows, int width, int row_stride,
+                                  hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    kv_scatter_rows_kernel<<<blocks_for(rows * width), kThreads, 0, stream>>>(
+        rows_data, cache_bases, positions, rows, width, row_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_in_place(bf16_t* destination, const bf16_t* source, int width,
+                               hipStream_t stream) {
+    if (width <= 0) return hipErrorInvalidValue;
+    add_in_place_kernel<<<blocks_for(width), kThreads, 0, stream>>>(destination, source, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_activation_rows(bf16_t* values, const bf16_t* bias, int rows, int width,
+                                       bool silu, hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    bias_activation_rows_kernel<<<blocks_for(rows * width), kThreads, 0, stream>>>(
+        values, bias, rows * width, width, silu);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_gate(bf16_t* gate, const bf16_t* up, int width, hipStream_t stream) {
+    if (width <= 0) return hipErrorInvalidValue;
+    silu_gate_kernel<<<blocks_for(width), kThreads, 0, stream>>>(gate, up, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(bf16_t* values, int width, hipStream_t stream) {
+    if (width <= 0) return hipErrorInvalidValue;
+    fill_zero_kernel<<<blocks_for(width), kThreads, 0, stream>>>(values, width);
+    return hipGetLastError();
+}
+
+}  // namespace q3

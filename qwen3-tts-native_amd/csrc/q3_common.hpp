@@ -1,0 +1,202 @@
+// Shared definitions of the MI355X (gfx950) int8 decode-path library.
+//
+// bf16 values are carried as raw uint16_t bit patterns everywhere (device and
+// host) so that no vendor bf16 type with its own rounding rules sits on the
+// hot path.  All conversions round to nearest even, like the reference's
+// __float2bfloat16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace q3 {
+
+using bf16_t = uint16_t;
+
+// ---------------------------------------------------------------------------
+// bf16 conversions
+// ---------------------------------------------------------------------------
+__host__ __device__ inline float bf2f(bf16_t v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+#else
+    uint32_t u = static_cast<uint32_t>(v) << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+#endif
+}
+
+__host__ __device__ inline bf16_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t u = __float_as_uint(f);
+#else
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+#endif
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return 0x7fff;
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<bf16_t>(u >> 16);
+}
+
+__host__ __device__ inline float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// ---------------------------------------------------------------------------
+// Errors: internal code throws; the C ABI maps exceptions to status codes.
+// ---------------------------------------------------------------------------
+class DeviceFailure final : public std::runtime_error {
+public:
+    using std::runtime_error::runtime_error;
+};
+
+inline void check_hip(hipError_t status, const char* operation) {
+    if (status != hipSuccess) {
+        throw DeviceFailure(std::string(operation) + " failed: " + hipGetErrorString(status));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel launch layer.  Names, argument meaning and the hipErrorInvalidValue
+// rule mirror the reference's internal launch API
+// (native/qwen3-tts-native/native/src/talker_internal.cuh:11-356).
+// ---------------------------------------------------------------------------
+
+// Epilogue applied by the int8 GEMV family to y = scale[c] * dot(W[c], x).
+enum GemvEpilogue : int {
+    kEpiStore = 0,        // out16 = bf16(y); out32 = y                (int8_gemv.cu:123)
+    kEpiAddFma = 1,       // out16 = bf16(fma(dot, scale, out16))      (int8_gemv.cu:192-196)
+    kEpiAddRounded = 2,   // out16 = bf16(out16 + bf16(y))   GEMV + add_in_place (talker.cu:3391-3405)
+    kEpiSiluFused = 3,    // out16 = bf16(silu(yg) * yu)               (int8_gemv.cu:283-289)
+    kEpiSiluRounded = 4,  // gate/up bf16, silu_gate kernel            (talker.cu:3416-3442)
+    kEpiBias = 5,         // out16 = bf16(bf16(y) + bias)   GEMV + bias_activation (talker.cu:3498-3515)
+    kEpiBiasSilu = 6,     // v = bf16(y) + bias; out16 = bf16(v * (1/(1+exp(-v))))  (talker.cu:2683-2696)
+    kEpiBiasAdd = 7,      // out16 = bf16(out16 + bf16(bf16(y) + bias))  fc2 + bias + add (talker.cu:2697-2719,3572-3580)
+};
+
+// Weight-streaming implementation used for a GEMV launch.
+enum GemvMode : int {
+    kModeAuto = 0,   // exact order for rows == 1, MFMA for rows >= 2
+    kModeExact = 1,  // reference lane order on VALU (bit-exact to the reference)
+    kModeMfma = 2,   // int8 -> bf16 dequant in registers + v_mfma_f32_16x16x32_bf16
+};
+
+struct GemvArgs {
+    const int8_t* weight = nullptr;   // [out_rows][in] row-major (gate/up: [2*out][in])
+    const float* scales = nullptr;    // [out_rows]
+    const bf16_t* input = nullptr;    // [rows][in]
+    const bf16_t* norm_weight = nullptr;  // optional fused RMSNorm gain [in]
+    const bf16_t* bias = nullptr;         // [out] for the bias epilogues
+    const int* input_row_index = nullptr; // optional: input += (*index) * in (rows == 1)
+    float norm_epsilon = 1.0e-6f;
+    bf16_t* out16 = nullptr;          // [rows][out] (nullable for kEpiStore)
+    float* out32 = nullptr;           // [rows][out] (kEpiStore only, nullable)
+    int in_features = 0;
+    int out_features = 0;             // channels written (gate/up: intermediate)
+    int rows = 1;
+    int epilogue = kEpiStore;
+    int mode = kModeAuto;
+};
+
+hipError_t launch_int8_gemv(const GemvArgs& args, hipStream_t stream);
+
+hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,
+                                       int in_features, int out_features, hipStream_t stream);
+hipError_t launch_int8_gemm_rows(const int8_t* weight, const float* scales, const bf16_t* input,
+                                 bf16_t* output, int in_features, int out_features, int rows,
+                                 hipStream_t stream);
+hipError_t launch_int8_gemm_rows_add(const int8_t* weight, const float* scales,
+                                     const bf16_t* input, bf16_t* output, int in_features,
+                                     int out_features, int rows, hipStream_t stream);
+hipError_t launch_int8_gate_up_silu_rows(const int8_t* weight, const float* scales,
+                                         const bf16_t* input, bf16_t* output, int in_features,
+                                         int out_features, int rows, hipStream_t stream);
+
+// Transformer primitives (talker_kernels.cu equivalents).
+hipError_t launch_rms_norm_rows(const bf16_t* input, const bf16_t* weight, bf16_t* output,
+                                int rows, int width, float epsilon, hipStream_t stream);
+hipError_t launch_head_rms_norm_rows(bf16_t* values, const bf16_t* weight, int rows, int heads,
+                                     int head_dimension, float epsilon, hipStream_t stream);
+hipError_t launch_rope_rows(bf16_t* values, int rows, int heads, int head_dimension,
+                            int first_position, float theta, hipStream_t stream);
+hipError_t launch_rope_rows_at(bf16_t* values, int rows, int heads, int head_dimension,
+                               const int* positions, float theta, hipStream_t stream);
+// Fused per-head epilogue of the QKV projection: head RMSNorm on q and k,
+// RoPE at `position`, and the KV-cache append of k and v.  qkv is
+// [rows][q_width + 2*kv_width]; q is rewritten in place; k/v rows go to
+// key_bases[r] / value_bases[r] + positions[r] * kv_width.
+hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm,
+                                         bf16_t* const* key_bases, bf16_t* const* value_bases,
+                                         const int* positions, const bf16_t* rope_table, int rows,
+                                         int query_heads, int key_value_heads, int head_dimension,
+                                         float epsilon, hipStream_t stream);
+// Decode attention.  exact: causal_gqa_attention semantics (talker_kernels.cu:287-357);
+// otherwise batch_causal_gqa_attention_fast semantics (:506-595).  Keys/values come
+// from key_bases[row] (or key_cache when key_bases is null); the length is
+// positions[row] + 1 (or fixed_sequence_length when positions is null).
+hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
+                            bf16_t* const* key_bases, bf16_t* const* value_bases,
+                            const bf16_t* key_cache, const bf16_t* value_cache,
+                            const int* positions, int fixed_sequence_length, bf16_t* output,
+                            int rows, int query_heads, int key_value_heads, int head_dimension,
+                            int max_sequence_length, hipStream_t stream);
+hipError_t launch_causal_gqa_attention(const bf16_t* query, const bf16_t* key_cache,
+                                       const bf16_t* value_cache, bf16_t* output, int query_heads,
+                                       int key_value_heads, int head_dimension,
+                                       int sequence_length, int query_stride, hipStream_t stream);
+hipError_t launch_batch_causal_gqa_attention_fast(const bf16_t* query,
+                                                  bf16_t* const* key_bases,
+                                                  bf16_t* const* value_bases,
+                                                  const int* positions, bf16_t* output, int rows,
+                                                  int query_heads, int key_value_heads,
+                                                  int head_dimension, int max_sequence_length,
+                                                  int query_stride, hipStream_t stream);
+hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,
+                                  const int* positions, int rows, int width, int row_stride,
+                                  hipStream_t stream);
+hipError_t launch_add_in_place(bf16_t* destination, const bf16_t* source, int width,
+                               hipStream_t stream);
+hipError_t launch_bias_activation_rows(bf16_t* values, const bf16_t* bias, int rows, int width,
+                                       bool silu, hipStream_t stream);
+hipError_t launch_silu_gate(bf16_t* gate, const bf16_t* up, int width, hipStream_t stream);
+hipError_t launch_fill_zero(bf16_t* values, int width, hipStream_t stream);
+hipError_t launch_increment(int* counter, hipStream_t stream);
+hipError_t launch_fill_bf16_normal(bf16_t* destination, uint64_t count, uint64_t seed, float mean,
+                                   float stddev, hipStream_t stream);
+
+// Sampling / frame glue (sampling_kernels.cu equivalents).
+hipError_t launch_sample_logits(const bf16_t* logits, int vocabulary,
+                                bool suppress_talker_reserved, int codec_eos_token,
+                                const int* semantic_history, const int* semantic_history_count,
+                                int semantic_history_count_fallback, int do_sample, int top_k,
+                                float top_p, float temperature, float repetition_penalty,
+                                uint64_t* random_state, int* selected_token,
+                                int* store_tokens, const int* store_index,
+                                int store_index_fallback, hipStream_t stream);
+hipError_t launch_sample_logits_ex(const bf16_t* logits, int vocabulary, bool suppress, int eos,
+                                   const int* history, const int* history_count,
+                                   int history_count_fallback, int do_sample, int top_k,
+                                   float top_p, float temperature, float penalty,
+                                   uint64_t* random_state, int* selected, int* store_tokens,
+                                   const int* store_index, int store_index_fallback,
+                                   int* append_history, int* append_count, hipStream_t stream);
+hipError_t launch_argmax_bf16(const bf16_t* logits, int vocabulary, int* selected_token,
+                              hipStream_t stream);
+hipError_t launch_store_token(int* tokens, int index, int value, hipStream_t stream);
+hipError_t launch_pack_frame_codes(const int* tokens, uint16_t* codes, int count,
+                                   hipStream_t stream);
+hipError_t launch_gather_embedding(const bf16_t* table, int vocabulary, int width,
+                                   const int* token, bf16_t* output, bool add,
+                                   hipStream_t stream);
+// output = bf16( table0[tok[0]] + table1[tok[1]] + ... ) summed in order with
+// bf16 rounding after every addition (the reference's chained add_embedding).
+hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int vocabulary0,
+                                 int vocabulary, int width, const int* tokens, bf16_t* output,
+                                 hipStream_t stream);
+
+}  // namespace q3

@@ -1,0 +1,448 @@
+// Codec-token sampler and frame glue kernels, gfx950.
+//
+// Semantics follow native/qwen3-tts-native/native/src/sampling_kernels.cu:
+//   adjusted logits (talker reserved-token mask, repetition penalty over the
+//   semantic history, :30-51); greedy argmax with lower-index ties (:208-236);
+//   direct categorical draw (:238-265); top-k/top-p: the top `selections`
+//   tokens in the order (value desc, index asc), weights exp(double) of
+//   (v/T - max/T), sequential double sums, top-p cut and one uniform draw
+//   from xorshift64* (:53-69, :350-387).
+//
+// Design: one 1024-thread block.  The repetition penalty uses an LDS mark
+// table built from the history in one pass (O(history + vocabulary)).  The
+// k-th largest logit is found by a 4-pass 8-bit radix select over monotone
+// 32-bit keys; the survivors (ties included) are ordered by rank counting, a
+// single barrier-free pass that yields the exact total order.  The sampled
+// token can be stored straight into the frame token array and the semantic
+// history (device-resident counters), so a frame needs no host round trip.
+#include "q3_common.hpp"
+
+namespace q3 {
+namespace {
+
+constexpr int kSampleThreads = 1024;
+constexpr int kMaxVocabulary = 4096;
+constexpr int kCandidateCap = 1024;
+
+__device__ __forceinline__ bool before(float av, int ai, float bv, int bi) {
+    return (av > bv) || (av == bv && ai < bi);
+}
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ uint64_t next_random(uint64_t* state) {
+    uint64_t value = *state;
+    if (value == 0) value = 0x9e3779b97f4a7c15ULL;
+    value ^= value >> 12;
+    value ^= value << 25;
+    value ^= value >> 27;
+    *state = value;
+    return value * 0x2545f4914f6cdd1dULL;
+}
+
+__device__ float uniform_random(uint64_t* state) {
+    const uint64_t value = next_random(state);
+    return static_cast<float>(static_cast<double>(value >> 11) * (1.0 / 9007199254740992.0));
+}
+
+struct SampleArgs {
+    const bf16_t* logits;
+    int vocabulary;
+    bool suppress;
+    int eos;
+    const int* history;
+    const int* history_count;
+    int history_count_fallback;
+    int do_sample;
+    int top_k;
+    float top_p;
+    float temperature;
+    float penalty;
+    uint64_t* random_state;
+    int* selected;
+    int* store_tokens;
+    const int* store_index;
+    int store_index_fallback;
+    int* append_history;   // history array to append to (talker), nullable
+    int* append_count;     // device history counter to increment, nullable
+};
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
+    __shared__ float values[kMaxVocabulary];
+    __shared__ unsigned char marked[kMaxVocabulary];
+    __shared__ double weights[kMaxVocabulary];
+    __shared__ float cand_v[kCandidateCap];
+    __shared__ int cand_i[kCandidateCap];
+    __shared__ float sorted_v[kMaxVocabulary];
+    __shared__ int sorted_i[kMaxVocabulary];
+    __shared__ uint32_t hist[256];
+    __shared__ float red_v[kSampleThreads / 64];
+    __shared__ int red_i[kSampleThreads / 64];
+    __shared__ uint32_t s_prefix;
+    __shared__ int s_above;
+    __shared__ int s_count;
+    __shared__ int s_best;
+
+    const int tid = threadIdx.x;
+    const int V = a.vocabulary;
+    const int count = a.history_count ? *a.history_count : a.history_count_fallback;
+    const bool penalize = a.suppress && a.penalty != 1.0f;
+
+    for (int t = tid; t < V; t += kSampleThreads) marked[t] = 0;
+    __syncthreads();
+    if (penalize) {
+        for (int h = tid; h < count; h += kSampleThreads) {
+            const int token = a.history[h];
+            if (token >= 0 && token < V) marked[token] = 1;
+        }
+        __syncthreads();
+    }
+    for (int t = tid; t < V; t += kSampleThreads) {
+        float value;
+        if (a.suppress && t >= 2048 && t != a.eos) {
+            value = -INFINITY;
+        } else {
+            value = bf2f(a.logits[t]);
+            if (penalize && marked[t]) value = value < 0.0f ? value * a.penalty : value / a.penalty;
+        }
+        values[t] = value;
+    }
+    __syncthreads();
+
+    const bool direct = a.do_sample != 0 && a.top_k == 0 && a.top_p >= 1.0f;
+    const int selections = a.do_sample == 0 ? 1 : (a.top_k == 0 ? V : min(a.top_k, V));
+    int selected = 0;
+
+    if (a.do_sample == 0 || direct) {
+        // Block argmax, lower index on ties.
+        float bv = -INFINITY;
+        int bi = -1;
+        for (int t = tid; t < V; t += kSampleThreads) {
+            const float v = values[t];
+            if (bi < 0 || v > bv) {
+                bv = v;
+                bi = t;
+            }
+        }
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            const float ov = __shfl_down(bv, offset, 64);
+            const int oi = __shfl_down(bi, offset, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((tid & 63) == 0) {
+            red_v[tid >> 6] = bv;
+            red_i[tid >> 6] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float v = red_v[0];
+            int i = red_i[0];
+            for (int w = 1; w < kSampleThreads / 64; ++w) {
+                if (red_i[w] >= 0 && (i < 0 || red_v[w] > v || (red_v[w] == v && red_i[w] < i))) {
+                    v = red_v[w];
+                    i = red_i[w];
+                }
+            }
+            s_best = i;
+        }
+        __syncthreads();
+        selected = s_best;
+        if (direct) {
+            const float maximum = values[selected] / a.temperature;
+            for (int t = tid; t < V; t += kSampleThreads) {
+                weights[t] = exp(static_cast<double>(values[t] / a.temperature - maximum));
+            }
+            __syncthreads();
+            if (tid == 0) {
+                double total = 0.0;
+                for (int t = 0; t < V; ++t) total += weights[t];
+                const double target = static_cast<double>(uniform_random(a.random_state)) * total;
+                double cumulative = 0.0;
+                for (int t = 0; t < V; ++t) {
+                    cumulative += weights[t];
+                    if (cumulative >= target) {
+                        selected = t;
+                        break;
+                    }
+                }
+                s_best = selected;
+            }
+            __syncthreads();
+            selected = s_best;
+        }
+    } else {
+        // Threshold key of the selections-th largest value (radix select).
+        if (tid == 0) {
+            s_prefix = 0u;
+            s_above = 0;
+        }
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0u;
+            __syncthreads();
+            const uint32_t prefix = s_prefix;
+            const int high = shift + 8;
+            for (int t = tid; t < V; t += kSampleThreads) {
+                const uint32_t key = order_key(values[t]);
+                if (high >= 32 || (key >> high) == (prefix >> high)) {
+                    atomicAdd(&hist[(key >> shift) & 0xffu], 1u);
+                }
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cumulative = s_above;
+                int chosen = 0;
+                for (int b = 255; b >= 0; --b) {
+                    if (cumulative + static_cast<int>(hist[b]) >= selections) {
+                        chosen = b;
+                        break;
+                    }
+                    cumulative += static_cast<int>(hist[b]);
+                }
+                s_above = cumulative;
+                s_prefix = prefix | (static_cast<uint32_t>(chosen) << shift);
+            }
+            __syncthreads();
+        }
+        const uint32_t threshold = s_prefix;
+        if (tid == 0) s_count = 0;
+        __syncthreads();
+        for (int t = tid; t < V; t += kSampleThreads) {
+            if (order_key(values[t]) >= threshold) {
+                const int slot = atomicAdd(&s_count, 1);
+                if (slot < kCandidateCap) {
+                    cand_v[slot] = values[t];
+                    cand_i[slot] = t;
+                }
+            }
+        }
+        __syncthreads();
+        const int n = s_count;
+        if (n <= kCandidateCap) {
+            // Rank counting over the survivors: exact total order.
+            for (int c = tid; c < n; c += kSampleThreads) {
+                const float v = cand_v[c];
+                const int i = cand_i[c];
+                int rank = 0;
+                for (int j = 0; j < n; ++j) rank += before(cand_v[j], cand_i[j], v, i) ? 1 : 0;
+                sorted_v[rank] = v;
+                sorted_i[rank] = i;
+            }
+        } else {
+            for (int t = tid; t < V; t += kSampleThreads) {
+                const float v = values[t];
+                int rank = 0;
+                for (int j = 0; j < V; ++j) rank += before(values[j], j, v, t) ? 1 : 0;
+                sorted_v[rank] = v;
+                sorted_i[rank] = t;
+            }
+        }
+        __syncthreads();
+        const float maximum = sorted_v[0] / a.temperature;
+        for (int r = tid; r < selections; r += kSampleThreads) {
+            weights[r] = exp(static_cast<double>(sorted_v[r] / a.temperature - maximum));
+        }
+        __syncthreads();
+        if (tid == 0) {
+            double denominator = 0.0;
+            for (int r = 0; r < selections; ++r) denominator += weights[r];
+            double cumulative = 0.0;
+            int retained = selections;
+            for (int r = 0; r < selections; ++r) {
+                cumulative += weights[r] / denominator;
+                if (cumulative >= static_cast<double>(a.top_p)) {
+                    retained = r + 1;
+                    break;
+                }
+            }
+            double retained_total = 0.0;
+            for (int r = 0; r < retained; ++r) retained_total += weights[r];
+            const double target = static_cast<double>(uniform_random(a.random_state)) * retained_total;
+            cumulative = 0.0;
+            int choice = sorted_i[retained - 1];
+            for (int r = 0; r < retained; ++r) {
+                cumulative += weights[r];
+                if (cumulative >= target) {
+                    choice = sorted_i[r];
+                    break;
+                }
+            }
+            s_best = choice;
+        }
+        __syncthreads();
+        selected = s_best;
+    }
+
+    if (tid == 0) {
+        if (a.selected) *a.selected = selected;
+        if (a.store_tokens) {
+            const int index = a.store_index ? *a.store_index : a.store_index_fallback;
+            a.store_tokens[index] = selected;
+        }
+        if (a.append_history && a.append_count) {
+            const int c = *a.append_count;
+            a.append_history[c] = selected;
+            *a.append_count = c + 1;
+        }
+    }
+}
+
+// bf16_argmax_kernel (runtime.cu:43-82): strided argmax + lower-index ties.
+__global__ __launch_bounds__(256) void argmax_kernel(const bf16_t* logits, int vocabulary,
+                                                     int* selected) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int t = threadIdx.x; t < vocabulary; t += 256) {
+        const float v = bf2f(logits[t]);
+        if (bi < 0 || v > bv) {
+            bv = v;
+            bi = t;
+        }
+    }
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        const float ov = __shfl_down(bv, offset, 64);
+        const int oi = __shfl_down(bi, offset, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            if (ri[w] >= 0 && (ri[0] < 0 || rv[w] > rv[0] || (rv[w] == rv[0] && ri[w] < ri[0]))) {
+                rv[0] = rv[w];
+                ri[0] = ri[w];
+            }
+        }
+        *selected = ri[0];
+    }
+}
+
+__global__ void store_token_kernel(int* tokens, int index, int value) {
+    if (threadIdx.x == 0) tokens[index] = value;
+}
+
+__global__ void pack_codes_kernel(const int* tokens, uint16_t* codes, int count) {
+    const int i = threadIdx.x;
+    if (i < count) codes[i] = static_cast<uint16_t>(tokens[i]);
+}
+
+// gather_embedding_kernel (sampling_kernels.cu:428-452): an out-of-range
+// token leaves the output untouched.
+__global__ void gather_embedding_kernel(const bf16_t* table, int vocabulary, int width,
+                                        const int* token, bf16_t* output, bool add) {
+    const int row = *token;
+    if (row < 0 || row >= vocabulary) return;
+    const bf16_t* src = table + static_cast<size_t>(row) * width;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += blockDim.x * gridDim.x) {
+        output[i] = add ? f2bf(bf2f(output[i]) + bf2f(src[i])) : src[i];
+    }
+}
+
+// One gather followed by count-1 adds, each rounded to bf16, fused.
+__global__ void sum_embeddings_kernel(const bf16_t* const* tables, int count, int vocabulary0,
+                                      int vocabulary, int width, const int* tokens,
+                                      bf16_t* output) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= width) return;
+    const int first = tokens[0];
+    float acc = bf2f(output[i]);
+    bool have = false;
+    if (first >= 0 && first < vocabulary0) {
+        acc = bf2f(tables[0][static_cast<size_t>(first) * width + i]);
+        have = true;
+    }
+    for (int r = 1; r < count; ++r) {
+        const int tok = tokens[r];
+        if (tok < 0 || tok >= vocabulary) continue;
+        acc = round_bf(acc + bf2f(tables[r][static_cast<size_t>(tok) * width + i]));
+        have = true;
+    }
+    if (have) output[i] = f2bf(acc);
+}
+
+}  // namespace
+
+hipError_t launch_sample_logits(const bf16_t* logits, int vocabulary, bool suppress, int eos,
+                                const int* history, const int* history_count,
+                                int history_count_fallback, int do_sample, int top_k, float top_p,
+                                float temperature, float penalty, uint64_t* random_state,
+                                int* selected, int* store_tokens, const int* store_index,
+                                int store_index_fallback, hipStream_t stream) {
+    return launch_sample_logits_ex(logits, vocabulary, suppress, eos, history, history_count,
+                                   history_count_fallback, do_sample, top_k, top_p, temperature,
+                                   penalty, random_state, selected, store_tokens, store_index,
+                                   store_index_fallback, nullptr, nullptr, stream);
+}
+
+hipError_t launch_sample_logits_ex(const bf16_t* logits, int vocabulary, bool suppress, int eos,
+                                   const int* history, const int* history_count,
+                                   int history_count_fallback, int do_sample, int top_k,
+                                   float top_p, float temperature, float penalty,
+                                   uint64_t* random_state, int* selected, int* store_tokens,
+                                   const int* store_index, int store_index_fallback,
+                                   int* append_history, int* append_count, hipStream_t stream) {
+    if (vocabulary <= 0 || vocabulary > kMaxVocabulary) return hipErrorInvalidValue;
+    if (top_k < 0 || !(top_p > 0.0f) || top_p > 1.0f || !(temperature > 0.0f) || !(penalty > 0.0f)) {
+        return hipErrorInvalidValue;
+    }
+    SampleArgs a{logits, vocabulary, suppress, eos, history, history_count,
+                 history_count_fallback, do_sample, top_k, top_p, temperature, penalty,
+                 random_state, selected, store_tokens, store_index, store_index_fallback,
+                 append_history, append_count};
+    sample_kernel<<<1, kSampleThreads, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_bf16(const bf16_t* logits, int vocabulary, int* selected,
+                              hipStream_t stream) {
+    if (vocabulary <= 0) return hipErrorInvalidValue;
+    argmax_kernel<<<1, 256, 0, stream>>>(logits, vocabulary, selected);
+    return hipGetLastError();
+}
+
+hipError_t launch_store_token(int* tokens, int index, int value, hipStream_t stream) {
+    store_token_kernel<<<1, 64, 0, stream>>>(tokens, index, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_frame_codes(const int* tokens, uint16_t* codes, int count,
+                                   hipStream_t stream) {
+    if (count <= 0 || count > 64) return hipErrorInvalidValue;
+    pack_codes_kernel<<<1, 64, 0, stream>>>(tokens, codes, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_embedding(const bf16_t* table, int vocabulary, int width,
+                                   const int* token, bf16_t* output, bool add,
+                                   hipStream_t stream) {
+    if (width <= 0) return hipErrorInvalidValue;
+    gather_embedding_kernel<<<(width + 255) / 256, 256, 0, stream>>>(table, vocabulary, width,
+                                                                     token, output, add);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int vocabulary0,
+                                 int vocabulary, int width, const int* tokens, bf16_t* output,
+                                 hipStream_t stream) {
+    if (width <= 0 || count <= 0) return hipErrorInvalidValue;
+    sum_embeddings_kernel<<<(width + 255) / 256, 256, 0, stream>>>(tables, count, vocabulary0,
+                                                                   vocabulary, width, tokens,
+                                                                   output);
+    return hipGetLastError();
+}
+
+}  // namespace q3

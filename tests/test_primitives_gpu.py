@@ -1,0 +1,253 @@
+"""GPU parity of the decode-step primitives against the CPU oracle
+(native/qwen3-tts-native/native/src/talker_kernels.cu and sampling_kernels.cu
+as restated in oracle/oracle.c).  Integer/byte work and every kernel that
+reproduces the reference's operation order are compared bit-for-bit."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import gen
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(hip, a):
+    return hip.DeviceArray.from_numpy(a)
+
+
+def ptr_array(hip, pointers):
+    return dev(hip, np.array(pointers, dtype=np.uint64))
+
+
+@pytest.mark.parametrize("rows,width", [(1, 2048), (3, 1024), (1, 128), (2, 300)])
+def test_rms_norm_rows(hip, orc, rows, width):
+    rng = np.random.default_rng(width + rows)
+    x, g = gen.activations(rng, rows, width), gen.gains(rng, width)
+    out = hip.DeviceArray((rows, width), np.uint16)
+    hip.call("qwen3_tts_op_rms_norm_rows", dev(hip, x).ptr, dev(hip, g).ptr, out.ptr, rows, width,
+             C.c_float(1e-6), None)
+    assert np.array_equal(out.numpy(), orc.rms_norm_rows(x, g))
+
+
+def test_head_rms_norm(hip, orc):
+    rng = np.random.default_rng(2)
+    v, g = gen.activations(rng, 2 * 16 * 128), gen.gains(rng, 128)
+    d = dev(hip, v)
+    hip.call("qwen3_tts_op_head_rms_norm_rows", d.ptr, dev(hip, g).ptr, 2, 16, 128, C.c_float(1e-6), None)
+    assert np.array_equal(d.numpy(), orc.head_rms_norm_rows(v, g, 16, 128))
+
+
+def test_rope_in_kernel_math_close(hip, orc):
+    """The reference-formula RoPE op (powf/cosf/sinf on the device) agrees
+    with the host libm restatement within bf16 resolution."""
+    rng = np.random.default_rng(4)
+    v = gen.activations(rng, 3 * 8 * 128)
+    pos = np.array([0, 37, 1023], np.int32)
+    d = dev(hip, v)
+    hip.call("qwen3_tts_op_rope_rows", d.ptr, 3, 8, 128, dev(hip, pos).ptr, C.c_float(1e6), None)
+    ref = gen.f32(orc.rope_rows(v, 8, 128, pos))
+    got = gen.f32(d.numpy())
+    assert np.max(np.abs(got - ref)) <= 0.016
+    assert np.mean(got == ref) > 0.98
+
+
+@pytest.mark.parametrize("position", [0, 5, 1023])
+def test_qk_norm_rope_kv_append(hip, orc, position):
+    rng = np.random.default_rng(position + 1)
+    qh, kvh, d = 16, 8, 128
+    qw, kw = qh * d, kvh * d
+    qkv = gen.activations(rng, qw + 2 * kw)
+    qn, kn = gen.gains(rng, d), gen.gains(rng, d)
+    max_seq = 1024
+    table = np.empty(max_seq * d, np.uint16)
+    hip.call("qwen3_tts_rope_table_v1", max_seq, d, C.c_float(1e6), table.ctypes.data)
+    kc = hip.DeviceArray((max_seq, kw), np.uint16)
+    vc = hip.DeviceArray((max_seq, kw), np.uint16)
+    kc.upload(np.zeros((max_seq, kw), np.uint16))
+    vc.upload(np.zeros((max_seq, kw), np.uint16))
+    dq = dev(hip, qkv)
+    hip.call("qwen3_tts_op_qk_norm_rope_kv_append", dq.ptr, dev(hip, qn).ptr, dev(hip, kn).ptr,
+             ptr_array(hip, [kc.ptr]).ptr, ptr_array(hip, [vc.ptr]).ptr,
+             dev(hip, np.array([position], np.int32)).ptr, dev(hip, table).ptr, 1, qh, kvh, d,
+             C.c_float(1e-6), None)
+    q_ref = orc.rope_rows(orc.head_rms_norm_rows(qkv[:qw], qn, qh, d), qh, d, [position])
+    k_ref = orc.rope_rows(orc.head_rms_norm_rows(qkv[qw:qw + kw], kn, kvh, d), kvh, d, [position])
+    got = dq.numpy()
+    assert np.array_equal(got[:qw], q_ref)
+    assert np.array_equal(kc.numpy()[position], k_ref)
+    assert np.array_equal(vc.numpy()[position], qkv[qw + kw:])
+    untouched = np.delete(np.arange(max_seq), position)
+    assert not kc.numpy()[untouched].any() and not vc.numpy()[untouched].any()
+
+
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("length", [1, 7, 300, 1024])
+def test_attention(hip, orc, exact, length):
+    rng = np.random.default_rng(length * 2 + exact)
+    qh, kvh, d, max_seq = 16, 8, 128, 1024
+    q = gen.activations(rng, qh * d)
+    k = gen.bf16(rng.standard_normal((max_seq, kvh * d)).astype(np.float32) * 0.5)
+    v = gen.activations(rng, max_seq, kvh * d)
+    dk, dv = dev(hip, k), dev(hip, v)
+    out = hip.DeviceArray(qh * d, np.uint16)
+    pos = dev(hip, np.array([length - 1], np.int32))
+    hip.call("qwen3_tts_op_attention", exact, dev(hip, q).ptr, qh * d, ptr_array(hip, [dk.ptr]).ptr,
+             ptr_array(hip, [dv.ptr]).ptr, pos.ptr, out.ptr, 1, qh, kvh, d, max_seq, None)
+    ref = orc.attention(q, k[:length], v[:length], qh, kvh, d, length, exact=bool(exact))
+    assert np.array_equal(out.numpy(), ref)
+
+
+def test_attention_rows_with_own_caches(hip, orc):
+    rng = np.random.default_rng(9)
+    qh, kvh, d, max_seq, rows = 16, 8, 128, 64, 3
+    lengths = [1, 17, 64]
+    q = gen.activations(rng, rows, qh * d)
+    ks = [gen.activations(rng, max_seq, kvh * d) for _ in range(rows)]
+    vs = [gen.activations(rng, max_seq, kvh * d) for _ in range(rows)]
+    dks, dvs = [dev(hip, k) for k in ks], [dev(hip, v) for v in vs]
+    out = hip.DeviceArray((rows, qh * d), np.uint16)
+    pos = dev(hip, np.array([n - 1 for n in lengths], np.int32))
+    hip.call("qwen3_tts_op_attention", 0, dev(hip, q).ptr, qh * d, ptr_array(hip, [a.ptr for a in dks]).ptr,
+             ptr_array(hip, [a.ptr for a in dvs]).ptr, pos.ptr, out.ptr, rows, qh, kvh, d, max_seq, None)
+    got = out.numpy()
+    for r in range(rows):
+        n = lengths[r]
+        assert np.array_equal(got[r], orc.attention(q[r], ks[r][:n], vs[r][:n], qh, kvh, d, n, exact=False))
+
+
+def test_kv_scatter_rows(hip):
+    rng = np.random.default_rng(1)
+    rows, width = 3, 1024
+    data = gen.activations(rng, rows, 4096)
+    caches = [hip.DeviceArray((32, width), np.uint16) for _ in range(rows)]
+    for c in caches:
+        c.upload(np.zeros((32, width), np.uint16))
+    pos = np.array([0, 9, 31], np.int32)
+    hip.call("qwen3_tts_op_kv_scatter_rows", dev(hip, data).ptr, ptr_array(hip, [c.ptr for c in caches]).ptr,
+             dev(hip, pos).ptr, rows, width, 4096, None)
+    for r in range(rows):
+        got = caches[r].numpy()
+        assert np.array_equal(got[pos[r]], data[r, :width])
+        assert np.count_nonzero(got) == np.count_nonzero(data[r, :width])
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_elementwise(hip, orc, op):
+    rng = np.random.default_rng(op)
+    rows, width = 2, 777
+    a = gen.activations(rng, rows, width)
+    b = gen.activations(rng, width if op in (1, 2) else rows * width)
+    d = dev(hip, a)
+    hip.call("qwen3_tts_op_elementwise", op, d.ptr, dev(hip, b).ptr, rows, width, None)
+    if op == 0:
+        ref = orc.add_in_place(a.ravel(), b).reshape(rows, width)
+    elif op in (1, 2):
+        ref = orc.bias_activation(a, b, op == 2)
+    else:
+        ref = orc.silu_gate(a.ravel(), b).reshape(rows, width)
+    assert np.array_equal(d.numpy(), ref)
+
+
+def test_sum_embeddings(hip, orc):
+    rng = np.random.default_rng(6)
+    width, v0, v = 512, 300, 200
+    tables = [gen.activations(rng, v0 if i == 0 else v, width) for i in range(16)]
+    toks = np.concatenate([[250], rng.integers(0, v, 15)]).astype(np.int32)
+    dts = [dev(hip, t) for t in tables]
+    out = hip.DeviceArray(width, np.uint16)
+    hip.call("qwen3_tts_op_sum_embeddings", ptr_array(hip, [t.ptr for t in dts]).ptr, 16, v0, v, width,
+             dev(hip, toks).ptr, out.ptr, None)
+    ref = tables[0][250].copy()
+    for i in range(1, 16):
+        ref = orc.add_in_place(ref, tables[i][toks[i]])
+    assert np.array_equal(out.numpy(), ref)
+
+
+def sample_gpu(hip, logits, suppress, history, cfg, state):
+    d_state = dev(hip, np.array([state], np.uint64))
+    tok = hip.DeviceArray(1, np.int32)
+    hist = dev(hip, np.array(history if history else [0], np.int32))
+    cnt = dev(hip, np.array([len(history)], np.int32))
+    hip.call("qwen3_tts_op_sample_logits", dev(hip, logits).ptr, len(logits), int(suppress), 2150, hist.ptr,
+             cnt.ptr, cfg, d_state.ptr, tok.ptr, None)
+    return int(tok.numpy()[0]), int(d_state.numpy()[0])
+
+
+@pytest.mark.parametrize("vocab", [2048, 3072])
+def test_sampler_greedy_matches_oracle(hip, orc, vocab):
+    rng = np.random.default_rng(vocab)
+    for trial in range(6):
+        logits = gen.bf16(rng.standard_normal(vocab).astype(np.float32) * 2)
+        if trial == 1:  # many ties
+            logits = gen.bf16(np.round(rng.standard_normal(vocab)).astype(np.float32))
+        history = list(rng.integers(0, 2048, 40)) if trial % 2 else []
+        for suppress in (False, True):
+            cfg = hip.sampling(0, 0, 1.0, 1.0, 1.05)
+            got, _ = sample_gpu(hip, logits, suppress, history, cfg, 5)
+            ref, _ = orc.sample_logits(logits, suppress, 2150, history, 0, 0, 1.0, 1.0, 1.05, 5)
+            assert got == ref
+
+
+@pytest.mark.parametrize("top_k,top_p", [(50, 1.0), (50, 0.8), (1, 1.0), (0, 1.0), (0, 0.9), (700, 1.0)])
+def test_sampler_topk_matches_oracle(hip, orc, top_k, top_p):
+    """Same logits, same RNG state -> same token and same next state.  (The
+    draw compares double sums; exp in double on the device vs the host may
+    differ in the last ulp, which only matters at an exact boundary.)"""
+    rng = np.random.default_rng(top_k * 10 + int(top_p * 10))
+    state = 0x1234567
+    for trial in range(12):
+        logits = gen.bf16(rng.standard_normal(3072).astype(np.float32) * 3)
+        history = list(rng.integers(0, 2048, 30))
+        cfg = hip.sampling(1, top_k, top_p, 0.9, 1.05)
+        got, gstate = sample_gpu(hip, logits, True, history, cfg, state)
+        ref, rstate = orc.sample_logits(logits, True, 2150, history, 1, top_k, top_p, 0.9, 1.05, state)
+        assert (got, gstate) == (ref, rstate), trial
+        state = rstate
+
+
+def test_argmax_benchmark_known_answer(hip):
+    for vocab in (2048, 3072):
+        out = hip.ArgmaxBenchmark()
+        hip.call("qwen3_tts_benchmark_bf16_argmax", 0, vocab, 100, C.byref(out))
+        assert out.selected_token == out.expected_token == 1729
+
+
+def test_validate_transformer_primitives(hip):
+    out = hip.PrimitiveParity()
+    hip.call("qwen3_tts_validate_transformer_primitives", 0, C.byref(out))
+    for f, _ in hip.PrimitiveParity._fields_:
+        assert getattr(out, f) <= 0.016
+
+
+def test_probe_and_bf16_gemv_benchmark(hip):
+    info = hip.DeviceInfo()
+    hip.call("qwen3_tts_probe_device", 0, C.byref(info))
+    assert b"gfx950" in info.device_name
+    assert info.total_global_memory_bytes > 200 << 30
+    out = hip.GemvBenchmark()
+    hip.call("qwen3_tts_benchmark_bf16_gemv", 0, 2048, 2048, 50, C.byref(out))
+    assert out.mean_launch_microseconds > 0
+
+
+def test_device_buffer_sequential_upload(hip):
+    lib = hip.load()
+    buf = C.c_void_p()
+    m = hip.WeightUploadMetrics()
+    hip.call("qwen3_tts_device_buffer_create", 0, 1 << 20, 1 << 16, C.byref(buf), C.byref(m))
+    try:
+        data = np.arange(1 << 20, dtype=np.uint8) * 7
+        hip.call("qwen3_tts_device_buffer_upload", buf, 0, data.ctypes.data, 1 << 19)
+        with pytest.raises(hip.Qwen3TtsError):  # not contiguous
+            hip.call("qwen3_tts_device_buffer_upload", buf, 0, data.ctypes.data, 16)
+        with pytest.raises(hip.Qwen3TtsError):  # not complete
+            hip.call("qwen3_tts_device_buffer_finish", buf, C.byref(m))
+        hip.call("qwen3_tts_device_buffer_upload", buf, 1 << 19, data[1 << 19:].ctypes.data, 1 << 19)
+        hip.call("qwen3_tts_device_buffer_finish", buf, C.byref(m))
+        assert m.uploaded_bytes == 1 << 20 and m.upload_calls == 16
+        back = np.empty(1 << 20, np.uint8)
+        hip.call("qwen3_tts_device_buffer_read", buf, 0, back.ctypes.data, 1 << 20)
+        assert np.array_equal(back, data)
+        assert lib.qwen3_tts_device_buffer_data(buf)
+    finally:
+        lib.qwen3_tts_device_buffer_destroy(buf)
