@@ -12,8 +12,23 @@ import gen
 pytestmark = pytest.mark.gpu
 
 
+# Device arrays must outlive the kernels that use them: a DeviceArray frees
+# its memory when garbage-collected, so every upload is kept alive here until
+# the test ends (passing `.ptr` of a temporary would hand the kernel freed
+# memory).
+_KEEP = []
+
+
+@pytest.fixture(autouse=True)
+def _release_device_arrays():
+    yield
+    _KEEP.clear()
+
+
 def dev(hip, a):
-    return hip.DeviceArray.from_numpy(a)
+    d = hip.DeviceArray.from_numpy(a)
+    _KEEP.append(d)
+    return d
 
 
 def ptr_array(hip, pointers):
