@@ -184,9 +184,12 @@ __device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, fl
 
 // ---------------------------------------------------------------------------
 // Exact-order GEMV, one activation row, K = kVpl * 512 known at compile time.
-// Each half-wave processes a unit of two weight rows per iteration:
-//   plain/residual epilogues: channels 2u and 2u+1;
-//   SiLU epilogues: gate row u and up row out+u.
+// A half-wave owns one unit per iteration: one weight row (plain / residual /
+// bias epilogues) or the gate row u and the up row out+u (SiLU epilogues).
+// Latency order: the first unit's weight loads are issued before anything
+// else (they do not depend on x), then x (and the RMSNorm gain) is staged
+// into LDS with 128-bit loads, the norm statistic is reduced from LDS, and
+// each lane pulls its x slice into registers while the weights are in flight.
 // ---------------------------------------------------------------------------
 template <int kVpl, int kEpi, bool kNorm>
 __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
@@ -194,12 +197,38 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
         a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
     }
     constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    constexpr int kRows = kSilu ? 2 : 1;
     constexpr bool kPacked = kVpl > 6;
     constexpr int kIn = kVpl * 512;
+    constexpr int kChunks = kIn * 2 / 16;  // 16-byte chunks of one bf16 row
+    __shared__ uint4 x_lds[kChunks];
+    __shared__ uint4 g_lds[kNorm ? kChunks : 1];
     const int lane = threadIdx.x & 31;
+    const int units = a.out_features;
+    const int stride = gridDim.x * kHalfWaves;
+    int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5);
+
+    int4 w[kRows][kVpl];
+    auto issue = [&](int u) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const int row = r == 0 ? u : a.out_features + u;
+            const int4* base = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row) * kIn);
+#pragma unroll
+            for (int i = 0; i < kVpl; ++i) w[r][i] = stream_load(base + lane + 32 * i);
+        }
+    };
+    if (unit < units) issue(unit);
+
+    for (int c = threadIdx.x; c < kChunks; c += kThreads) {
+        x_lds[c] = reinterpret_cast<const uint4*>(a.input)[c];
+        if constexpr (kNorm) g_lds[c] = reinterpret_cast<const uint4*>(a.norm_weight)[c];
+    }
+    __syncthreads();
+    const bf16_t* xs = reinterpret_cast<const bf16_t*>(x_lds);
     float inverse = 1.0f;
     if constexpr (kNorm) {
-        inverse = wave_inverse_rms(a.input, kIn, a.norm_epsilon);
+        inverse = wave_inverse_rms(xs, kIn, a.norm_epsilon);
     }
     // Activation slice of this lane: vectors lane + 32*i.
     float xf[kPacked ? 1 : kVpl][16];
@@ -207,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < kVpl; ++i) {
         float tmp[16];
-        load_x16<kNorm>(a.input, a.norm_weight, lane + 32 * i, inverse, tmp);
+        load_x16<kNorm>(xs, reinterpret_cast<const bf16_t*>(g_lds), lane + 32 * i, inverse, tmp);
         if constexpr (kPacked) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -220,42 +249,28 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
         }
     }
 
-    const int units = kSilu ? a.out_features : (a.out_features + 1) / 2;
-    const int stride = gridDim.x * kHalfWaves;
-    for (int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5); unit < units; unit += stride) {
-        const int row0 = kSilu ? unit : 2 * unit;
-        const int row1 = kSilu ? a.out_features + unit : 2 * unit + 1;
-        const bool has1 = kSilu || row1 < a.out_features;
-        const int4* w0 = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row0) * kIn);
-        const int4* w1 = reinterpret_cast<const int4*>(
-            a.weight + static_cast<size_t>(has1 ? row1 : row0) * kIn);
-        int4 r0[kVpl];
-        int4 r1[kVpl];
+    for (; unit < units; unit += stride) {
+        float acc[kRows];
 #pragma unroll
-        for (int i = 0; i < kVpl; ++i) {
-            r0[i] = stream_load(w0 + lane + 32 * i);
-            r1[i] = stream_load(w1 + lane + 32 * i);
-        }
-        float acc0 = 0.0f;
-        float acc1 = 0.0f;
+        for (int r = 0; r < kRows; ++r) {
+            acc[r] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kVpl; ++i) {
-            if constexpr (kPacked) {
-                acc0 += chain16_packed(r0[i], xp[i]);
-                acc1 += chain16_packed(r1[i], xp[i]);
-            } else {
-                acc0 += chain16(r0[i], xf[i]);
-                acc1 += chain16(r1[i], xf[i]);
+            for (int i = 0; i < kVpl; ++i) {
+                if constexpr (kPacked) {
+                    acc[r] += chain16_packed(w[r][i], xp[i]);
+                } else {
+                    acc[r] += chain16(w[r][i], xf[i]);
+                }
             }
         }
-        acc0 = fold32(acc0);
-        acc1 = fold32(acc1);
+        if (unit + stride < units) issue(unit + stride);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[r] = fold32(acc[r]);
         if (lane == 0) {
             if constexpr (kSilu) {
-                store_gate_up<kEpi>(a, unit, acc0, acc1);
+                store_gate_up<kEpi>(a, unit, acc[0], acc[kRows - 1]);
             } else {
-                store_channel<kEpi>(a, row0, acc0);
-                if (has1) store_channel<kEpi>(a, row1, acc1);
+                store_channel<kEpi>(a, unit, acc[0]);
             }
         }
     }
@@ -553,11 +568,10 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
         gemv_mfma<kEpi, kNorm><<<grid, kThreads, 0, s>>>(a);
         return hipGetLastError();
     }
-    const int units = kSilu ? a.out_features : (a.out_features + 1) / 2;
     if (a.rows == 1 && a.in_features % 512 == 0) {
         const int vpl = a.in_features / 512;
         if (vpl == 2 || vpl == 4 || vpl == 6 || vpl == 12) {
-            const int grid = (units + kHalfWaves - 1) / kHalfWaves;
+            const int grid = (a.out_features + kHalfWaves - 1) / kHalfWaves;
             return dispatch_fixed<kEpi, kNorm>(a, vpl, grid, s);
         }
     }
