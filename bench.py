@@ -79,12 +79,15 @@ def cpu_baseline(seconds: float = 10.0):
     }
 
 
-def frame_benchmark(hip, frames: int = 200, prompt: int = 824, max_seq: int = 1024):
+def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3):
     """Config 5 through the reference C ABI: VoiceDesign geometry, synthetic
     bf16 weights quantized to int8 at finalize, prompt of `prompt` tokens,
-    then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed."""
+    then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed.  The
+    prompt fills the KV cache so that the timed frames run at context
+    max_seq - frames .. max_seq (attention reads up to 1024 positions)."""
     import numpy as np
 
+    prompt = max_seq - frames - warm
     lib = hip.load()
     cfg = hip.default_config()
     model = C.c_void_p()
@@ -157,7 +160,6 @@ def frame_benchmark(hip, frames: int = 200, prompt: int = 824, max_seq: int = 10
             info = hip.CodecFrameInfo()
             nxt = C.c_uint16()
             trailing = rng.integers(0, cfg.text_vocabulary, frames + 8).astype(np.int32)
-            warm = 3
             done = 0
             pred_ms = talk_ms = 0.0
             eos = 0

@@ -697,7 +697,7 @@ public:
             check_hip(hipEventRecord(stop_, stream_), "hipEventRecord(talker stop)");
             ++position_;
             ++history_count_;
-            device_samples_ += kCodebooks;
+            device_samples_ += kCodebooks;  // 15 predictor samples + 1 talker sample
             check_hip(hipMemcpyAsync(pinned_, ints_.as<int>() + 2, sizeof(int), hipMemcpyDeviceToHost, stream_), "copy sampled token");
             check_hip(hipEventRecord(semantic_ready_, stream_), "hipEventRecord(semantic ready)");
         } catch (...) {
@@ -914,6 +914,7 @@ private:
                                           history_.as<int>(), history_count_ptr(), stream_),
                   "talker sample");
         ++device_samples_;
+        ++history_count_;
     }
 
     // Predictor: 16 positions (talker.cu:1153-1220).

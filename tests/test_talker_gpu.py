@@ -150,13 +150,15 @@ def test_begin_finish_lease_protocol(hip, orc, toy):
             with pytest.raises(hip.Qwen3TtsError) as e:
                 hip.call("qwen3_tts_session_next_frame_begin_v2", s, 1, g, g, C.byref(v2))
             assert e.value.status == hip.STATUS_STATE
-            codes = np.zeros(16, np.uint16)
-            hip.call("qwen3_tts_device_memcpy", codes.ctypes.data, view.device_codes, 32)
             nxt = C.c_uint16()
             info = hip.CodecFrameInfo()
             with pytest.raises(hip.Qwen3TtsError):  # stale lease
                 hip.call("qwen3_tts_session_next_frame_finish_v2", s, view.lease_id + 1, None, C.byref(nxt), C.byref(info))
             hip.call("qwen3_tts_session_next_frame_finish_v2", s, view.lease_id, None, C.byref(nxt), C.byref(info))
+            # the borrowed codes are readable once ready_event has fired; finish
+            # synchronized past it and no later frame has overwritten them yet
+            codes = np.zeros(16, np.uint16)
+            hip.call("qwen3_tts_device_memcpy", codes.ctypes.data, view.device_codes, 32)
             ocodes, onxt = osess.frame(semantic, 17 + f, GREEDY, GREEDY)
             assert np.array_equal(codes, ocodes) and nxt.value == onxt
             semantic = nxt.value
