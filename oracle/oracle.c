@@ -608,7 +608,8 @@ static void gemv_bf16(const int8_t* w, const float* s, const uint16_t* x,
  * post norm, separate gate and up GEMVs, silu_gate, down + residual. */
 void orc_run_decoder(const OrcLayer* layers, const OrcDims* dims,
                      uint16_t* hidden, uint16_t* k_cache, uint16_t* v_cache,
-                     int cache_rows, int position, float eps, float theta) {
+                     int cache_rows, int position, float eps, float theta,
+                     int batch_semantics) {
     const int H = dims->hidden;
     const int I = dims->intermediate;
     const int qw = dims->query_heads * dims->head_dimension;
@@ -635,6 +636,16 @@ void orc_run_decoder(const OrcLayer* layers, const OrcDims* dims,
         orc_rope_rows(k, 1, dims->key_value_heads, dims->head_dimension, &position, theta);
         memcpy(kc + (size_t)position * kvw, k, (size_t)kvw * 2);
         memcpy(vc + (size_t)position * kvw, v, (size_t)kvw * 2);
+        if (batch_semantics) {
+            /* batch_run_decoder, int8 branch (K/talker.cu:2178-2285) */
+            orc_causal_gqa_attention_fast(q, kc, vc, attn, dims->query_heads, dims->key_value_heads,
+                                          dims->head_dimension, position + 1);
+            orc_int8_gemm_rows_add(L->o, L->o_s, attn, hidden, qw, H, 1);
+            orc_rms_norm_rows(hidden, L->post_norm, normalized, 1, H, eps);
+            orc_int8_gate_up_silu_rows(L->gate_up, L->gate_up_s, normalized, gate, H, I, 1);
+            orc_int8_gemm_rows_add(L->down, L->down_s, gate, hidden, I, H, 1);
+            continue;
+        }
         orc_causal_gqa_attention(q, kc, vc, attn, dims->query_heads, dims->key_value_heads,
                                  dims->head_dimension, position + 1);
         gemv_bf16(L->o, L->o_s, attn, proj, qw, H);
@@ -667,7 +678,7 @@ void orc_talker_step(const OrcModel* m, OrcSession* s, const uint16_t* input) {
     uint16_t* hidden = (uint16_t*)malloc((size_t)H * 2);
     memcpy(hidden, input, (size_t)H * 2);
     orc_run_decoder(m->talker_layers, &m->talker, hidden, s->talker_k, s->talker_v,
-                    s->max_seq, s->position, m->rms_eps, m->rope_theta);
+                    s->max_seq, s->position, m->rms_eps, m->rope_theta, m->batch_semantics);
     orc_rms_norm_rows(hidden, m->talker_norm, s->last_hidden, 1, H, m->rms_eps);
     gemv_bf16(m->codec_head, m->codec_head_s, s->last_hidden, s->logits, H, m->talker_vocab);
     free(hidden);
@@ -693,7 +704,7 @@ static void predictor_position(const OrcModel* m, OrcSession* s, const uint16_t*
     gemv_bf16(m->small_to_mtp, m->small_to_mtp_s, input, hidden, H, PH);
     orc_bias_activation(hidden, m->small_to_mtp_bias, 1, PH, 0);
     orc_run_decoder(m->predictor_layers, &m->predictor, hidden, s->pred_k, s->pred_v,
-                    m->codebooks, position, m->rms_eps, m->rope_theta);
+                    m->codebooks, position, m->rms_eps, m->rope_theta, m->batch_semantics);
     if (head >= 0) {
         uint16_t* normalized = (uint16_t*)malloc((size_t)PH * 2);
         orc_rms_norm_rows(hidden, m->predictor_norm, normalized, 1, PH, m->rms_eps);
@@ -704,7 +715,9 @@ static void predictor_position(const OrcModel* m, OrcSession* s, const uint16_t*
     free(hidden);
 }
 
-/* begin_frame, K/talker.cu:1095-1244 (single session). */
+/* begin_frame, K/talker.cu:1095-1244 (single session); with
+ * m->batch_semantics one session's row of batch_begin_frames,
+ * K/talker.cu:1495-1881 (each row of the lockstep batch is independent). */
 int orc_frame_step(const OrcModel* m, OrcSession* s, int semantic_token,
                    int trailing_text_token, const OrcSampling* ts,
                    const OrcSampling* ps, uint16_t* codes) {

@@ -118,6 +118,10 @@ typedef struct OrcModel {
     const uint16_t* const* predictor_embeddings; /* [codebooks-1] x [pvocab][talker.hidden] */
     const int8_t* const* predictor_heads;        /* [codebooks-1] x [pvocab][predictor.hidden] */
     const float* const* predictor_heads_s;
+    /* 0: single-session decoder (K/talker.cu:3251-3456); 1: the lockstep
+     * batched int8 decoder (K/talker.cu:2038-2334): fast attention, fma
+     * residual epilogue, fused gate/up SiLU. */
+    int batch_semantics;
 } OrcModel;
 
 typedef struct OrcSession {
@@ -143,7 +147,8 @@ typedef struct OrcSampling {
  * (K/talker.cu:3251-3456).  k_cache/v_cache: [layers][cache_rows][kv_width]. */
 void orc_run_decoder(const OrcLayer* layers, const OrcDims* dims,
                      uint16_t* hidden, uint16_t* k_cache, uint16_t* v_cache,
-                     int cache_rows, int position, float eps, float theta);
+                     int cache_rows, int position, float eps, float theta,
+                     int batch_semantics);
 /* Talker step on a prepared input embedding; writes logits + last_hidden. */
 void orc_talker_step(const OrcModel* m, OrcSession* s, const uint16_t* input);
 /* Text projection fc1+SiLU, fc2+bias (K/talker.cu:2676-2719). */

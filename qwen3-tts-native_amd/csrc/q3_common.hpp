@@ -199,4 +199,17 @@ hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int voc
                                  int vocabulary, int width, const int* tokens, bf16_t* output,
                                  hipStream_t stream);
 
+// Lockstep-batch glue: rows of a batch from / to per-session buffers.
+hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,
+                              hipStream_t stream);
+hipError_t launch_scatter_rows(const bf16_t* input, bf16_t* const* destinations, int rows, int width,
+                               hipStream_t stream);
+hipError_t launch_gather_embedding_rows(const bf16_t* table, int vocabulary, int width,
+                                        const int* const* token_bases, int offset, bf16_t* output,
+                                        int rows, hipStream_t stream);
+hipError_t launch_sum_embeddings_rows(const bf16_t* const* tables, int count, int vocabulary0,
+                                      int vocabulary, int width, const int* const* token_bases,
+                                      bf16_t* output, int rows, hipStream_t stream);
+hipError_t launch_increment_each(int* const* counters, int count, hipStream_t stream);
+
 }  // namespace q3

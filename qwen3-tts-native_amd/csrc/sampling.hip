@@ -374,7 +374,98 @@ __global__ void sum_embeddings_kernel(const bf16_t* const* tables, int count, in
     if (have) output[i] = f2bf(acc);
 }
 
+// Lockstep-batch glue (talker.cu:1552-1607,1700-1770 equivalents): rows of a
+// batch come from / go to per-session buffers through pointer tables.
+__global__ void gather_rows_kernel(const bf16_t* const* sources, int width, bf16_t* output) {
+    const bf16_t* src = sources[blockIdx.y];
+    bf16_t* dst = output + static_cast<size_t>(blockIdx.y) * width;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += blockDim.x * gridDim.x) dst[i] = src[i];
+}
+
+__global__ void scatter_rows_kernel(const bf16_t* input, bf16_t* const* destinations, int width) {
+    const bf16_t* src = input + static_cast<size_t>(blockIdx.y) * width;
+    bf16_t* dst = destinations[blockIdx.y];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += blockDim.x * gridDim.x) dst[i] = src[i];
+}
+
+// gather_embedding_rows_kernel semantics (talker_kernels.cu:680-709): row r
+// reads token_bases[r][offset]; an out-of-range token leaves the row as is.
+__global__ void gather_embedding_rows_kernel(const bf16_t* table, int vocabulary, int width,
+                                             const int* const* token_bases, int offset, bf16_t* output) {
+    const int token = token_bases[blockIdx.y][offset];
+    if (token < 0 || token >= vocabulary) return;
+    const bf16_t* src = table + static_cast<size_t>(token) * width;
+    bf16_t* dst = output + static_cast<size_t>(blockIdx.y) * width;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += blockDim.x * gridDim.x) dst[i] = src[i];
+}
+
+__global__ void sum_embeddings_rows_kernel(const bf16_t* const* tables, int count, int vocabulary0,
+                                           int vocabulary, int width, const int* const* token_bases,
+                                           bf16_t* output) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= width) return;
+    const int* tokens = token_bases[blockIdx.y];
+    bf16_t* out = output + static_cast<size_t>(blockIdx.y) * width;
+    const int first = tokens[0];
+    float acc = bf2f(out[i]);
+    bool have = false;
+    if (first >= 0 && first < vocabulary0) {
+        acc = bf2f(tables[0][static_cast<size_t>(first) * width + i]);
+        have = true;
+    }
+    for (int r = 1; r < count; ++r) {
+        const int tok = tokens[r];
+        if (tok < 0 || tok >= vocabulary) continue;
+        acc = round_bf(acc + bf2f(tables[r][static_cast<size_t>(tok) * width + i]));
+        have = true;
+    }
+    if (have) out[i] = f2bf(acc);
+}
+
+__global__ void increment_each_kernel(int* const* counters, int count) {
+    const int i = threadIdx.x;
+    if (i < count) *counters[i] += 1;
+}
+
 }  // namespace
+
+hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,
+                              hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    gather_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(sources, width, output);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_rows(const bf16_t* input, bf16_t* const* destinations, int rows, int width,
+                               hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    scatter_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(input, destinations, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_embedding_rows(const bf16_t* table, int vocabulary, int width,
+                                        const int* const* token_bases, int offset, bf16_t* output,
+                                        int rows, hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    gather_embedding_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(
+        table, vocabulary, width, token_bases, offset, output);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_embeddings_rows(const bf16_t* const* tables, int count, int vocabulary0,
+                                      int vocabulary, int width, const int* const* token_bases,
+                                      bf16_t* output, int rows, hipStream_t stream) {
+    if (rows <= 0 || width <= 0 || count <= 0) return hipErrorInvalidValue;
+    sum_embeddings_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(
+        tables, count, vocabulary0, vocabulary, width, token_bases, output);
+    return hipGetLastError();
+}
+
+hipError_t launch_increment_each(int* const* counters, int count, hipStream_t stream) {
+    if (count <= 0 || count > 64) return hipErrorInvalidValue;
+    increment_each_kernel<<<1, 64, 0, stream>>>(counters, count);
+    return hipGetLastError();
+}
 
 hipError_t launch_sample_logits(const bf16_t* logits, int vocabulary, bool suppress, int eos,
                                 const int* history, const int* history_count,

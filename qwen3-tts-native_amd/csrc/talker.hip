@@ -175,10 +175,12 @@ bool int8_decode_enabled() {
     return !(std::strcmp(value, "0") == 0 || std::strcmp(value, "false") == 0);
 }
 
+// GEMV mode of the lockstep batch: the exact reference order (VALU) on
+// request, otherwise exact for one row and the MFMA skinny GEMM for 2..8.
 int batch_gemv_mode() {
     const char* value = std::getenv("QWEN3_TTS_BATCH_GEMV");
     if (value != nullptr && std::strcmp(value, "exact") == 0) return kModeExact;
-    return kModeMfma;
+    return kModeAuto;
 }
 
 class Session;
@@ -451,6 +453,9 @@ private:
     const bf16_t* predictor_norm_ = nullptr;
     std::array<const bf16_t*, kResidualCodebooks> predictor_embeddings_{};
     std::mutex batch_mutex_;
+
+public:
+    std::unique_ptr<BatchRunner, void (*)(BatchRunner*)> batch_{nullptr, nullptr};
 };
 
 // ---------------------------------------------------------------------------
@@ -1075,9 +1080,342 @@ Qwen3TtsModelConfigV1 default_config() {
     return c;
 }
 
-void batch_begin_frames(Model*, Session**, int, const int*, const Qwen3TtsSamplingConfig*,
-                        const Qwen3TtsSamplingConfig*, Qwen3TtsDeviceFrameViewV2*) {
-    throw std::runtime_error("batched frames are not available yet");
+
+// ---------------------------------------------------------------------------
+// Lockstep batch of up to 8 sessions (talker.cu:1352-1969): one frame for all
+// sessions with every weight matrix read once.  Row semantics are those of
+// the reference's batched int8 decoder (talker.cu:2038-2334): fused QKV,
+// fast attention, fma residual epilogue, fused gate/up SiLU.  KV caches,
+// sampler state, histories and events stay session-local; per-frame values
+// reach the (graph-captured) kernels through device tables refreshed from
+// pinned host memory before each launch.
+// ---------------------------------------------------------------------------
+class BatchRunner {
+public:
+    static constexpr int kCapacity = kMaxBatch;
+    static constexpr int kSlots = kCodebooks + 1;  // predictor positions 0..15, talker
+
+    explicit BatchRunner(Model& m) : m_(m), cfg_(m.config()), device_(m.device_index()) {
+        check_hip(hipSetDevice(device_), "hipSetDevice(batch)");
+        check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate(batch)");
+        for (hipEvent_t& e : join_) check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate(join)");
+        const Dims& T = cfg_.talker;
+        const Dims& P = cfg_.predictor;
+        const size_t b = sizeof(bf16_t);
+        const size_t R = kCapacity;
+        hidden_ = DeviceBuffer(R * T.hidden * b);
+        normalized_ = DeviceBuffer(R * T.hidden * b);
+        p_hidden_ = DeviceBuffer(R * P.hidden * b);
+        text_input_ = DeviceBuffer(R * T.hidden * b);
+        proj_ = DeviceBuffer(R * T.hidden * b);
+        qkv_ = DeviceBuffer(R * std::max(T.qkv_width(), P.qkv_width()) * b);
+        attn_ = DeviceBuffer(R * std::max(T.query_width(), P.query_width()) * b);
+        act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
+        logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
+        layers_ = T.layers + P.layers;
+        table_bytes_ = off_trail_values() + R * sizeof(int);
+        tables_ = DeviceBuffer(table_bytes_);
+        check_hip(hipHostMalloc(&pinned_, table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
+        std::memset(pinned_, 0, table_bytes_);
+    }
+    ~BatchRunner() {
+        (void)hipSetDevice(device_);
+        if (stream_) (void)hipStreamSynchronize(stream_);
+        destroy_graphs();
+        if (pinned_) (void)hipHostFree(pinned_);
+        for (hipEvent_t e : join_) if (e) (void)hipEventDestroy(e);
+        if (stream_) (void)hipStreamDestroy(stream_);
+    }
+
+    void begin(Session** s, int n, const int* trailing, const Qwen3TtsSamplingConfig* ts,
+               const Qwen3TtsSamplingConfig* ps, Qwen3TtsDeviceFrameViewV2* views) {
+        check_hip(hipSetDevice(device_), "hipSetDevice(batch frame)");
+        std::vector<SamplingParams> tp(n), pp(n);
+        for (int i = 0; i < n; ++i) {
+            if (s[i]->model() != &m_) throw std::runtime_error("batched session belongs to a different model");
+            for (int j = 0; j < i; ++j) {
+                if (s[j] == s[i]) throw std::runtime_error("a session appears twice in the batch");
+            }
+            s[i]->validate_frame(s[i]->semantic_, trailing[i]);
+            tp[i] = params_of(ts[i]);
+            pp[i] = params_of(ps[i]);
+        }
+        for (int i = 0; i < n; ++i) {
+            Session* c = s[i];
+            const uint64_t lease = c->next_lease_++;
+            if (c->next_lease_ == 0) c->next_lease_ = 1;
+            c->frame_in_flight_ = true;
+            c->pending_copy_ = false;
+            c->pending_lease_ = lease;
+            c->pending_position_ = static_cast<uint32_t>(c->position_);
+        }
+        fill_tables(s, n, trailing);
+        std::vector<uint64_t> key;
+        key.push_back(static_cast<uint64_t>(n));
+        for (int i = 0; i < n; ++i) {
+            key.push_back(reinterpret_cast<uint64_t>(s[i]));
+            for (const SamplingParams* q : {&tp[i], &pp[i]}) {
+                uint32_t bits[3];
+                std::memcpy(&bits[0], &q->top_p, 4);
+                std::memcpy(&bits[1], &q->temperature, 4);
+                std::memcpy(&bits[2], &q->penalty, 4);
+                key.push_back((static_cast<uint64_t>(q->do_sample) << 32) | static_cast<uint32_t>(q->top_k));
+                key.push_back((static_cast<uint64_t>(bits[0]) << 32) | bits[1]);
+                key.push_back(bits[2]);
+            }
+        }
+        try {
+            for (int i = 0; i < n; ++i) {
+                check_hip(hipEventRecord(join_[i], s[i]->stream_), "hipEventRecord(join)");
+                check_hip(hipStreamWaitEvent(stream_, join_[i], 0), "hipStreamWaitEvent(join)");
+            }
+            if (key != key_) {
+                destroy_graphs();
+                key_ = key;
+            }
+            check_hip(hipMemcpyAsync(tables_.as<void>(), pinned_, table_bytes_, hipMemcpyHostToDevice, stream_),
+                      "upload batch tables");
+            for (int i = 0; i < n; ++i) check_hip(hipEventRecord(s[i]->predictor_start_, stream_), "hipEventRecord");
+            run_graph(predictor_graph_, [&] { enqueue_predictor(s, n, pp); });
+            for (int i = 0; i < n; ++i) {
+                check_hip(hipEventRecord(s[i]->predictor_stop_, stream_), "hipEventRecord");
+                check_hip(hipEventRecord(s[i]->codes_ready_, stream_), "hipEventRecord");
+                check_hip(hipEventRecord(s[i]->start_, stream_), "hipEventRecord");
+            }
+            run_graph(talker_graph_, [&] { enqueue_talker(s, n, tp); });
+            for (int i = 0; i < n; ++i) {
+                Session* c = s[i];
+                check_hip(hipEventRecord(c->stop_, stream_), "hipEventRecord");
+                check_hip(hipMemcpyAsync(c->pinned_, c->sampled_ptr(), sizeof(int), hipMemcpyDeviceToHost, stream_),
+                          "copy sampled token");
+                check_hip(hipEventRecord(c->semantic_ready_, stream_), "hipEventRecord(semantic ready)");
+                check_hip(hipStreamWaitEvent(c->stream_, c->semantic_ready_, 0), "hipStreamWaitEvent(session)");
+                c->device_samples_ += kCodebooks;
+                ++c->history_count_;
+                ++c->position_;
+            }
+        } catch (...) {
+            for (int i = 0; i < n; ++i) s[i]->poison();
+            destroy_graphs();
+            (void)hipStreamSynchronize(stream_);
+            throw;
+        }
+        for (int i = 0; i < n; ++i) views[i] = s[i]->view(s[i]->pending_lease_);
+    }
+
+private:
+    // Table layout (identical in pinned host memory and in device memory):
+    // positions int[kSlots][8] | K/V bases ptr[2*layers][8] | token bases ptr[8] |
+    // trailing-token ptrs ptr[8] | last_hidden ptrs ptr[8] | position ptrs ptr[8] |
+    // trailing tokens int[8]
+    size_t off_kv() const { return kSlots * kCapacity * sizeof(int); }
+    size_t off_tokens() const { return off_kv() + 2 * layers_ * kCapacity * sizeof(void*); }
+    size_t off_trail_ptrs() const { return off_tokens() + kCapacity * sizeof(void*); }
+    size_t off_last() const { return off_trail_ptrs() + kCapacity * sizeof(void*); }
+    size_t off_pos_ptrs() const { return off_last() + kCapacity * sizeof(void*); }
+    size_t off_trail_values() const { return off_pos_ptrs() + kCapacity * sizeof(void*); }
+    template <typename T>
+    T* dev_at(size_t offset) const { return reinterpret_cast<T*>(tables_.as<char>() + offset); }
+    template <typename T>
+    T* host_at(size_t offset) const { return reinterpret_cast<T*>(static_cast<char*>(pinned_) + offset); }
+
+    int* positions(int slot) const { return dev_at<int>(0) + slot * kCapacity; }
+    bf16_t* const* kv_table(int layer_slot, bool value) const {
+        return dev_at<bf16_t*>(off_kv()) + (2 * layer_slot + (value ? 1 : 0)) * kCapacity;
+    }
+    const int* const* token_bases() const { return dev_at<const int*>(off_tokens()); }
+    const int* const* trailing_ptrs() const { return dev_at<const int*>(off_trail_ptrs()); }
+    bf16_t* const* last_hidden_ptrs() const { return dev_at<bf16_t*>(off_last()); }
+    int* const* position_ptrs() const { return dev_at<int*>(off_pos_ptrs()); }
+
+    void fill_tables(Session** s, int n, const int* trailing) {
+        int* pos = host_at<int>(0);
+        for (int slot = 0; slot < kCodebooks; ++slot)
+            for (int i = 0; i < kCapacity; ++i) pos[slot * kCapacity + i] = slot;
+        for (int i = 0; i < kCapacity; ++i) pos[kCodebooks * kCapacity + i] = i < n ? s[i]->position_ : 0;
+        bf16_t** kv = host_at<bf16_t*>(off_kv());
+        const int TL = cfg_.talker.layers, PL = cfg_.predictor.layers;
+        const int* trail_dev = dev_at<int>(off_trail_values());
+        for (int i = 0; i < n; ++i) {
+            const std::vector<bf16_t*>& hb = s[i]->host_bases_;
+            for (int l = 0; l < TL; ++l) {
+                kv[(2 * l) * kCapacity + i] = hb[l];
+                kv[(2 * l + 1) * kCapacity + i] = hb[TL + l];
+            }
+            for (int l = 0; l < PL; ++l) {
+                kv[(2 * (TL + l)) * kCapacity + i] = hb[2 * TL + l];
+                kv[(2 * (TL + l) + 1) * kCapacity + i] = hb[2 * TL + PL + l];
+            }
+            host_at<const int*>(off_tokens())[i] = s[i]->frame_tokens();
+            host_at<const int*>(off_trail_ptrs())[i] = trail_dev + i;
+            host_at<bf16_t*>(off_last())[i] = s[i]->last_hidden_.as<bf16_t>();
+            host_at<int*>(off_pos_ptrs())[i] = s[i]->position_ptr();
+            host_at<int>(off_trail_values())[i] = trailing[i];
+        }
+    }
+
+    template <typename Enqueue>
+    void run_graph(hipGraphExec_t& exec, Enqueue&& enqueue) {
+        if (exec != nullptr) {
+            check_hip(hipGraphLaunch(exec, stream_), "hipGraphLaunch(batch)");
+            return;
+        }
+        if (uncaptured_ < 2 || !Session::graphs_enabled()) {
+            enqueue();
+            ++uncaptured_;
+            return;
+        }
+        check_hip(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture(batch)");
+        try {
+            enqueue();
+        } catch (...) {
+            hipGraph_t aborted = nullptr;
+            (void)hipStreamEndCapture(stream_, &aborted);
+            if (aborted) (void)hipGraphDestroy(aborted);
+            throw;
+        }
+        hipGraph_t graph = nullptr;
+        check_hip(hipStreamEndCapture(stream_, &graph), "hipStreamEndCapture(batch)");
+        const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        check_hip(st, "hipGraphInstantiate(batch)");
+        check_hip(hipGraphLaunch(exec, stream_), "hipGraphLaunch(batch)");
+    }
+
+    void destroy_graphs() {
+        for (hipGraphExec_t* g : {&predictor_graph_, &talker_graph_}) {
+            if (*g) (void)hipGraphExecDestroy(*g);
+            *g = nullptr;
+        }
+        uncaptured_ = 0;
+    }
+
+    void run_decoder(bool predictor, int n, const int* pos, int capacity) {
+        const Dims& d = predictor ? cfg_.predictor : cfg_.talker;
+        const std::vector<Layer>& layers = predictor ? m_.predictor_layers_ : m_.talker_layers_;
+        bf16_t* hidden = predictor ? p_hidden_.as<bf16_t>() : hidden_.as<bf16_t>();
+        const int slot0 = predictor ? cfg_.talker.layers : 0;
+        const int mode = batch_gemv_mode();
+        for (int l = 0; l < d.layers; ++l) {
+            const Layer& L = layers[l];
+            Gemv(L.qkv, hidden, d.hidden, d.qkv_width(), kEpiStore).norm(L.input_norm, cfg_.eps).rows(n, mode)
+                .to(qkv_.as<bf16_t>()).run(stream_, "batch QKV GEMV");
+            check_hip(launch_qk_norm_rope_kv_append(qkv_.as<bf16_t>(), L.q_norm, L.k_norm, kv_table(slot0 + l, false),
+                                                    kv_table(slot0 + l, true), pos, m_.rope_table_.as<bf16_t>(), n,
+                                                    d.query_heads, d.key_value_heads, d.head_dimension, cfg_.eps, stream_),
+                      "batch q/k norm + RoPE + KV append");
+            check_hip(launch_attention(false, qkv_.as<bf16_t>(), d.qkv_width(), kv_table(slot0 + l, false),
+                                       kv_table(slot0 + l, true), nullptr, nullptr, pos, 0, attn_.as<bf16_t>(), n,
+                                       d.query_heads, d.key_value_heads, d.head_dimension, capacity, stream_),
+                      "batch attention");
+            Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
+                .run(stream_, "batch O GEMV");
+            Gemv(L.gate_up, hidden, d.hidden, d.intermediate, kEpiSiluFused).norm(L.post_norm, cfg_.eps).rows(n, mode)
+                .to(act_.as<bf16_t>()).run(stream_, "batch gate/up GEMV");
+            Gemv(L.down, act_.as<bf16_t>(), d.intermediate, d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
+                .run(stream_, "batch down GEMV");
+        }
+    }
+
+    void enqueue_predictor(Session** s, int n, const std::vector<SamplingParams>& ps) {
+        const int H = cfg_.talker.hidden, PH = cfg_.predictor.hidden, PV = cfg_.predictor_vocab;
+        const int mode = batch_gemv_mode();
+        bf16_t* input = text_input_.as<bf16_t>();
+        for (int p = 0; p < kCodebooks; ++p) {
+            if (p == 0) {
+                check_hip(launch_gather_rows(reinterpret_cast<const bf16_t* const*>(last_hidden_ptrs()), n, H, input, stream_),
+                          "gather last hidden");
+            } else if (p == 1) {
+                check_hip(launch_gather_embedding_rows(m_.codec_embedding_, cfg_.talker_vocab, H, token_bases(), 0, input, n, stream_),
+                          "gather semantic embedding");
+            } else {
+                check_hip(launch_gather_embedding_rows(m_.predictor_embeddings_[p - 2], PV, H, token_bases(), p - 1, input, n, stream_),
+                          "gather residual embedding");
+            }
+            Gemv(m_.small_to_mtp_, input, H, PH, kEpiBias).bias(m_.small_to_mtp_bias_).rows(n, mode)
+                .to(p_hidden_.as<bf16_t>()).run(stream_, "batch small_to_mtp");
+            run_decoder(true, n, positions(p), kCodebooks);
+            if (p >= 1) {
+                Gemv(m_.predictor_heads_[p - 1], p_hidden_.as<bf16_t>(), PH, PV, kEpiStore).norm(m_.predictor_norm_, cfg_.eps)
+                    .rows(n, mode).to(logits_.as<bf16_t>()).run(stream_, "batch predictor head");
+                for (int i = 0; i < n; ++i) {
+                    Session* c = s[i];
+                    check_hip(launch_sample_logits_ex(logits_.as<bf16_t>() + static_cast<size_t>(i) * PV, PV, false,
+                                                      cfg_.codec_eos, c->history_.as<int>(), c->history_count_ptr(), 0,
+                                                      ps[i].do_sample, ps[i].top_k, ps[i].top_p, ps[i].temperature,
+                                                      ps[i].penalty, c->random_state_.as<uint64_t>(), c->sampled_ptr(),
+                                                      c->frame_tokens(), nullptr, p, nullptr, nullptr, stream_),
+                              "batch predictor sample");
+                }
+            }
+        }
+        for (int i = 0; i < n; ++i) {
+            check_hip(launch_pack_frame_codes(s[i]->frame_tokens(), s[i]->codes_.as<uint16_t>(), kCodebooks, stream_),
+                      "pack frame codes");
+        }
+    }
+
+    void enqueue_talker(Session** s, int n, const std::vector<SamplingParams>& ts) {
+        const int H = cfg_.talker.hidden, TV = cfg_.talker_vocab;
+        const int mode = batch_gemv_mode();
+        int max_capacity = kCodebooks;
+        for (int i = 0; i < n; ++i) max_capacity = std::max(max_capacity, s[i]->max_seq_);
+        check_hip(launch_sum_embeddings_rows(m_.embedding_tables_.as<const bf16_t*>(), kCodebooks, TV, cfg_.predictor_vocab, H,
+                                             token_bases(), hidden_.as<bf16_t>(), n, stream_),
+                  "batch codec embeddings");
+        check_hip(launch_gather_embedding_rows(m_.text_embedding_, cfg_.text_vocab, H, trailing_ptrs(), 0,
+                                               text_input_.as<bf16_t>(), n, stream_),
+                  "gather text embedding");
+        Gemv(m_.text_fc1_, text_input_.as<bf16_t>(), H, H, kEpiBiasSilu).bias(m_.text_fc1_bias_).rows(n, mode)
+            .to(proj_.as<bf16_t>()).run(stream_, "batch text fc1");
+        Gemv(m_.text_fc2_, proj_.as<bf16_t>(), H, H, kEpiBiasAdd).bias(m_.text_fc2_bias_).rows(n, mode)
+            .to(hidden_.as<bf16_t>()).run(stream_, "batch text fc2");
+        run_decoder(false, n, positions(kCodebooks), max_capacity);
+        check_hip(launch_rms_norm_rows(hidden_.as<bf16_t>(), m_.talker_norm_, normalized_.as<bf16_t>(), n, H, cfg_.eps, stream_),
+                  "batch talker final norm");
+        check_hip(launch_scatter_rows(normalized_.as<bf16_t>(), last_hidden_ptrs(), n, H, stream_), "scatter last hidden");
+        Gemv(m_.codec_head_, normalized_.as<bf16_t>(), H, TV, kEpiStore).rows(n, mode).to(logits_.as<bf16_t>())
+            .run(stream_, "batch codec head");
+        for (int i = 0; i < n; ++i) {
+            Session* c = s[i];
+            check_hip(launch_sample_logits_ex(logits_.as<bf16_t>() + static_cast<size_t>(i) * TV, TV, true, cfg_.codec_eos,
+                                              c->history_.as<int>(), c->history_count_ptr(), 0, ts[i].do_sample,
+                                              ts[i].top_k, ts[i].top_p, ts[i].temperature, ts[i].penalty,
+                                              c->random_state_.as<uint64_t>(), c->sampled_ptr(), c->frame_tokens(),
+                                              nullptr, 0, c->history_.as<int>(), c->history_count_ptr(), stream_),
+                      "batch talker sample");
+        }
+        check_hip(launch_increment_each(position_ptrs(), n, stream_), "advance positions");
+    }
+
+    Model& m_;
+    Config cfg_;
+    int device_;
+    int layers_ = 0;
+    hipStream_t stream_ = nullptr;
+    std::array<hipEvent_t, kCapacity> join_{};
+    DeviceBuffer hidden_, normalized_, p_hidden_, text_input_, proj_, qkv_, attn_, act_, logits_, tables_;
+    size_t table_bytes_ = 0;
+    void* pinned_ = nullptr;
+    hipGraphExec_t predictor_graph_ = nullptr, talker_graph_ = nullptr;
+    int uncaptured_ = 0;
+    std::vector<uint64_t> key_;
+};
+
+void delete_batch_runner(BatchRunner* r) { delete r; }
+
+void batch_begin_frames(Model* model, Session** s, int n, const int* trailing,
+                        const Qwen3TtsSamplingConfig* ts, const Qwen3TtsSamplingConfig* ps,
+                        Qwen3TtsDeviceFrameViewV2* views) {
+    if (model == nullptr || s == nullptr || n <= 0 || n > kMaxBatch) {
+        throw std::invalid_argument("invalid batch frame arguments");
+    }
+    if (!model->finalized()) throw std::runtime_error("model weights must be finalized");
+    std::lock_guard<std::mutex> lock(model->batch_mutex());
+    if (!model->batch_) {
+        model->batch_ = std::unique_ptr<BatchRunner, void (*)(BatchRunner*)>(new BatchRunner(*model), delete_batch_runner);
+    }
+    model->batch_->begin(s, n, trailing, ts, ps, views);
 }
 
 }  // namespace

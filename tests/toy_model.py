@@ -118,7 +118,7 @@ class OrcModel(C.Structure):
                 ("small_to_mtp", C.c_void_p), ("small_to_mtp_s", C.c_void_p),
                 ("small_to_mtp_bias", C.c_void_p), ("predictor_norm", C.c_void_p),
                 ("predictor_embeddings", C.c_void_p), ("predictor_heads", C.c_void_p),
-                ("predictor_heads_s", C.c_void_p)]
+                ("predictor_heads_s", C.c_void_p), ("batch_semantics", C.c_int)]
 
 
 class OrcSession(C.Structure):
@@ -140,7 +140,7 @@ def _ptr(a):
 class OracleModel:
     """Host-side int8 model for the oracle (keeps every buffer alive)."""
 
-    def __init__(self, orc, c: dict, weights: dict):
+    def __init__(self, orc, c: dict, weights: dict, batch_semantics: bool = False):
         self.orc, self.c, self.keep = orc, c, []
         q = {}
 
@@ -203,6 +203,7 @@ class OracleModel:
         self.keep += [embs, heads, heads_s, weights]
         m.predictor_embeddings, m.predictor_heads, m.predictor_heads_s = (
             C.addressof(embs), C.addressof(heads), C.addressof(heads_s))
+        m.batch_semantics = int(batch_semantics)
         self.model = m
         lib = orc.lib()
         lib.orc_frame_step.restype = C.c_int
