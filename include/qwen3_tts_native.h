@@ -437,13 +437,14 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     int32_t mode;
     int32_t warmup;
     int32_t steps;
-    int32_t use_graph;
+    int32_t use_graph;     /* 0 eager launches, 1 hipGraph per step, 2 persistent chain kernel */
     int32_t kernel_filter; /* 0 whole chain; 1 QKV, 2 O, 3 gate/up, 4 down GEMVs only */
     uint64_t weight_bytes;
     uint64_t algorithmic_bytes_per_step;
     double total_milliseconds;
     double milliseconds_per_step;
     double gemv_kernel_milliseconds_per_step;
+    uint64_t output_checksum; /* FNV-1a of the final hidden, qkv and activation rows */
 } Qwen3TtsStepBenchmarkV1;
 QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(
     int32_t device_index, Qwen3TtsStepBenchmarkV1* inout, char* error, size_t error_capacity);

@@ -3,6 +3,7 @@
 // hipEvents on one stream; inputs are synthetic and generated on the device.
 #include "q3_common.hpp"
 
+
 #include "../../include/qwen3_tts_native.h"
 
 #include <algorithm>
@@ -173,6 +174,7 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         check_hip(launch_fill_bf16_normal(gains, 2ull * H, 0x5EED0013ULL, 1.0f, 0.1f, stream), "fill gains");
         check_hip(launch_fill_bf16_normal(hidden, static_cast<uint64_t>(R) * H, 0x5EED0014ULL, 0.0f, 1.0f, stream), "fill x");
         check_hip(launch_fill_bf16_normal(qkv, static_cast<uint64_t>(R) * qkv_rows, 0x5EED0015ULL, 0.0f, 1.0f, stream), "fill q");
+        check_hip(launch_fill_bf16_normal(act, static_cast<uint64_t>(R) * I, 0x5EED0016ULL, 0.0f, 1.0f, stream), "fill act");
         const int mode = b->mode;
         const int filter = b->kernel_filter;
         // QKV output has the full fused row; O reads the q part with row
@@ -224,7 +226,48 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                 }
             }
         };
-        if (b->use_graph) {
+        // Persistent chain: the same GEMVs as one op list.
+        const int workgroups = chain_workgroups();
+        ChainOp* d_ops = nullptr;
+        unsigned* d_sync = nullptr;
+        int op_count = 0;
+        if (b->use_graph == 2) {
+            if (R != 1) throw std::invalid_argument("the persistent chain serves batch 1");
+            std::vector<ChainOp> ops;
+            for (int l = 0; l < L; ++l) {
+                int8_t* base = w + per_layer * l;
+                float* sb = s + scales_per_layer * l;
+                const int8_t* wqkv = base;
+                const int8_t* wo = wqkv + qkv_rows * H;
+                const int8_t* wgu = wo + static_cast<size_t>(H) * QW;
+                const int8_t* wd = wgu + 2ull * I * H;
+                auto add = [&](const int8_t* wt, const float* sc, const bf16_t* in, const bf16_t* norm, bf16_t* out,
+                               int in_f, int out_f, int epi) {
+                    ChainOp op{};
+                    op.kind = chain_kind_for(in_f, out_f, epi, workgroups);
+                    if (op.kind < 0) throw std::invalid_argument("GEMV shape not supported by the persistent chain");
+                    op.epilogue = epi;
+                    op.in_features = in_f;
+                    op.out_features = out_f;
+                    op.weight = wt;
+                    op.scales = sc;
+                    op.input = in;
+                    op.norm_weight = norm;
+                    op.out16 = out;
+                    op.norm_epsilon = 1.0e-6f;
+                    ops.push_back(op);
+                };
+                if (filter == 0 || filter == 1) add(wqkv, sb, hidden, gains, qkv, H, static_cast<int>(qkv_rows), kEpiStore);
+                if (filter == 0 || filter == 2) add(wo, sb + qkv_rows, qkv, nullptr, hidden, QW, H, kEpiAddRounded);
+                if (filter == 0 || filter == 3) add(wgu, sb + qkv_rows + H, hidden, gains + H, act, H, I, kEpiSiluRounded);
+                if (filter == 0 || filter == 4) add(wd, sb + qkv_rows + H + 2 * I, act, nullptr, hidden, I, H, kEpiAddRounded);
+            }
+            op_count = static_cast<int>(ops.size());
+            d_ops = mem.get<ChainOp>(ops.size());
+            d_sync = mem.get<unsigned>(4);
+            check_hip(hipMemcpy(d_ops, ops.data(), ops.size() * sizeof(ChainOp), hipMemcpyHostToDevice), "upload ops");
+        }
+        if (b->use_graph == 1) {
             check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             enqueue_step();
             hipGraph_t graph = nullptr;
@@ -234,7 +277,9 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             check_hip(st, "hipGraphInstantiate");
         }
         auto run = [&] {
-            if (exec) {
+            if (d_ops) {
+                check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream), "persistent chain");
+            } else if (exec) {
                 check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
             } else {
                 enqueue_step();
@@ -273,6 +318,25 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         b->total_milliseconds = ms;
         b->milliseconds_per_step = ms / b->steps;
         b->gemv_kernel_milliseconds_per_step = ms / b->steps;
+        if (d_sync) {
+            int status = 0;
+            check_hip(hipMemcpy(&status, d_sync + 1, sizeof(int), hipMemcpyDeviceToHost), "read chain status");
+            if (status != 0) throw DeviceFailure("persistent chain: a grid barrier wait timed out");
+        }
+        {
+            uint64_t h = 1469598103934665603ULL;
+            for (auto [ptr, count] : {std::make_pair(hidden, static_cast<size_t>(R) * H),
+                                      std::make_pair(qkv, static_cast<size_t>(R) * qkv_rows),
+                                      std::make_pair(act, static_cast<size_t>(R) * I)}) {
+                std::vector<bf16_t> out(count);
+                check_hip(hipMemcpy(out.data(), ptr, count * sizeof(bf16_t), hipMemcpyDeviceToHost), "read outputs");
+                for (bf16_t v : out) {
+                    h ^= v;
+                    h *= 1099511628211ULL;
+                }
+            }
+            b->output_checksum = h;
+        }
         if (exec) (void)hipGraphExecDestroy(exec);
         (void)hipEventDestroy(start);
         (void)hipEventDestroy(stop);

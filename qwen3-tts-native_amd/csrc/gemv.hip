@@ -24,163 +24,12 @@
 // MFMA mode (rows 2..8): weights are dequantized int8 -> bf16 (exact) in
 // registers and fed to v_mfma_f32_16x16x32_bf16 with the session rows padded
 // to 16; the per-channel scale is applied after accumulation.
-#include "q3_common.hpp"
-#include "q3_math.h"
+#include "gemv_device.hpp"
 
 namespace q3 {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kHalfWaves = kThreads / 32;
-
-__device__ __forceinline__ float byte_f(int word, int b) {
-    return static_cast<float>(static_cast<int8_t>(word >> (8 * b)));
-}
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Streaming 128-bit weight load (nontemporal: weights are read once per step).
-__device__ __forceinline__ int4 stream_load(const void* p) {
-    const i32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p));
-    return make_int4(v.x, v.y, v.z, v.w);
-}
-
-// Reference 32-lane shuffle-down fold, offsets 16..1 (int8_gemv.cu:114-118).
-__device__ __forceinline__ float fold32(float value) {
-#pragma unroll
-    for (int offset = 16; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 32);
-    }
-    return value;
-}
-
-// inv_rms of x[0..width) with the exact 256-thread tree of the reference's
-// block_sum (talker_kernels.cu:14-25,36-41), computed by one wave64.
-__device__ float wave_inverse_rms(const bf16_t* x, int width, float epsilon) {
-    const int lane = threadIdx.x & 63;
-    float part[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float s = 0.0f;
-        for (int i = lane + 64 * j; i < width; i += 256) {
-            const float v = bf2f(x[i]);
-            s = fmaf(v, v, s);
-        }
-        part[j] = s;
-    }
-    part[0] += part[2];
-    part[1] += part[3];
-    float value = part[0] + part[1];
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 64);
-    }
-    const float total = __shfl(value, 0, 64);
-    return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
-}
-
-__device__ __forceinline__ float normalize_one(float x, float inverse, float gain) {
-    return round_bf(round_bf(x * inverse) * gain);
-}
-
-// Load the 16 activations of vector `v` (bf16) as fp32, normalized if needed.
-template <bool kNorm>
-__device__ __forceinline__ void load_x16(const bf16_t* x, const bf16_t* gain, int v,
-                                         float inverse, float* out) {
-    const uint4* p = reinterpret_cast<const uint4*>(x + static_cast<size_t>(v) * 16);
-    const uint4 a = p[0];
-    const uint4 b = p[1];
-    const uint32_t words[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        out[2 * i] = __uint_as_float(words[i] << 16);
-        out[2 * i + 1] = __uint_as_float(words[i] & 0xffff0000u);
-    }
-    if constexpr (kNorm) {
-        const uint4* g = reinterpret_cast<const uint4*>(gain + static_cast<size_t>(v) * 16);
-        const uint4 ga = g[0];
-        const uint4 gb = g[1];
-        const uint32_t gw[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            out[2 * i] = normalize_one(out[2 * i], inverse, __uint_as_float(gw[i] << 16));
-            out[2 * i + 1] =
-                normalize_one(out[2 * i + 1], inverse, __uint_as_float(gw[i] & 0xffff0000u));
-        }
-    }
-}
-
-// One 16-byte weight vector against 16 fp32 activations: the reference's
-// fresh fmaf chain (int8_gemv.cu:99-112).
-__device__ __forceinline__ float chain16(const int4 w, const float* x) {
-    const int words[4] = {w.x, w.y, w.z, w.w};
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            sum = fmaf(byte_f(words[i], b), x[4 * i + b], sum);
-        }
-    }
-    return sum;
-}
-
-// Packed-activation variant: x as 8 words of bf16 pairs.
-__device__ __forceinline__ float chain16_packed(const int4 w, const uint32_t* xp) {
-    const int words[4] = {w.x, w.y, w.z, w.w};
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const uint32_t pair = xp[(4 * i + b) >> 1];
-            const float xv = ((b & 1) == 0) ? __uint_as_float(pair << 16)
-                                            : __uint_as_float(pair & 0xffff0000u);
-            sum = fmaf(byte_f(words[i], b), xv, sum);
-        }
-    }
-    return sum;
-}
-
-// Half-wave lane 0 epilogue for the plain / residual epilogues.
-template <int kEpi>
-__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
-    const float scale = a.scales[channel];
-    if constexpr (kEpi == kEpiStore) {
-        const float y = value * scale;
-        if (a.out32 != nullptr) a.out32[channel] = y;
-        if (a.out16 != nullptr) a.out16[channel] = f2bf(y);
-    } else if constexpr (kEpi == kEpiAddFma) {
-        a.out16[channel] = f2bf(fmaf(value, scale, bf2f(a.out16[channel])));
-    } else if constexpr (kEpi == kEpiAddRounded) {
-        const float projected = round_bf(value * scale);
-        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
-    } else if constexpr (kEpi == kEpiBias) {
-        a.out16[channel] = f2bf(round_bf(value * scale) + bf2f(a.bias[channel]));
-    } else if constexpr (kEpi == kEpiBiasSilu) {
-        float v = round_bf(value * scale) + bf2f(a.bias[channel]);
-        v *= 1.0f / (1.0f + q3_expf(-v));
-        a.out16[channel] = f2bf(v);
-    } else if constexpr (kEpi == kEpiBiasAdd) {
-        const float projected = round_bf(round_bf(value * scale) + bf2f(a.bias[channel]));
-        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
-    }
-}
-
-template <int kEpi>
-__device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
-    const float gate = g * a.scales[channel];
-    const float up = u * a.scales[a.out_features + channel];
-    if constexpr (kEpi == kEpiSiluFused) {
-        const float activated = gate / (1.0f + q3_expf(-gate));
-        a.out16[channel] = f2bf(activated * up);
-    } else {
-        const float gate16 = round_bf(gate);
-        const float up16 = round_bf(up);
-        const float activated = round_bf(gate16 / (1.0f + q3_expf(-gate16)));
-        a.out16[channel] = f2bf(activated * up16);
-    }
-}
+using namespace gemv_detail;
 
 // ---------------------------------------------------------------------------
 // Exact-order GEMV, one activation row, K = kVpl * 512 known at compile time.

@@ -199,6 +199,26 @@ hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int voc
                                  int vocabulary, int width, const int* tokens, bf16_t* output,
                                  hipStream_t stream);
 
+// Persistent GEMV chain (persistent.hip): one op per dependent GEMV.
+struct ChainOp {
+    int kind;  // chosen by chain_kind_for
+    int epilogue;
+    int in_features;
+    int out_features;
+    const int8_t* weight;
+    const float* scales;
+    const bf16_t* input;
+    const bf16_t* norm_weight;
+    const bf16_t* bias;
+    bf16_t* out16;
+    float norm_epsilon;
+    int reserved;
+};
+int chain_kind_for(int in_features, int out_features, int epilogue, int workgroups);
+int chain_workgroups();
+hipError_t launch_persistent_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups,
+                                   hipStream_t stream);
+
 // Lockstep-batch glue: rows of a batch from / to per-session buffers.
 hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,
                               hipStream_t stream);

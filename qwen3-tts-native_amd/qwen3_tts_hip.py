@@ -138,7 +138,7 @@ class StepBenchmarkV1(C.Structure):
             "warmup", "steps", "use_graph", "kernel_filter")] + [
         ("weight_bytes", C.c_uint64), ("algorithmic_bytes_per_step", C.c_uint64),
         ("total_milliseconds", C.c_double), ("milliseconds_per_step", C.c_double),
-        ("gemv_kernel_milliseconds_per_step", C.c_double)]
+        ("gemv_kernel_milliseconds_per_step", C.c_double), ("output_checksum", C.c_uint64)]
 
 
 # Layouts pinned by the reference's Rust FFI test (native_talker.rs:1734-1744).

@@ -1,0 +1,33 @@
+"""The persistent GEMV chain kernel (one cooperative launch per talker step,
+grid barriers between dependent GEMVs, next-GEMV weights prefetched before
+each barrier) must produce bit-identical hidden states to the same chain run
+as one kernel launch per GEMV."""
+import ctypes as C
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def run(hip, use_graph, layers, steps=1, warmup=0, kernel_filter=0):
+    b = hip.StepBenchmarkV1()
+    b.struct_size = C.sizeof(hip.StepBenchmarkV1)
+    b.layers, b.hidden, b.intermediate, b.query_width, b.key_value_width = layers, 2048, 6144, 2048, 1024
+    b.rows, b.mode, b.warmup, b.steps, b.use_graph, b.kernel_filter = 1, 1, warmup, steps, use_graph, kernel_filter
+    hip.call("qwen3_tts_benchmark_talker_step_gemvs", 0, C.byref(b))
+    return b
+
+
+@pytest.mark.parametrize("layers,steps", [(1, 1), (2, 1), (28, 2)])
+def test_persistent_chain_bit_identical(hip, layers, steps):
+    eager = run(hip, 0, layers, steps=steps)
+    persistent = run(hip, 2, layers, steps=steps)
+    assert persistent.output_checksum == eager.output_checksum
+    assert persistent.algorithmic_bytes_per_step == eager.algorithmic_bytes_per_step
+
+
+@pytest.mark.parametrize("kernel_filter", [1, 2, 3, 4])
+def test_persistent_single_kind_chains(hip, kernel_filter):
+    eager = run(hip, 0, 3, kernel_filter=kernel_filter)
+    persistent = run(hip, 2, 3, kernel_filter=kernel_filter)
+    assert persistent.output_checksum == eager.output_checksum
