@@ -446,6 +446,13 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     double gemv_kernel_milliseconds_per_step;
     uint64_t output_checksum; /* FNV-1a of the final hidden, qkv and activation rows */
 } Qwen3TtsStepBenchmarkV1;
+/* Diagnostic: device time per grid barrier of the persistent chain kernel's
+ * barrier variants (0: agent fences + relaxed atomics; 1: no fences;
+ * 2: release/acquire atomics; 3: no sleep in the poll; 4: variant 0 + a 4 KB
+ * re-read after each barrier).  workgroups <= 0 uses one per CU. */
+QWEN3_TTS_API int32_t qwen3_tts_benchmark_grid_barrier(
+    int32_t device_index, int32_t variant, int32_t barriers, int32_t workgroups,
+    double* microseconds_per_barrier, char* error, size_t error_capacity);
 QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(
     int32_t device_index, Qwen3TtsStepBenchmarkV1* inout, char* error, size_t error_capacity);
 

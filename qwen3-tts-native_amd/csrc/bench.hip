@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -264,7 +265,7 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             }
             op_count = static_cast<int>(ops.size());
             d_ops = mem.get<ChainOp>(ops.size());
-            d_sync = mem.get<unsigned>(4);
+            d_sync = mem.get<unsigned>(kChainSyncWords);
             check_hip(hipMemcpy(d_ops, ops.data(), ops.size() * sizeof(ChainOp), hipMemcpyHostToDevice), "upload ops");
         }
         if (b->use_graph == 1) {
@@ -276,9 +277,13 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             (void)hipGraphDestroy(graph);
             check_hip(st, "hipGraphInstantiate");
         }
+        // QWEN3_TTS_CHAIN_TRACE=<file>: phase timestamps of workgroup 0 of the
+        // last persistent launch, written as text (diagnostics).
+        const char* trace_path = std::getenv("QWEN3_TTS_CHAIN_TRACE");
+        unsigned long long* d_trace = (d_ops && trace_path) ? mem.get<unsigned long long>(256 * 8) : nullptr;
         auto run = [&] {
             if (d_ops) {
-                check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream), "persistent chain");
+                check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "persistent chain");
             } else if (exec) {
                 check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
             } else {
@@ -318,6 +323,18 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         b->total_milliseconds = ms;
         b->milliseconds_per_step = ms / b->steps;
         b->gemv_kernel_milliseconds_per_step = ms / b->steps;
+        if (d_trace) {
+            std::vector<unsigned long long> t(256 * 8);
+            check_hip(hipMemcpy(t.data(), d_trace, t.size() * 8, hipMemcpyDeviceToHost), "read trace");
+            if (FILE* f = std::fopen(trace_path, "w")) {
+                for (int i = 0; i < std::min(op_count, 256); ++i) {
+                    std::fprintf(f, "%d", i);
+                    for (int p = 0; p < 6; ++p) std::fprintf(f, " %llu", t[i * 8 + p]);
+                    std::fprintf(f, "\n");
+                }
+                std::fclose(f);
+            }
+        }
         if (d_sync) {
             int status = 0;
             check_hip(hipMemcpy(&status, d_sync + 1, sizeof(int), hipMemcpyDeviceToHost), "read chain status");

@@ -125,43 +125,65 @@ __device__ __forceinline__ float chain16_packed(const int4 w, const uint32_t* xp
     return sum;
 }
 
-// Half-wave lane 0 epilogue for the plain / residual epilogues.
-template <int kEpi>
-__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
-    const float scale = a.scales[channel];
-    if constexpr (kEpi == kEpiStore) {
-        const float y = value * scale;
-        if (a.out32 != nullptr) a.out32[channel] = y;
-        if (a.out16 != nullptr) a.out16[channel] = f2bf(y);
-    } else if constexpr (kEpi == kEpiAddFma) {
-        a.out16[channel] = f2bf(fmaf(value, scale, bf2f(a.out16[channel])));
-    } else if constexpr (kEpi == kEpiAddRounded) {
-        const float projected = round_bf(value * scale);
-        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
-    } else if constexpr (kEpi == kEpiBias) {
-        a.out16[channel] = f2bf(round_bf(value * scale) + bf2f(a.bias[channel]));
-    } else if constexpr (kEpi == kEpiBiasSilu) {
-        float v = round_bf(value * scale) + bf2f(a.bias[channel]);
-        v *= 1.0f / (1.0f + q3_expf(-v));
-        a.out16[channel] = f2bf(v);
-    } else if constexpr (kEpi == kEpiBiasAdd) {
-        const float projected = round_bf(round_bf(value * scale) + bf2f(a.bias[channel]));
-        a.out16[channel] = f2bf(bf2f(a.out16[channel]) + projected);
+// bf16 output access.  kCoherent: agent-scope relaxed atomics (device-
+// coherent loads/stores that bypass the non-coherent caches), used when other
+// workgroups of a persistent grid read the value after a grid barrier.
+template <bool kCoherent>
+__device__ __forceinline__ float load_out(const bf16_t* p) {
+    if constexpr (kCoherent) {
+        return bf2f(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    } else {
+        return bf2f(*p);
     }
 }
 
-template <int kEpi>
+template <bool kCoherent>
+__device__ __forceinline__ void store_out(bf16_t* p, bf16_t v) {
+    if constexpr (kCoherent) {
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *p = v;
+    }
+}
+
+// Half-wave lane 0 epilogue for the plain / residual epilogues.
+template <int kEpi, bool kCoherent = false>
+__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
+    const float scale = a.scales[channel];
+    bf16_t* out = a.out16 + channel;
+    if constexpr (kEpi == kEpiStore) {
+        const float y = value * scale;
+        if (a.out32 != nullptr) a.out32[channel] = y;
+        if (a.out16 != nullptr) store_out<kCoherent>(out, f2bf(y));
+    } else if constexpr (kEpi == kEpiAddFma) {
+        store_out<kCoherent>(out, f2bf(fmaf(value, scale, load_out<kCoherent>(out))));
+    } else if constexpr (kEpi == kEpiAddRounded) {
+        const float projected = round_bf(value * scale);
+        store_out<kCoherent>(out, f2bf(load_out<kCoherent>(out) + projected));
+    } else if constexpr (kEpi == kEpiBias) {
+        store_out<kCoherent>(out, f2bf(round_bf(value * scale) + bf2f(a.bias[channel])));
+    } else if constexpr (kEpi == kEpiBiasSilu) {
+        float v = round_bf(value * scale) + bf2f(a.bias[channel]);
+        v *= 1.0f / (1.0f + q3_expf(-v));
+        store_out<kCoherent>(out, f2bf(v));
+    } else if constexpr (kEpi == kEpiBiasAdd) {
+        const float projected = round_bf(round_bf(value * scale) + bf2f(a.bias[channel]));
+        store_out<kCoherent>(out, f2bf(load_out<kCoherent>(out) + projected));
+    }
+}
+
+template <int kEpi, bool kCoherent = false>
 __device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
     const float gate = g * a.scales[channel];
     const float up = u * a.scales[a.out_features + channel];
     if constexpr (kEpi == kEpiSiluFused) {
         const float activated = gate / (1.0f + q3_expf(-gate));
-        a.out16[channel] = f2bf(activated * up);
+        store_out<kCoherent>(a.out16 + channel, f2bf(activated * up));
     } else {
         const float gate16 = round_bf(gate);
         const float up16 = round_bf(up);
         const float activated = round_bf(gate16 / (1.0f + q3_expf(-gate16)));
-        a.out16[channel] = f2bf(activated * up16);
+        store_out<kCoherent>(a.out16 + channel, f2bf(activated * up16));
     }
 }
 

@@ -17,6 +17,8 @@
 
 #include "../../include/qwen3_tts_native.h"
 
+#include <cstdio>
+
 namespace q3 {
 
 
@@ -36,37 +38,62 @@ constexpr int kTileSlots = 24;  // int4 weight registers per lane
 constexpr int kMaxIn = 6144;
 
 struct ChainState {
-    unsigned* barrier;  // zeroed before the launch
-    int* status;        // set to 1 if a barrier wait timed out
+    unsigned* barrier;             // zeroed before the launch
+    int* status;                   // set to 1 if a barrier wait timed out
+    unsigned long long* trace;     // optional: phase timestamps of workgroup 0
 };
 
-// Grid-wide barrier with a bounded wait: monotone counter, target =
-// (index + 1) * gridDim.x.  Agent-scope release before arriving and acquire
-// after observing the target make every workgroup's stores visible to every
-// other XCD.  A wait that exceeds ~1 s records an error and lets the grid
-// drain instead of hanging.
-__device__ void grid_barrier(const ChainState& st, unsigned index) {
-    __syncthreads();
+// Phase timestamps (100 MHz wall clock) of workgroup 0, op i, phase p.
+__device__ __forceinline__ void trace_phase(const ChainState& st, int op, int phase) {
+    if (st.trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && op < 256) {
+        st.trace[op * 8 + phase] = wall_clock64();
+    }
+}
+
+// Grid-wide barrier with a bounded wait.  Two levels: workgroup b arrives on
+// the counter of group b % 8 (one group per XCD under round-robin dispatch);
+// the last arriver of a group arrives on the global counter, which everyone
+// polls.  Counters are monotone within a launch (barrier i completes at
+// (i + 1) * members).  No cache fences are needed: activations travel only
+// through device-coherent (agent-scope atomic) loads and stores, and
+// __syncthreads orders each workgroup's stores before its arrival.  A wait
+// longer than ~1 s records an error and every later barrier stops waiting,
+// so the grid always drains.
+constexpr int kGroups = 8;
+constexpr int kLineWords = 32;  // 128-byte spacing between counters
+
+// Split-phase barrier: arrive as soon as this workgroup's outputs are
+// stored, do independent work (issue the next GEMV's weight loads), then wait.
+__device__ void grid_arrive(const ChainState& st, unsigned index) {
+    __syncthreads();  // every wave's stores of this op have completed
     if (threadIdx.x == 0) {
-        const unsigned target = (index + 1) * gridDim.x;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __hip_atomic_fetch_add(st.barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned g = blockIdx.x % kGroups;
+        const unsigned members = (gridDim.x - g + kGroups - 1) / kGroups;
+        unsigned* group = st.barrier + kLineWords * (1 + g);
+        const unsigned old = __hip_atomic_fetch_add(group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1 == (index + 1) * members) {
+            __hip_atomic_fetch_add(st.barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+__device__ void grid_wait(const ChainState& st, unsigned index) {
+    if (threadIdx.x == 0) {
+        const unsigned groups = gridDim.x < kGroups ? gridDim.x : kGroups;
+        const unsigned target = (index + 1) * groups;
         unsigned spins = 0;
         while (__hip_atomic_load(st.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(1);
             ++spins;
-            // after one timeout every later barrier stops waiting, so the
-            // grid always drains
             if ((spins & 1023u) == 0 &&
                 __hip_atomic_load(st.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
                 break;
             }
-            if (spins > (1u << 24)) {
+            if (spins > (1u << 25)) {
                 __hip_atomic_store(st.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
 }
@@ -162,9 +189,9 @@ __device__ void compute_tiles(const ChainOp& op, const int4 (&tile)[kTileSlots],
         }
         if (lane == 0) {
             if constexpr (kRowsPerUnit == 2) {
-                store_gate_up<kEpi>(a, unit, acc[0], acc[1]);
+                store_gate_up<kEpi, true>(a, unit, acc[0], acc[1]);
             } else {
-                store_channel<kEpi>(a, unit, acc[0]);
+                store_channel<kEpi, true>(a, unit, acc[0]);
             }
         }
     }
@@ -196,24 +223,56 @@ __global__ __launch_bounds__(kThreads, 1) void persistent_chain_kernel(const Cha
                                                                        ChainState st) {
     __shared__ uint4 x_lds[kMaxIn * 2 / 16];
     __shared__ uint4 g_lds[kMaxIn * 2 / 16];
+    __shared__ float partial_lds[kThreads];
     __shared__ float inverse_lds;
     int4 tile[kTileSlots];
     if (count > 0) issue(ops[0], tile);
     for (int i = 0; i < count; ++i) {
+        trace_phase(st, i, 0);
         const ChainOp op = ops[i];
         const int chunks = op.in_features * 2 / 16;
         for (int c = threadIdx.x; c < chunks; c += kThreads) {
-            x_lds[c] = reinterpret_cast<const uint4*>(op.input)[c];
+            // the activation was written by other workgroups: device-coherent loads
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(op.input) + 4 * c;
+            uint4 v;
+            v.x = __hip_atomic_load(src + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v.y = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v.z = __hip_atomic_load(src + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v.w = __hip_atomic_load(src + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x_lds[c] = v;
             if (op.norm_weight != nullptr) g_lds[c] = reinterpret_cast<const uint4*>(op.norm_weight)[c];
         }
         __syncthreads();
+        trace_phase(st, i, 1);
         const bf16_t* xs = reinterpret_cast<const bf16_t*>(x_lds);
         const bf16_t* gs = reinterpret_cast<const bf16_t*>(g_lds);
-        if (op.norm_weight != nullptr && threadIdx.x < 64) {
-            const float inv = wave_inverse_rms(xs, op.in_features, op.norm_epsilon);
-            if (threadIdx.x == 0) inverse_lds = inv;
+        if (op.norm_weight != nullptr) {
+            // RMSNorm statistic with the reference's 256-thread order
+            // (talker_kernels.cu:36-41): thread t sums x[t], x[t+256], ...;
+            // then the block tree, folded by wave 0 exactly as wave_tree256.
+            const bf16_t* xl = reinterpret_cast<const bf16_t*>(x_lds);
+            float sq = 0.0f;
+            for (int k = threadIdx.x; k < op.in_features; k += kThreads) {
+                const float v = bf2f(xl[k]);
+                sq = fmaf(v, v, sq);
+            }
+            partial_lds[threadIdx.x] = sq;
+            __syncthreads();
+            if (threadIdx.x < 64) {
+                float p0 = partial_lds[threadIdx.x], p1 = partial_lds[threadIdx.x + 64];
+                const float p2 = partial_lds[threadIdx.x + 128], p3 = partial_lds[threadIdx.x + 192];
+                p0 += p2;
+                p1 += p3;
+                float value = p0 + p1;
+#pragma unroll
+                for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_down(value, offset, 64);
+                if (threadIdx.x == 0) {
+                    inverse_lds = 1.0f / sqrtf(value / static_cast<float>(op.in_features) + op.norm_epsilon);
+                }
+            }
         }
         __syncthreads();
+        trace_phase(st, i, 2);
         const float inverse = inverse_lds;
         switch (op.kind) {
             case kChainK2048U2: compute_dispatch<4, 2, 1>(op, tile, xs, gs, inverse); break;
@@ -222,8 +281,14 @@ __global__ __launch_bounds__(kThreads, 1) void persistent_chain_kernel(const Cha
             case kChainK6144U1: compute_dispatch<12, 1, 1>(op, tile, xs, gs, inverse); break;
             default: break;
         }
-        if (i + 1 < count) issue(ops[i + 1], tile);
-        grid_barrier(st, static_cast<unsigned>(i));
+        trace_phase(st, i, 3);
+        if (i + 1 < count) {
+            grid_arrive(st, static_cast<unsigned>(i));
+            issue(ops[i + 1], tile);
+            trace_phase(st, i, 4);
+            grid_wait(st, static_cast<unsigned>(i));
+        }
+        trace_phase(st, i, 5);
     }
 }
 
@@ -234,7 +299,121 @@ __global__ void zero_sync_kernel(unsigned* barrier, int* status) {
     }
 }
 
+// Zeroes a larger synchronization area (counters, group counters, flags).
+__global__ void zero_words_kernel(unsigned* words, int count) {
+    for (int i = threadIdx.x; i < count; i += blockDim.x) words[i] = 0u;
+}
+
+// Barrier cost probe: `count` barriers, no work.  variant 0: agent fences +
+// relaxed atomics (the chain's barrier); 1: relaxed atomics without fences;
+// 2: release add / acquire poll; 3: variant 0 polling without sleep;
+// 4: variant 0 plus a 4 KB activation re-read after each barrier.
+template <int kVariant>
+__global__ __launch_bounds__(kThreads, 1) void barrier_probe_kernel(int count, ChainState st, const uint4* x,
+                                                                    uint4* sink) {
+    __shared__ uint4 lds[256];
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < count; ++i) {
+        __syncthreads();
+        if constexpr (kVariant == 5) {
+            // two-level counter: 8 groups (one per XCD under round-robin
+            // dispatch), the last arriver of a group arrives globally
+            if (threadIdx.x == 0) {
+                unsigned* group = st.barrier + 32 * (1 + (blockIdx.x & 7));
+                const unsigned members = (gridDim.x + 7 - (blockIdx.x & 7)) / 8;
+                const unsigned old = __hip_atomic_fetch_add(group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (old + 1 == static_cast<unsigned>(i + 1) * members) {
+                    __hip_atomic_fetch_add(st.barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                const unsigned target = static_cast<unsigned>(i + 1) * 8u;
+                unsigned spins = 0;
+                while (__hip_atomic_load(st.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > (1u << 25)) {
+                        __hip_atomic_store(st.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __syncthreads();
+            continue;
+        }
+        if constexpr (kVariant == 6) {
+            // flag array: each workgroup publishes its epoch in its own slot;
+            // wave 0 polls every slot in parallel
+            unsigned* flags = st.barrier + 32 * 16;
+            const unsigned epoch = static_cast<unsigned>(i + 1);
+            if (threadIdx.x == 0) __hip_atomic_store(flags + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (threadIdx.x < 64) {
+                unsigned spins = 0;
+                while (true) {
+                    bool ok = true;
+                    for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 64) {
+                        ok = ok && __hip_atomic_load(flags + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= epoch;
+                    }
+                    if (__all(ok)) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > (1u << 25)) {
+                        if (threadIdx.x == 0) __hip_atomic_store(st.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __syncthreads();
+            continue;
+        }
+        if (threadIdx.x == 0) {
+            const unsigned target = static_cast<unsigned>(i + 1) * gridDim.x;
+            if constexpr (kVariant == 0 || kVariant == 3 || kVariant == 4) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            if constexpr (kVariant == 2) {
+                __hip_atomic_fetch_add(st.barrier, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __hip_atomic_fetch_add(st.barrier, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            unsigned spins = 0;
+            while (true) {
+                const unsigned seen = kVariant == 2
+                    ? __hip_atomic_load(st.barrier, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)
+                    : __hip_atomic_load(st.barrier, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (seen >= target) break;
+                if constexpr (kVariant != 3) __builtin_amdgcn_s_sleep(2);
+                if (++spins > (1u << 24)) {
+                    __hip_atomic_store(st.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+            if constexpr (kVariant == 0 || kVariant == 3 || kVariant == 4) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        __syncthreads();
+        if constexpr (kVariant == 4) {
+            lds[threadIdx.x] = x[threadIdx.x];
+            __syncthreads();
+            acc.x ^= lds[(threadIdx.x + i) & 255].x;
+        }
+    }
+    if (acc.x == 0x12345678u) sink[blockIdx.x] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_barrier_probe(int variant, int count, unsigned* sync, const void* x, void* sink, int workgroups,
+                                hipStream_t stream) {
+    zero_words_kernel<<<1, 256, 0, stream>>>(sync, 32 * 16 + 1024);
+    ChainState state{sync, reinterpret_cast<int*>(sync + 1), nullptr};
+    void* args[] = {&count, &state, &x, &sink};
+    const void* fn = nullptr;
+    switch (variant) {
+        case 0: fn = reinterpret_cast<const void*>(barrier_probe_kernel<0>); break;
+        case 1: fn = reinterpret_cast<const void*>(barrier_probe_kernel<1>); break;
+        case 2: fn = reinterpret_cast<const void*>(barrier_probe_kernel<2>); break;
+        case 3: fn = reinterpret_cast<const void*>(barrier_probe_kernel<3>); break;
+        case 4: fn = reinterpret_cast<const void*>(barrier_probe_kernel<4>); break;
+        case 5: fn = reinterpret_cast<const void*>(barrier_probe_kernel<5>); break;
+        case 6: fn = reinterpret_cast<const void*>(barrier_probe_kernel<6>); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipLaunchCooperativeKernel(fn, dim3(workgroups), dim3(kThreads), args, 0, stream);
+}
 
 // Picks the chain kind for a GEMV on a grid of `workgroups`; -1 if unsupported.
 int chain_kind_for(int in_features, int out_features, int epilogue, int workgroups) {
@@ -255,17 +434,64 @@ int chain_workgroups() {
     return props.multiProcessorCount;
 }
 
-// ops: device array of `count` ChainOp; sync: device scratch of 2 ints.
+// ops: device array of `count` ChainOp; sync: device scratch of
+// kChainSyncWords words (global counter, status, 8 group counters).
 hipError_t launch_persistent_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, unsigned long long* trace) {
     if (ops == nullptr || count <= 0 || sync == nullptr || workgroups <= 0) return hipErrorInvalidValue;
-    zero_sync_kernel<<<1, 64, 0, stream>>>(sync, reinterpret_cast<int*>(sync + 1));
+    zero_words_kernel<<<1, 256, 0, stream>>>(sync, kChainSyncWords);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    ChainState state{sync, reinterpret_cast<int*>(sync + 1)};
+    ChainState state{sync, reinterpret_cast<int*>(sync + 1), trace};
     void* args[] = {const_cast<ChainOp**>(&ops), &count, &state};
     return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(persistent_chain_kernel), dim3(workgroups),
                                       dim3(kThreads), args, 0, stream);
 }
 
 }  // namespace q3
+
+using namespace q3;
+
+// Diagnostic: microseconds per grid barrier of the persistent kernel's
+// barrier variants (see barrier_probe_kernel).
+extern "C" QWEN3_TTS_API int32_t qwen3_tts_benchmark_grid_barrier(int32_t device_index, int32_t variant,
+                                                                  int32_t barriers, int32_t workgroups,
+                                                                  double* microseconds_per_barrier,
+                                                                  char* error, size_t cap) {
+    auto fail = [&](const char* m) {
+        if (error && cap) std::snprintf(error, cap, "%s", m);
+        return QWEN3_TTS_TALKER_STATUS_CUDA;
+    };
+    if (microseconds_per_barrier == nullptr || barriers <= 0) return fail("invalid arguments");
+    if (hipSetDevice(device_index) != hipSuccess) return fail("hipSetDevice");
+    if (workgroups <= 0) workgroups = chain_workgroups();
+    unsigned* sync = nullptr;
+    void* x = nullptr;
+    void* sink = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t st = hipMalloc(&sync, (32 * 16 + 1024) * sizeof(unsigned));
+    if (st == hipSuccess) st = hipMalloc(&x, 4096);
+    if (st == hipSuccess) st = hipMalloc(&sink, 16 * static_cast<size_t>(workgroups));
+    if (st == hipSuccess) st = hipMemset(x, 0, 4096);
+    if (st == hipSuccess) st = hipEventCreate(&a);
+    if (st == hipSuccess) st = hipEventCreate(&b);
+    if (st == hipSuccess) st = launch_barrier_probe(variant, 16, sync, x, sink, workgroups, nullptr);
+    if (st == hipSuccess) st = hipEventRecord(a, nullptr);
+    if (st == hipSuccess) st = launch_barrier_probe(variant, barriers, sync, x, sink, workgroups, nullptr);
+    if (st == hipSuccess) st = hipEventRecord(b, nullptr);
+    if (st == hipSuccess) st = hipEventSynchronize(b);
+    float ms = 0.0f;
+    if (st == hipSuccess) st = hipEventElapsedTime(&ms, a, b);
+    int status = 0;
+    if (st == hipSuccess) st = hipMemcpy(&status, sync + 1, sizeof(int), hipMemcpyDeviceToHost);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (sync) (void)hipFree(sync);
+    if (x) (void)hipFree(x);
+    if (sink) (void)hipFree(sink);
+    if (st != hipSuccess) return fail(hipGetErrorString(st));
+    if (status != 0) return fail("barrier wait timed out");
+    *microseconds_per_barrier = ms * 1000.0 / barriers;
+    if (error && cap) error[0] = 0;
+    return QWEN3_TTS_TALKER_STATUS_OK;
+}

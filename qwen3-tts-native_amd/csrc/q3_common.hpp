@@ -214,10 +214,11 @@ struct ChainOp {
     float norm_epsilon;
     int reserved;
 };
+constexpr int kChainSyncWords = 32 * 16;
 int chain_kind_for(int in_features, int out_features, int epilogue, int workgroups);
 int chain_workgroups();
 hipError_t launch_persistent_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups,
-                                   hipStream_t stream);
+                                   hipStream_t stream, unsigned long long* trace = nullptr);
 
 // Lockstep-batch glue: rows of a batch from / to per-session buffers.
 hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,
