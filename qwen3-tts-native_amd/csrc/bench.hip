@@ -232,7 +232,7 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         ChainOp* d_ops = nullptr;
         unsigned* d_sync = nullptr;
         int op_count = 0;
-        if (b->use_graph == 2) {
+        if (b->use_graph == 2 || b->use_graph == 3) {
             if (R != 1) throw std::invalid_argument("the persistent chain serves batch 1");
             std::vector<ChainOp> ops;
             for (int l = 0; l < L; ++l) {
@@ -245,7 +245,8 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                 auto add = [&](const int8_t* wt, const float* sc, const bf16_t* in, const bf16_t* norm, bf16_t* out,
                                int in_f, int out_f, int epi) {
                     ChainOp op{};
-                    op.kind = chain_kind_for(in_f, out_f, epi, workgroups);
+                    op.kind = b->use_graph == 3 ? (stream_chain_supports(in_f, out_f, epi) ? 0 : -1)
+                                                : chain_kind_for(in_f, out_f, epi, workgroups);
                     if (op.kind < 0) throw std::invalid_argument("GEMV shape not supported by the persistent chain");
                     op.epilogue = epi;
                     op.in_features = in_f;
@@ -283,7 +284,11 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         unsigned long long* d_trace = (d_ops && trace_path) ? mem.get<unsigned long long>(256 * 8) : nullptr;
         auto run = [&] {
             if (d_ops) {
-                check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "persistent chain");
+                if (b->use_graph == 3) {
+                    check_hip(launch_stream_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "stream chain");
+                } else {
+                    check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "persistent chain");
+                }
             } else if (exec) {
                 check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
             } else {

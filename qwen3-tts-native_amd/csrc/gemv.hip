@@ -33,12 +33,15 @@ using namespace gemv_detail;
 
 // ---------------------------------------------------------------------------
 // Exact-order GEMV, one activation row, K = kVpl * 512 known at compile time.
-// A half-wave owns one unit per iteration: one weight row (plain / residual /
+// The grid has one half-wave per unit: one weight row (plain / residual /
 // bias epilogues) or the gate row u and the up row out+u (SiLU epilogues).
-// Latency order: the first unit's weight loads are issued before anything
-// else (they do not depend on x), then x (and the RMSNorm gain) is staged
-// into LDS with 128-bit loads, the norm statistic is reduced from LDS, and
-// each lane pulls its x slice into registers while the weights are in flight.
+// Latency order: x (and the RMSNorm gain) is requested first, then the first
+// unit's weights and its epilogue operands (scales, residual, bias).  Vector
+// memory completes in issue order, so x is staged into LDS, normalized once
+// per block (statistic reduced by all 256 threads, each thread normalizing its
+// own chunks) and each lane's x slice pulled into registers while the weights
+// are still in flight; no memory round trip follows the dot product except the
+// output store.
 // ---------------------------------------------------------------------------
 template <int kVpl, int kEpi, bool kNorm>
 __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
@@ -51,11 +54,34 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
     constexpr int kIn = kVpl * 512;
     constexpr int kChunks = kIn * 2 / 16;  // 16-byte chunks of one bf16 row
     __shared__ uint4 x_lds[kChunks];
-    __shared__ uint4 g_lds[kNorm ? kChunks : 1];
+    __shared__ float partial_lds[kNorm ? kThreads : 1];
     const int lane = threadIdx.x & 31;
     const int units = a.out_features;
-    const int stride = gridDim.x * kHalfWaves;
-    int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5);
+    const int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5);
+
+    // The activation row (and RMSNorm gain) is requested first: vector memory
+    // returns in issue order, so it lands while the weights are in flight and
+    // the norm statistic is computed under the weight stream.
+    constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+    static_assert(kPer <= 3, "x staging holds at most three 16-byte chunks per thread");
+    // Clamped rather than guarded (a branch here would make the compiler wait
+    // for the whole weight stream before the LDS stores below); named
+    // registers rather than an array, which the compiler would place in
+    // scratch memory.
+    auto chunk = [](int j) { return min(static_cast<int>(threadIdx.x) + j * kThreads, kChunks - 1); };
+    const uint4* xin = reinterpret_cast<const uint4*>(a.input);
+    const uint4* gin = reinterpret_cast<const uint4*>(a.norm_weight);
+    uint4 x0 = xin[chunk(0)], x1{}, x2{}, g0{}, g1{}, g2{};
+    if constexpr (kNorm) g0 = gin[chunk(0)];
+    if constexpr (kPer > 1) {
+        x1 = xin[chunk(1)];
+        if constexpr (kNorm) g1 = gin[chunk(1)];
+    }
+    if constexpr (kPer > 2) {
+        x2 = xin[chunk(2)];
+        if constexpr (kNorm) g2 = gin[chunk(2)];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight loads
 
     int4 w[kRows][kVpl];
     auto issue = [&](int u) {
@@ -67,17 +93,33 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
             for (int i = 0; i < kVpl; ++i) w[r][i] = stream_load(base + lane + 32 * i);
         }
     };
-    if (unit < units) issue(unit);
+    // Unconditional (clamped) so the x loads' wait is not merged with a path
+    // that skipped the weight loads: half-waves past the end read the last
+    // unit and discard it.
+    const int first = unit < units ? unit : units - 1;
+    issue(first);
+    EpiInputs epi = prefetch_epi<kEpi>(a, first);
+    __builtin_amdgcn_sched_barrier(0);  // and the LDS stores of x behind them
 
-    for (int c = threadIdx.x; c < kChunks; c += kThreads) {
-        x_lds[c] = reinterpret_cast<const uint4*>(a.input)[c];
-        if constexpr (kNorm) g_lds[c] = reinterpret_cast<const uint4*>(a.norm_weight)[c];
-    }
+    auto stage = [&](int j, const uint4& xv) {
+        const int c = static_cast<int>(threadIdx.x) + j * kThreads;
+        if (kChunks % kThreads == 0 || c < kChunks) x_lds[c] = xv;
+    };
+    stage(0, x0);
+    if constexpr (kPer > 1) stage(1, x1);
+    if constexpr (kPer > 2) stage(2, x2);
     __syncthreads();
     const bf16_t* xs = reinterpret_cast<const bf16_t*>(x_lds);
-    float inverse = 1.0f;
     if constexpr (kNorm) {
-        inverse = wave_inverse_rms(xs, kIn, a.norm_epsilon);
+        // The block normalizes x once, in place: each thread its own chunks
+        // from registers, after the statistic has been reduced.
+        partial_lds[threadIdx.x] = block_partial_sq(xs, kIn);
+        __syncthreads();
+        const float inverse = fold_partials256(partial_lds, kIn, a.norm_epsilon);
+        stage(0, normalize_chunk(x0, g0, inverse));
+        if constexpr (kPer > 1) stage(1, normalize_chunk(x1, g1, inverse));
+        if constexpr (kPer > 2) stage(2, normalize_chunk(x2, g2, inverse));
+        __syncthreads();
     }
     // Activation slice of this lane: vectors lane + 32*i.
     float xf[kPacked ? 1 : kVpl][16];
@@ -85,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < kVpl; ++i) {
         float tmp[16];
-        load_x16<kNorm>(xs, reinterpret_cast<const bf16_t*>(g_lds), lane + 32 * i, inverse, tmp);
+        load_x16<false>(xs, nullptr, lane + 32 * i, 1.0f, tmp);
         if constexpr (kPacked) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -98,29 +140,28 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
         }
     }
 
-    for (; unit < units; unit += stride) {
-        float acc[kRows];
+    // One unit per half-wave (the grid covers every unit): no loop, so the
+    // first weight vectors are consumed as soon as they land.
+    float acc[kRows];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            acc[r] = 0.0f;
+    for (int r = 0; r < kRows; ++r) {
+        acc[r] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < kVpl; ++i) {
-                if constexpr (kPacked) {
-                    acc[r] += chain16_packed(w[r][i], xp[i]);
-                } else {
-                    acc[r] += chain16(w[r][i], xf[i]);
-                }
+        for (int i = 0; i < kVpl; ++i) {
+            if constexpr (kPacked) {
+                acc[r] += chain16_packed(w[r][i], xp[i]);
+            } else {
+                acc[r] += chain16(w[r][i], xf[i]);
             }
         }
-        if (unit + stride < units) issue(unit + stride);
+    }
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) acc[r] = fold32(acc[r]);
-        if (lane == 0) {
-            if constexpr (kSilu) {
-                store_gate_up<kEpi>(a, unit, acc[0], acc[kRows - 1]);
-            } else {
-                store_channel<kEpi>(a, unit, acc[0]);
-            }
+    for (int r = 0; r < kRows; ++r) acc[r] = fold32(acc[r]);
+    if (lane == 0 && unit < units) {
+        if constexpr (kSilu) {
+            finish_gate_up<kEpi>(a, unit, acc[0], acc[kRows - 1], epi);
+        } else {
+            finish_channel<kEpi>(a, unit, acc[0], epi);
         }
     }
 }
@@ -407,7 +448,6 @@ hipError_t dispatch_generic(const GemvArgs& a, int grid, hipStream_t s) {
 
 template <int kEpi, bool kNorm>
 hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
-    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
     const bool mfma = a.mode == kModeMfma || (a.mode == kModeAuto && a.rows >= 2);
     if (mfma) {
         if (a.in_features % 256 != 0 || (kNorm && a.in_features > 6144)) {

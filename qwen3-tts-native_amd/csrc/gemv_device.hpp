@@ -62,8 +62,53 @@ __device__ inline float wave_inverse_rms(const bf16_t* x, int width, float epsil
     return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
 }
 
+// Cooperative RMSNorm statistic of a 256-thread block, identical to the
+// reference's 256-thread block_sum (talker_kernels.cu:36-41): thread t's
+// partial is sum(x[i]^2, i = t, t+256, ...) as one fma chain, written to
+// partial[t]; after a barrier every wave folds the 256 partials in the tree
+// order of wave_inverse_rms and gets the same inverse.
+__device__ __forceinline__ float block_partial_sq(const bf16_t* x, int width) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < width; i += 256) {
+        const float v = bf2f(x[i]);
+        s = fmaf(v, v, s);
+    }
+    return s;
+}
+
+__device__ __forceinline__ float fold_partials256(const float* partial, int width, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    float p0 = partial[lane], p1 = partial[lane + 64];
+    const float p2 = partial[lane + 128], p3 = partial[lane + 192];
+    p0 += p2;
+    p1 += p3;
+    float value = p0 + p1;
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        value += __shfl_down(value, offset, 64);
+    }
+    const float total = __shfl(value, 0, 64);
+    return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
+}
+
 __device__ __forceinline__ float normalize_one(float x, float inverse, float gain) {
     return round_bf(round_bf(x * inverse) * gain);
+}
+
+// Normalize one 16-byte chunk (8 bf16 activations with their gains).  The
+// result of normalize_one is a bf16 value, so its top half is exact.
+__device__ __forceinline__ uint4 normalize_chunk(const uint4 x, const uint4 g, float inverse) {
+    const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = normalize_one(__uint_as_float(xw[i] << 16), inverse, __uint_as_float(gw[i] << 16));
+        const float hi = normalize_one(__uint_as_float(xw[i] & 0xffff0000u), inverse,
+                                       __uint_as_float(gw[i] & 0xffff0000u));
+        o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Load the 16 activations of vector `v` (bf16) as fp32, normalized if needed.
@@ -146,36 +191,65 @@ __device__ __forceinline__ void store_out(bf16_t* p, bf16_t v) {
     }
 }
 
-// Half-wave lane 0 epilogue for the plain / residual epilogues.
+// Epilogue operands of one output channel (or gate/up pair): the scale(s),
+// the residual or bias.  Loaded before the dot products so their memory
+// latency overlaps the weight stream instead of following it.
+struct EpiInputs {
+    float scale0 = 0.0f;
+    float scale1 = 0.0f;
+    float extra = 0.0f;  // residual (add epilogues) or bias
+    float prior = 0.0f;  // residual of bias-add
+};
+
 template <int kEpi, bool kCoherent = false>
-__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
-    const float scale = a.scales[channel];
+__device__ __forceinline__ EpiInputs prefetch_epi(const GemvArgs& a, int channel) {
+    EpiInputs e;
+    e.scale0 = a.scales[channel];
+    if constexpr (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded) {
+        e.scale1 = a.scales[a.out_features + channel];
+    } else if constexpr (kEpi == kEpiAddFma || kEpi == kEpiAddRounded) {
+        e.extra = load_out<kCoherent>(a.out16 + channel);
+    } else if constexpr (kEpi == kEpiBias || kEpi == kEpiBiasSilu) {
+        e.extra = bf2f(a.bias[channel]);
+    } else if constexpr (kEpi == kEpiBiasAdd) {
+        e.extra = bf2f(a.bias[channel]);
+        e.prior = load_out<kCoherent>(a.out16 + channel);
+    }
+    return e;
+}
+
+// Half-wave lane 0 epilogue for the plain / residual / bias epilogues.
+template <int kEpi, bool kCoherent = false>
+__device__ __forceinline__ void finish_channel(const GemvArgs& a, int channel, float value, const EpiInputs& e) {
+    const float scale = e.scale0;
     bf16_t* out = a.out16 + channel;
     if constexpr (kEpi == kEpiStore) {
         const float y = value * scale;
         if (a.out32 != nullptr) a.out32[channel] = y;
         if (a.out16 != nullptr) store_out<kCoherent>(out, f2bf(y));
     } else if constexpr (kEpi == kEpiAddFma) {
-        store_out<kCoherent>(out, f2bf(fmaf(value, scale, load_out<kCoherent>(out))));
+        store_out<kCoherent>(out, f2bf(fmaf(value, scale, e.extra)));
     } else if constexpr (kEpi == kEpiAddRounded) {
         const float projected = round_bf(value * scale);
-        store_out<kCoherent>(out, f2bf(load_out<kCoherent>(out) + projected));
+        store_out<kCoherent>(out, f2bf(e.extra + projected));
     } else if constexpr (kEpi == kEpiBias) {
-        store_out<kCoherent>(out, f2bf(round_bf(value * scale) + bf2f(a.bias[channel])));
+        store_out<kCoherent>(out, f2bf(round_bf(value * scale) + e.extra));
     } else if constexpr (kEpi == kEpiBiasSilu) {
-        float v = round_bf(value * scale) + bf2f(a.bias[channel]);
+        float v = round_bf(value * scale) + e.extra;
         v *= 1.0f / (1.0f + q3_expf(-v));
         store_out<kCoherent>(out, f2bf(v));
     } else if constexpr (kEpi == kEpiBiasAdd) {
-        const float projected = round_bf(round_bf(value * scale) + bf2f(a.bias[channel]));
-        store_out<kCoherent>(out, f2bf(load_out<kCoherent>(out) + projected));
+        const float projected = round_bf(round_bf(value * scale) + e.extra);
+        store_out<kCoherent>(out, f2bf(e.prior + projected));
     }
 }
 
+// Gate/up pair epilogue (int8_gemv.cu:284-288 fused; separate SiLU-gate
+// rounding for the single-session path).
 template <int kEpi, bool kCoherent = false>
-__device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
-    const float gate = g * a.scales[channel];
-    const float up = u * a.scales[a.out_features + channel];
+__device__ __forceinline__ void finish_gate_up(const GemvArgs& a, int channel, float g, float u, const EpiInputs& e) {
+    const float gate = g * e.scale0;
+    const float up = u * e.scale1;
     if constexpr (kEpi == kEpiSiluFused) {
         const float activated = gate / (1.0f + q3_expf(-gate));
         store_out<kCoherent>(a.out16 + channel, f2bf(activated * up));
@@ -185,6 +259,16 @@ __device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, fl
         const float activated = round_bf(gate16 / (1.0f + q3_expf(-gate16)));
         store_out<kCoherent>(a.out16 + channel, f2bf(activated * up16));
     }
+}
+
+template <int kEpi, bool kCoherent = false>
+__device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
+    finish_channel<kEpi, kCoherent>(a, channel, value, prefetch_epi<kEpi, kCoherent>(a, channel));
+}
+
+template <int kEpi, bool kCoherent = false>
+__device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
+    finish_gate_up<kEpi, kCoherent>(a, channel, g, u, prefetch_epi<kEpi, kCoherent>(a, channel));
 }
 
 

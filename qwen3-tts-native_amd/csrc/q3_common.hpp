@@ -217,6 +217,12 @@ struct ChainOp {
 constexpr int kChainSyncWords = 32 * 16;
 int chain_kind_for(int in_features, int out_features, int epilogue, int workgroups);
 int chain_workgroups();
+// Warp-specialized persistent chain (loader waves stream weights into an LDS
+// ring; compute waves consume): same op list, ChainOp::kind ignored.
+bool stream_chain_supports(int in_features, int out_features, int epilogue);
+size_t stream_chain_lds_bytes();
+hipError_t launch_stream_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups, hipStream_t stream,
+                               unsigned long long* trace = nullptr);
 hipError_t launch_persistent_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups,
                                    hipStream_t stream, unsigned long long* trace = nullptr);
 

@@ -1,7 +1,9 @@
 """The persistent GEMV chain kernel (one cooperative launch per talker step,
 grid barriers between dependent GEMVs, next-GEMV weights prefetched before
 each barrier) must produce bit-identical hidden states to the same chain run
-as one kernel launch per GEMV."""
+as one kernel launch per GEMV.  Variant 2 is the tile-prefetching chain,
+variant 3 the warp-specialized chain (loader waves stream weights through an
+LDS ring with direct-to-LDS loads)."""
 import ctypes as C
 
 import pytest
@@ -18,16 +20,18 @@ def run(hip, use_graph, layers, steps=1, warmup=0, kernel_filter=0):
     return b
 
 
+@pytest.mark.parametrize("variant", [2, 3])
 @pytest.mark.parametrize("layers,steps", [(1, 1), (2, 1), (28, 2)])
-def test_persistent_chain_bit_identical(hip, layers, steps):
+def test_persistent_chain_bit_identical(hip, layers, steps, variant):
     eager = run(hip, 0, layers, steps=steps)
-    persistent = run(hip, 2, layers, steps=steps)
+    persistent = run(hip, variant, layers, steps=steps)
     assert persistent.output_checksum == eager.output_checksum
     assert persistent.algorithmic_bytes_per_step == eager.algorithmic_bytes_per_step
 
 
+@pytest.mark.parametrize("variant", [2, 3])
 @pytest.mark.parametrize("kernel_filter", [1, 2, 3, 4])
-def test_persistent_single_kind_chains(hip, kernel_filter):
+def test_persistent_single_kind_chains(hip, kernel_filter, variant):
     eager = run(hip, 0, 3, kernel_filter=kernel_filter)
-    persistent = run(hip, 2, 3, kernel_filter=kernel_filter)
+    persistent = run(hip, variant, 3, kernel_filter=kernel_filter)
     assert persistent.output_checksum == eager.output_checksum
