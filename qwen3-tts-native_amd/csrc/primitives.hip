@@ -152,148 +152,6 @@ __global__ void rope_kernel(bf16_t* values, int rows, int heads, int head_dimens
     base[d + half] = f2bf(sc + fs);
 }
 
-// ---------------------------------------------------------------------------
-// Decode attention, one 256-thread block per (row, query head), d = 128.
-//
-// kExact reproduces causal_gqa_attention_kernel (talker_kernels.cu:287-357):
-//   dot = 256-thread tree of the 128 exact products, rounded to bf16;
-//   score = bf16(dot * scale); softmax sequential in fp32 with bf16 probs;
-//   out[d] = bf16(sequential fmaf over positions).
-// !kExact reproduces batch_causal_gqa_attention_fast_kernel (:506-595):
-//   fp32 scores from a sequential fmaf over d; 256-thread max and sum trees
-//   over per-thread strided partials; out[d] = bf16(chain * (1/sum)).
-// Scores, each computed by one lane over a whole key row (no per-position
-// block barrier), live in LDS.  The sequential chains are the reference's
-// own order and are kept.
-// ---------------------------------------------------------------------------
-template <bool kExact>
-__global__ __launch_bounds__(kThreads) void attention_kernel(
-    const bf16_t* query, int query_stride, bf16_t* const* key_bases, bf16_t* const* value_bases,
-    const bf16_t* key_cache, const bf16_t* value_cache, const int* positions,
-    int fixed_sequence_length, bf16_t* output, int query_heads, int key_value_heads,
-    float scale) {
-    constexpr int kDim = 128;
-    extern __shared__ float scores[];
-    __shared__ float q_shared[kDim];
-    __shared__ float reduction[kThreads];
-    __shared__ float broadcast[2];
-    const int row = blockIdx.x / query_heads;
-    const int qh = blockIdx.x % query_heads;
-    const int kvh = qh / (query_heads / key_value_heads);
-    const int tid = threadIdx.x;
-    const int length = positions ? positions[row] + 1 : fixed_sequence_length;
-    const bf16_t* keys = key_bases ? key_bases[row] : key_cache;
-    const bf16_t* values = value_bases ? value_bases[row] : value_cache;
-    const int kv_width = key_value_heads * kDim;
-    const bf16_t* q = query + static_cast<size_t>(row) * query_stride + static_cast<size_t>(qh) * kDim;
-    if (tid < kDim) q_shared[tid] = bf2f(q[tid]);
-    __syncthreads();
-
-    float local_max = -INFINITY;
-    for (int p = tid; p < length; p += kThreads) {
-        const uint4* k4 = reinterpret_cast<const uint4*>(keys + static_cast<size_t>(p) * kv_width +
-                                                         static_cast<size_t>(kvh) * kDim);
-        float score;
-        if constexpr (kExact) {
-            // s[t] = (q[t]k[t] + 0) + (q[t+64]k[t+64] + 0), t < 64; then halves.
-            float s[64];
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                const uint4 lo = k4[v];
-                const uint4 hi = k4[v + 8];
-                const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
-                const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        const int t = 8 * v + 2 * i + b;
-                        const float kl = b ? __uint_as_float(lw[i] & 0xffff0000u) : __uint_as_float(lw[i] << 16);
-                        const float kh = b ? __uint_as_float(hw[i] & 0xffff0000u) : __uint_as_float(hw[i] << 16);
-                        const float a = fmaf(q_shared[t], kl, 0.0f) + 0.0f;
-                        const float c = fmaf(q_shared[t + 64], kh, 0.0f) + 0.0f;
-                        s[t] = a + c;
-                    }
-                }
-            }
-#pragma unroll
-            for (int w = 32; w > 0; w >>= 1) {
-#pragma unroll
-                for (int t = 0; t < w; ++t) s[t] += s[t + w];
-            }
-            score = round_bf(round_bf(s[0]) * scale);
-        } else {
-            float dot = 0.0f;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint4 w4 = k4[v];
-                const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    dot = fmaf(q_shared[8 * v + 2 * i], __uint_as_float(w[i] << 16), dot);
-                    dot = fmaf(q_shared[8 * v + 2 * i + 1], __uint_as_float(w[i] & 0xffff0000u), dot);
-                }
-            }
-            score = dot * scale;
-        }
-        scores[p] = score;
-        local_max = fmaxf(local_max, score);
-    }
-    // Maximum (order independent).
-    reduction[tid] = local_max;
-    __syncthreads();
-    for (int s = kThreads / 2; s > 0; s >>= 1) {
-        if (tid < s) reduction[tid] = fmaxf(reduction[tid], reduction[tid + s]);
-        __syncthreads();
-    }
-    const float maximum = reduction[0];
-    __syncthreads();
-    float inverse;
-    if constexpr (kExact) {
-        for (int p = tid; p < length; p += kThreads) scores[p] = q3_expf(scores[p] - maximum);
-        __syncthreads();
-        if (tid == 0) {
-            float denominator = 0.0f;
-            for (int p = 0; p < length; ++p) denominator += scores[p];
-            broadcast[0] = 1.0f / denominator;
-        }
-        __syncthreads();
-        inverse = broadcast[0];
-        for (int p = tid; p < length; p += kThreads) scores[p] = round_bf(scores[p] * inverse);
-        __syncthreads();
-    } else {
-        float local_sum = 0.0f;
-        for (int p = tid; p < length; p += kThreads) {
-            const float w = q3_expf(scores[p] - maximum);
-            scores[p] = w;
-            local_sum += w;
-        }
-        reduction[tid] = local_sum;
-        __syncthreads();
-        for (int s = kThreads / 2; s > 0; s >>= 1) {
-            if (tid < s) reduction[tid] += reduction[tid + s];
-            __syncthreads();
-        }
-        inverse = 1.0f / reduction[0];
-        __syncthreads();
-    }
-    if (tid < kDim) {
-        const bf16_t* vcol = values + static_cast<size_t>(kvh) * kDim + tid;
-        float acc = 0.0f;
-        int p = 0;
-        for (; p + 8 <= length; p += 8) {
-            float vv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) vv[u] = bf2f(vcol[static_cast<size_t>(p + u) * kv_width]);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = fmaf(scores[p + u], vv[u], acc);
-        }
-        for (; p < length; ++p) acc = fmaf(scores[p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
-        bf16_t* out = output + (static_cast<size_t>(row) * query_heads + qh) * kDim;
-        out[tid] = kExact ? f2bf(acc) : f2bf(acc * inverse);
-    }
-}
-
 __global__ void kv_scatter_rows_kernel(const bf16_t* rows_data, bf16_t* const* cache_bases,
                                        const int* positions, int rows, int width, int row_stride) {
     const int index = blockIdx.x * blockDim.x + threadIdx.x;
@@ -420,37 +278,32 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
     return hipGetLastError();
 }
 
-hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
-                            bf16_t* const* key_bases, bf16_t* const* value_bases,
-                            const bf16_t* key_cache, const bf16_t* value_cache,
-                            const int* positions, int fixed_sequence_length, bf16_t* output,
-                            int rows, int query_heads, int key_value_heads, int head_dimension,
-                            int max_sequence_length, hipStream_t stream) {
-    if (head_dimension != 128 || query_heads % key_value_heads != 0 || rows <= 0 ||
-        max_sequence_length <= 0 || max_sequence_length > 16384) {
-        return hipErrorInvalidValue;
-    }
-    const float scale = 1.0f / sqrtf(static_cast<float>(head_dimension));
-    const size_t shared = static_cast<size_t>(max_sequence_length) * sizeof(float);
-    if (exact) {
-        attention_kernel<true><<<rows * query_heads, kThreads, shared, stream>>>(
-            query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
-            fixed_sequence_length, output, query_heads, key_value_heads, scale);
-    } else {
-        attention_kernel<false><<<rows * query_heads, kThreads, shared, stream>>>(
-            query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
-            fixed_sequence_length, output, query_heads, key_value_heads, scale);
-    }
-    return hipGetLastError();
+// Stand-alone forms (primitive self-test and op exports): a stream-ordered
+// temporary workspace.
+static hipError_t attention_with_temporary(bool exact, const bf16_t* query, int query_stride,
+                                           bf16_t* const* key_bases, bf16_t* const* value_bases,
+                                           const bf16_t* key_cache, const bf16_t* value_cache,
+                                           const int* positions, int fixed_length, bf16_t* output, int rows,
+                                           int query_heads, int key_value_heads, int head_dimension, int capacity,
+                                           hipStream_t stream) {
+    if (rows <= 0 || query_heads <= 0 || capacity <= 0) return hipErrorInvalidValue;
+    void* workspace = nullptr;
+    hipError_t st = hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, capacity), stream);
+    if (st != hipSuccess) return st;
+    st = launch_attention(exact, query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
+                          fixed_length, output, rows, query_heads, key_value_heads, head_dimension, capacity,
+                          static_cast<float*>(workspace), stream);
+    const hipError_t freed = hipFreeAsync(workspace, stream);
+    return st != hipSuccess ? st : freed;
 }
 
 hipError_t launch_causal_gqa_attention(const bf16_t* query, const bf16_t* key_cache,
                                        const bf16_t* value_cache, bf16_t* output, int query_heads,
                                        int key_value_heads, int head_dimension,
                                        int sequence_length, int query_stride, hipStream_t stream) {
-    return launch_attention(true, query, query_stride, nullptr, nullptr, key_cache, value_cache,
-                            nullptr, sequence_length, output, 1, query_heads, key_value_heads,
-                            head_dimension, sequence_length, stream);
+    return attention_with_temporary(true, query, query_stride, nullptr, nullptr, key_cache, value_cache, nullptr,
+                                    sequence_length, output, 1, query_heads, key_value_heads, head_dimension,
+                                    sequence_length, stream);
 }
 
 hipError_t launch_batch_causal_gqa_attention_fast(const bf16_t* query, bf16_t* const* key_bases,
@@ -459,9 +312,19 @@ hipError_t launch_batch_causal_gqa_attention_fast(const bf16_t* query, bf16_t* c
                                                   int key_value_heads, int head_dimension,
                                                   int max_sequence_length, int query_stride,
                                                   hipStream_t stream) {
-    return launch_attention(false, query, query_stride, key_bases, value_bases, nullptr, nullptr,
-                            positions, 0, output, rows, query_heads, key_value_heads,
-                            head_dimension, max_sequence_length, stream);
+    return attention_with_temporary(false, query, query_stride, key_bases, value_bases, nullptr, nullptr,
+                                    positions, 0, output, rows, query_heads, key_value_heads, head_dimension,
+                                    max_sequence_length, stream);
+}
+
+hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride, bf16_t* const* key_bases,
+                               bf16_t* const* value_bases, const int* positions, bf16_t* output, int rows,
+                               int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,
+                               hipStream_t stream) {
+    if (key_bases == nullptr || value_bases == nullptr || positions == nullptr) return hipErrorInvalidValue;
+    return attention_with_temporary(exact, query, query_stride, key_bases, value_bases, nullptr, nullptr, positions,
+                                    0, output, rows, query_heads, key_value_heads, head_dimension,
+                                    max_sequence_length, stream);
 }
 
 hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,

@@ -139,12 +139,19 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
 // otherwise batch_causal_gqa_attention_fast semantics (:506-595).  Keys/values come
 // from key_bases[row] (or key_cache when key_bases is null); the length is
 // positions[row] + 1 (or fixed_sequence_length when positions is null).
+// Decode attention (head dimension 128).  workspace: attention_workspace_bytes
+// of device memory owned by the caller's stream.
+size_t attention_workspace_bytes(int rows, int query_heads, int capacity);
 hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
                             bf16_t* const* key_bases, bf16_t* const* value_bases,
                             const bf16_t* key_cache, const bf16_t* value_cache,
                             const int* positions, int fixed_sequence_length, bf16_t* output,
                             int rows, int query_heads, int key_value_heads, int head_dimension,
-                            int max_sequence_length, hipStream_t stream);
+                            int max_sequence_length, float* workspace, hipStream_t stream);
+hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride, bf16_t* const* key_bases,
+                               bf16_t* const* value_bases, const int* positions, bf16_t* output, int rows,
+                               int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,
+                               hipStream_t stream);
 hipError_t launch_causal_gqa_attention(const bf16_t* query, const bf16_t* key_cache,
                                        const bf16_t* value_cache, bf16_t* output, int query_heads,
                                        int key_value_heads, int head_dimension,

@@ -670,8 +670,8 @@ QWEN3_TTS_API int32_t qwen3_tts_op_attention(int32_t exact, const uint16_t* quer
                                              const int32_t* positions, uint16_t* output, int32_t rows, int32_t qh,
                                              int32_t kvh, int32_t hd, int32_t max_seq, void* stream, char* error,
                                              size_t cap) {
-    return launch_status(launch_attention(exact != 0, query, query_stride, key_bases, value_bases, nullptr, nullptr,
-                                          positions, 0, output, rows, qh, kvh, hd, max_seq, as_stream(stream)),
+    return launch_status(launch_attention_op(exact != 0, query, query_stride, key_bases, value_bases, positions, output,
+                                             rows, qh, kvh, hd, max_seq, as_stream(stream)),
                          "attention", error, cap);
 }
 

@@ -49,6 +49,7 @@ namespace {
 constexpr int kCodebooks = 16;
 constexpr int kResidualCodebooks = 15;
 constexpr int kMaxBatch = QWEN3_TTS_MAX_BATCH_SESSIONS;
+constexpr int kAttentionCapacity = 8192;  // largest session max_sequence_length
 
 void write_error(char* destination, size_t capacity, const char* message) {
     if (destination != nullptr && capacity != 0) {
@@ -523,7 +524,7 @@ public:
     Session(std::shared_ptr<Model> model, int max_sequence_length, uint64_t seed)
         : model_(std::move(model)), m_(*model_), cfg_(model_->config()),
           device_(model_->device_index()), max_seq_(max_sequence_length) {
-        if (max_sequence_length < 16 || max_sequence_length > 8192) {
+        if (max_sequence_length < 16 || max_sequence_length > kAttentionCapacity) {
             throw std::runtime_error("max sequence length must be in [16, 8192]");
         }
         if (!model_->finalized()) {
@@ -551,6 +552,8 @@ public:
             p_hidden_ = DeviceBuffer(static_cast<size_t>(P.hidden) * b);
             qkv_ = DeviceBuffer(static_cast<size_t>(widest) * b);
             attn_ = DeviceBuffer(static_cast<size_t>(std::max(T.query_width(), P.query_width())) * b);
+            attn_scratch_ = DeviceBuffer(attention_workspace_bytes(1, std::max(T.query_heads, P.query_heads),
+                                                                   std::max(max_seq_, kCodebooks)));
             act_ = DeviceBuffer(static_cast<size_t>(std::max(T.intermediate, P.intermediate)) * b);
             logits_ = DeviceBuffer(static_cast<size_t>(std::max(cfg_.talker_vocab, cfg_.predictor_vocab)) * b);
             proj_ = DeviceBuffer(static_cast<size_t>(T.hidden) * b);
@@ -769,7 +772,7 @@ public:
         Qwen3TtsSessionMemory r{};
         r.talker_kv_bytes = talker_k_.bytes() + talker_v_.bytes();
         r.predictor_kv_bytes = pred_k_.bytes() + pred_v_.bytes();
-        r.workspace_bytes = hidden_.bytes() + p_hidden_.bytes() + qkv_.bytes() + attn_.bytes() +
+        r.workspace_bytes = hidden_.bytes() + p_hidden_.bytes() + qkv_.bytes() + attn_.bytes() + attn_scratch_.bytes() +
                             act_.bytes() + logits_.bytes() + proj_.bytes() + last_hidden_.bytes() +
                             ints_.bytes() + history_.bytes() + codes_.bytes() + random_state_.bytes() +
                             kv_bases_.bytes();
@@ -887,7 +890,7 @@ private:
             const bf16_t* vc = host_bases_[(predictor ? 2 * cfg_.talker.layers : 0) + d.layers + l];
             check_hip(launch_attention(true, qkv_.as<bf16_t>(), d.qkv_width(), nullptr, nullptr, kc, vc, position, 0,
                                        attn_.as<bf16_t>(), 1, d.query_heads, d.key_value_heads, d.head_dimension,
-                                       cache_rows, stream_),
+                                       cache_rows, attn_scratch_.as<float>(), stream_),
                       "attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddRounded).to(hidden).run(stream_, "O GEMV");
             Gemv(L.gate_up, hidden, d.hidden, d.intermediate, kEpiSiluRounded).norm(L.post_norm, cfg_.eps).to(act_.as<bf16_t>()).run(stream_, "gate/up GEMV");
@@ -997,7 +1000,7 @@ private:
     hipEvent_t start_ = nullptr, stop_ = nullptr, predictor_start_ = nullptr, predictor_stop_ = nullptr;
     hipEvent_t codes_ready_ = nullptr, semantic_ready_ = nullptr;
     DeviceBuffer talker_k_, talker_v_, pred_k_, pred_v_;
-    DeviceBuffer hidden_, p_hidden_, qkv_, attn_, act_, logits_, proj_, last_hidden_;
+    DeviceBuffer hidden_, p_hidden_, qkv_, attn_, attn_scratch_, act_, logits_, proj_, last_hidden_;
     DeviceBuffer ints_, history_, codes_, random_state_, kv_bases_;
     std::vector<bf16_t*> host_bases_;
     int* pinned_ = nullptr;  // [0] sampled token, [1] text token, [8..] codes (u16)
@@ -1110,6 +1113,8 @@ public:
         proj_ = DeviceBuffer(R * T.hidden * b);
         qkv_ = DeviceBuffer(R * std::max(T.qkv_width(), P.qkv_width()) * b);
         attn_ = DeviceBuffer(R * std::max(T.query_width(), P.query_width()) * b);
+        attn_scratch_ = DeviceBuffer(attention_workspace_bytes(static_cast<int>(R), std::max(T.query_heads, P.query_heads),
+                                                               kAttentionCapacity));
         act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
         logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
         layers_ = T.layers + P.layers;
@@ -1306,7 +1311,8 @@ private:
                       "batch q/k norm + RoPE + KV append");
             check_hip(launch_attention(false, qkv_.as<bf16_t>(), d.qkv_width(), kv_table(slot0 + l, false),
                                        kv_table(slot0 + l, true), nullptr, nullptr, pos, 0, attn_.as<bf16_t>(), n,
-                                       d.query_heads, d.key_value_heads, d.head_dimension, capacity, stream_),
+                                       d.query_heads, d.key_value_heads, d.head_dimension, capacity,
+                                       attn_scratch_.as<float>(), stream_),
                       "batch attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
                 .run(stream_, "batch O GEMV");
@@ -1394,7 +1400,7 @@ private:
     int layers_ = 0;
     hipStream_t stream_ = nullptr;
     std::array<hipEvent_t, kCapacity> join_{};
-    DeviceBuffer hidden_, normalized_, p_hidden_, text_input_, proj_, qkv_, attn_, act_, logits_, tables_;
+    DeviceBuffer hidden_, normalized_, p_hidden_, text_input_, proj_, qkv_, attn_, attn_scratch_, act_, logits_, tables_;
     size_t table_bytes_ = 0;
     void* pinned_ = nullptr;
     hipGraphExec_t predictor_graph_ = nullptr, talker_graph_ = nullptr;

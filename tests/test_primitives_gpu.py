@@ -113,6 +113,26 @@ def test_attention(hip, orc, exact, length):
     assert np.array_equal(out.numpy(), ref)
 
 
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("qh,kvh", [(16, 8), (8, 8), (16, 4)])
+@pytest.mark.parametrize("length,max_seq", [(15, 16), (16, 16), (64, 64), (65, 65), (17, 1001), (513, 1001), (1001, 1001), (4096, 4099)])
+def test_attention_groups_and_ring_edges(hip, orc, exact, qh, kvh, length, max_seq):
+    """GQA group sizes 1/2/4, lengths around the value-ring and chunk edges,
+    cache capacities that are not multiples of four."""
+    rng = np.random.default_rng(length * 7 + qh + kvh + exact)
+    d = 128
+    q = gen.activations(rng, qh * d)
+    k = gen.bf16(rng.standard_normal((max_seq, kvh * d)).astype(np.float32) * 0.5)
+    v = gen.activations(rng, max_seq, kvh * d)
+    dk, dv = dev(hip, k), dev(hip, v)
+    out = hip.DeviceArray(qh * d, np.uint16)
+    pos = dev(hip, np.array([length - 1], np.int32))
+    hip.call("qwen3_tts_op_attention", exact, dev(hip, q).ptr, qh * d, ptr_array(hip, [dk.ptr]).ptr,
+             ptr_array(hip, [dv.ptr]).ptr, pos.ptr, out.ptr, 1, qh, kvh, d, max_seq, None)
+    ref = orc.attention(q, k[:length], v[:length], qh, kvh, d, length, exact=bool(exact))
+    assert np.array_equal(out.numpy(), ref)
+
+
 def test_attention_rows_with_own_caches(hip, orc):
     rng = np.random.default_rng(9)
     qh, kvh, d, max_seq, rows = 16, 8, 128, 64, 3
