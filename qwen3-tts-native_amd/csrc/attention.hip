@@ -9,7 +9,7 @@
 //   values   one wave per (row, kv head, slice of the head dimension): lanes
 //            are (query head of the group, dimension) pairs, each running the
 //            reference's sequential fma chain over positions.  Value rows are
-//            streamed through a 32-deep register ring (16-byte loads, 32 KB
+//            streamed through a 16-deep register ring (16-byte loads, 16 KB
 //            in flight per wave) and transposed through LDS.
 //
 // Caches of at most 64 positions (the code predictor's) run all three phases
@@ -38,7 +38,7 @@ namespace {
 constexpr int kDim = 128;
 constexpr int kScoreLanes = 64;   // positions per score block
 constexpr int kSoftmaxThreads = 256;
-constexpr int kRing = 32;         // value loads in flight per lane
+constexpr int kRing = 16;         // value loads in flight per lane
 constexpr int kMaxCapacity = 12288;
 
 struct AttnArgs {
@@ -148,88 +148,33 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     }
 }
 
-// ---------------------------------------------------------------------------
-// softmax: grid (query heads, rows), 256 threads
-// ---------------------------------------------------------------------------
-template <bool kExact>
-__global__ __launch_bounds__(kSoftmaxThreads) void attention_softmax_kernel(AttnArgs a) {
-    extern __shared__ __align__(16) float e_lds[];
-    __shared__ float reduction[kSoftmaxThreads];
-    __shared__ float broadcast;
-    const int row = blockIdx.y;
-    const int head = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int length = row_length(a, row);
-    float* s = a.scores + (static_cast<size_t>(row) * a.query_heads + head) * a.capacity;
+// Row stride of the probability table in LDS: room for whole chunks, 16-byte
+// aligned, and offset by four banks between query heads.
+__host__ __device__ constexpr int lds_stride(int capacity) { return (capacity + 31) / 32 * 32 + 4; }
 
-    float local_max = -INFINITY;
-    for (int p = tid; p < length; p += kSoftmaxThreads) {
-        const float v = s[p];
-        if constexpr (kExact) e_lds[p] = v;
-        local_max = fmaxf(local_max, v);
-    }
-    reduction[tid] = local_max;
-    __syncthreads();
-    for (int w = kSoftmaxThreads / 2; w > 0; w >>= 1) {
-        if (tid < w) reduction[tid] = fmaxf(reduction[tid], reduction[tid + w]);
-        __syncthreads();
-    }
-    const float maximum = reduction[0];
-    __syncthreads();
-    if constexpr (kExact) {
-        for (int p = tid; p < length; p += kSoftmaxThreads) e_lds[p] = q3_expf(e_lds[p] - maximum);
-        __syncthreads();
-        if (tid == 0) {
-            float denominator = 0.0f;
-            int p = 0;
-#pragma unroll 4
-            for (; p + 4 <= length; p += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(e_lds + p);
-                denominator += v.x;
-                denominator += v.y;
-                denominator += v.z;
-                denominator += v.w;
-            }
-            for (; p < length; ++p) denominator += e_lds[p];
-            broadcast = 1.0f / denominator;
-        }
-        __syncthreads();
-        const float inverse = broadcast;
-        for (int p = tid; p < length; p += kSoftmaxThreads) s[p] = round_bf(e_lds[p] * inverse);
-    } else {
-        float local = 0.0f;
-        for (int p = tid; p < length; p += kSoftmaxThreads) {
-            const float w = q3_expf(s[p] - maximum);
-            s[p] = w;
-            local += w;
-        }
-        reduction[tid] = local;
-        __syncthreads();
-        for (int w = kSoftmaxThreads / 2; w > 0; w >>= 1) {
-            if (tid < w) reduction[tid] += reduction[tid + w];
-            __syncthreads();
-        }
-        if (tid == 0) a.inverse[static_cast<size_t>(row) * a.query_heads + head] = 1.0f / reduction[0];
-    }
+// Wave-wide max (order independent).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
 }
 
-// Row stride of the probability table in LDS: 16-byte aligned and offset by
-// four banks between query heads.
-__host__ __device__ constexpr int lds_stride(int capacity) { return (capacity + 3) / 4 * 4 + 4; }
-
 // ---------------------------------------------------------------------------
-// values: grid (kv heads * 2G slices, rows), one wave.  Lane = (g, dim):
-// g = lane / (64/G), dim = slice * (64/G) + lane % (64/G).  One 16-byte load
-// per lane covers 8 dims of one position, so one wave load covers 8G
-// positions ("a chunk").
+// softmax + values: grid (kv heads * 2G slices, rows), one wave.
+// Lane = (g, dim): g = lane / (64/G), dim = slice * (64/G) + lane % (64/G).
+// One 16-byte load per lane covers 8 dims of one position, so one wave load
+// covers 8G positions ("a chunk").  The value ring is requested first; the
+// softmax of the group's G heads (redone by each of the 2G slice waves, in
+// parallel) runs while it is in flight.
 // ---------------------------------------------------------------------------
 template <bool kExact, int kG>
-__global__ __launch_bounds__(64) void attention_values_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     constexpr int kSliceDims = 64 / kG;
     constexpr int kLanesPerPos = kSliceDims / 8;
-    constexpr int kPosPerChunk = 64 / kLanesPerPos;
-    extern __shared__ __align__(16) float p_lds[];  // [kG][stride] probabilities
-    __shared__ __align__(16) bf16_t v_lds[2][kPosPerChunk * kSliceDims];
+    constexpr int kPos = 64 / kLanesPerPos;  // positions per chunk
+    extern __shared__ __align__(16) float p_lds[];  // [kG][stride]
+    __shared__ __align__(16) bf16_t v_lds[2][kPos * kSliceDims];
+    __shared__ float inverse_lds[kG];
     const int row = blockIdx.y;
     const int kvh = blockIdx.x / (2 * kG);
     const int slice = blockIdx.x % (2 * kG);
@@ -238,11 +183,31 @@ __global__ __launch_bounds__(64) void attention_values_kernel(AttnArgs a) {
     const int dl = lane % kSliceDims;
     const int length = row_length(a, row);
     const int stride = lds_stride(a.capacity);
+    const int chunks = (length + kPos - 1) / kPos;
+
+    // 1. value ring: chunks 0..kRing-1 in flight
+    const int kv_width = a.key_value_heads * kDim;
+    const bf16_t* vbase = row_values(a, row) + static_cast<size_t>(kvh) * kDim + slice * kSliceDims +
+                          (lane % kLanesPerPos) * 8;
+    const int lane_pos = lane / kLanesPerPos;
+    auto load = [&](int c) {
+        int pos = c * kPos + lane_pos;
+        pos = pos < length ? pos : length - 1;  // never past this row's last written position
+        return load_global16(vbase + static_cast<size_t>(pos) * kv_width);
+    };
+    uint4 ring[kRing];
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) ring[k] = load(k);
+    asm volatile("" ::: "memory");  // in flight before the scores are requested
+
+    // 2. scores of the group's heads into LDS, 16 loads in flight per lane
     const float* scores = a.scores + (static_cast<size_t>(row) * a.query_heads + static_cast<size_t>(kvh) * kG) *
                                          a.capacity;
-    // Probabilities into LDS, 16 loads in flight per lane.
+    float maximum[kG];
+#pragma unroll
     for (int gg = 0; gg < kG; ++gg) {
         const float* src = scores + static_cast<size_t>(gg) * a.capacity;
+        float m = -INFINITY;
         for (int base = 0; base < length; base += 16 * 64) {
             float t[16];
 #pragma unroll
@@ -253,58 +218,148 @@ __global__ __launch_bounds__(64) void attention_values_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 const int p = base + u * 64 + lane;
-                if (p < length) p_lds[gg * stride + p] = t[u];
+                if (p < length) {
+                    p_lds[gg * stride + p] = t[u];
+                    m = fmaxf(m, t[u]);
+                }
+            }
+        }
+        maximum[gg] = wave_max(m);
+    }
+
+    // 3. exponentials (each lane its own positions), then the normalizer
+    float* eg = p_lds;
+    float partial[kG][4];
+#pragma unroll
+    for (int gg = 0; gg < kG; ++gg) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) partial[gg][j] = 0.0f;
+        for (int base = 0; base < length; base += 8 * 64) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = base + u * 64 + lane;
+                t[u] = p < length ? eg[gg * stride + p] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = base + u * 64 + lane;
+                if (p < length) {
+                    const float w = q3_expf(t[u] - maximum[gg]);
+                    eg[gg * stride + p] = w;
+                    if constexpr (!kExact) partial[gg][(p >> 6) & 3] += w;  // thread (p mod 256)'s partial
+                }
             }
         }
     }
     __syncthreads();
-
-    const int kv_width = a.key_value_heads * kDim;
-    const bf16_t* vbase = row_values(a, row) + static_cast<size_t>(kvh) * kDim + slice * kSliceDims +
-                          (lane % kLanesPerPos) * 8;
-    const int lane_pos = lane / kLanesPerPos;
-    const int chunks = (length + kPosPerChunk - 1) / kPosPerChunk;
-    auto load = [&](int c) {
-        int pos = c * kPosPerChunk + lane_pos;
-        pos = pos < length ? pos : length - 1;  // never past this row's last written position
-        return load_global16(vbase + static_cast<size_t>(pos) * kv_width);
-    };
-    uint4 ring[kRing];
+    if constexpr (kExact) {
+        // thread 0 of the reference's block: one sequential sum per head, the
+        // G heads in G lanes of the same instructions
+        if (lane < kG) {
+            const float* e = p_lds + lane * stride;
+            float denominator = 0.0f;
+            int p = 0;
+            for (; p + 16 <= length; p += 16) {
+                float4 v[4];
 #pragma unroll
-    for (int k = 0; k < kRing; ++k) ring[k] = load(k);
+                for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(e + p + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    denominator += v[u].x;
+                    denominator += v[u].y;
+                    denominator += v[u].z;
+                    denominator += v[u].w;
+                }
+            }
+            for (; p < length; ++p) denominator += e[p];
+            inverse_lds[lane] = 1.0f / denominator;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int gg = 0; gg < kG; ++gg) {
+            const float inverse = inverse_lds[gg];
+            for (int p = lane; p < length; p += 64) eg[gg * stride + p] = round_bf(eg[gg * stride + p] * inverse);
+        }
+    } else {
+        // 256 strided partials: lane l holds those of threads l, l+64,
+        // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
+        // local, the rest a wave tree.
+#pragma unroll
+        for (int gg = 0; gg < kG; ++gg) {
+            float p0 = partial[gg][0] + partial[gg][2];
+            float p1 = partial[gg][1] + partial[gg][3];
+            float value = p0 + p1;
+#pragma unroll
+            for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_down(value, offset, 64);
+            if (lane == 0) inverse_lds[gg] = 1.0f / value;
+        }
+    }
+    __syncthreads();
 
+    // 4. the value chains.  Chunk c+1 is written to LDS and read into
+    // registers while chunk c is being accumulated.
     const float* pg = p_lds + g * stride;
     float acc = 0.0f;
-    for (int base = 0; base < chunks; base += kRing) {
+    float vcur[kPos], pcur[kPos], vnext[kPos], pnext[kPos];
+    auto fetch = [&](const bf16_t* slot, int c, float* v, float* pv) {
+#pragma unroll
+        for (int j = 0; j < kPos; ++j) v[j] = bf2f(slot[j * kSliceDims + dl]);
+#pragma unroll
+        for (int j = 0; j < kPos; j += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(pg + c * kPos + j);
+            pv[j] = t.x;
+            pv[j + 1] = t.y;
+            pv[j + 2] = t.z;
+            pv[j + 3] = t.w;
+        }
+    };
+    auto accumulate = [&](int c, const float* v, const float* pv) {
+        const int first = c * kPos;
+        if (first + kPos <= length) {
+#pragma unroll
+            for (int j = 0; j < kPos; ++j) acc = fmaf(pv[j], v[j], acc);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kPos; ++j) {
+                if (first + j < length) acc = fmaf(pv[j], v[j], acc);
+            }
+        }
+    };
+    reinterpret_cast<uint4*>(v_lds[0])[lane] = ring[0];
+    ring[0] = load(kRing);
+    asm volatile("" ::: "memory");
+    fetch(v_lds[0], 0, vcur, pcur);
+    bool done = false;
+    for (int base = 0; !done; base += kRing) {
 #pragma unroll
         for (int k = 0; k < kRing; ++k) {
             const int c = base + k;
-            bf16_t* slot = v_lds[k & 1];
-            reinterpret_cast<uint4*>(slot)[lane] = ring[k];
-            ring[k] = load(c + kRing);
-            // issue the refill here, not where its value is next needed
-            asm volatile("" ::: "memory");
-            const int first = c * kPosPerChunk;
-            if (first + kPosPerChunk <= length) {
-#pragma unroll
-                for (int j = 0; j < kPosPerChunk; j += 4) {
-                    const float4 pv = *reinterpret_cast<const float4*>(pg + first + j);
-                    acc = fmaf(pv.x, bf2f(slot[(j + 0) * kSliceDims + dl]), acc);
-                    acc = fmaf(pv.y, bf2f(slot[(j + 1) * kSliceDims + dl]), acc);
-                    acc = fmaf(pv.z, bf2f(slot[(j + 2) * kSliceDims + dl]), acc);
-                    acc = fmaf(pv.w, bf2f(slot[(j + 3) * kSliceDims + dl]), acc);
-                }
-            } else if (first < length) {
-                for (int j = 0; first + j < length; ++j) {
-                    acc = fmaf(pg[first + j], bf2f(slot[j * kSliceDims + dl]), acc);
-                }
+            const int kNext = (k + 1) % kRing;
+            // stage chunk c+1 (its ring slot is kNext); past the last chunk
+            // this only re-reads valid rows and stays unused
+            bf16_t* slot = v_lds[(k + 1) & 1];
+            reinterpret_cast<uint4*>(slot)[lane] = ring[kNext];
+            ring[kNext] = load(c + 1 + kRing);
+            asm volatile("" ::: "memory");  // issue the refill here
+            const int next = c + 1 < chunks ? c + 1 : chunks - 1;
+            if (k % 2 == 0) {
+                fetch(slot, next, vnext, pnext);
+                accumulate(c, vcur, pcur);
+            } else {
+                fetch(slot, next, vcur, pcur);
+                accumulate(c, vnext, pnext);
+            }
+            if (c + 1 >= chunks) {
+                done = true;
+                break;
             }
         }
     }
     const int head = kvh * kG + g;
     const int dim = slice * kSliceDims + dl;
     float y = acc;
-    if constexpr (!kExact) y = acc * a.inverse[static_cast<size_t>(row) * a.query_heads + head];
+    if constexpr (!kExact) y = acc * inverse_lds[g];
     a.output[(static_cast<size_t>(row) * a.query_heads + head) * kDim + dim] = f2bf(y);
 }
 
@@ -419,19 +474,16 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
 
 template <bool kExact, int kG>
 hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
-    const size_t softmax_lds = kExact ? static_cast<size_t>(a.capacity) * sizeof(float) : 0;
-    const size_t values_lds = static_cast<size_t>(kG) * lds_stride(a.capacity) * sizeof(float);
+    const size_t head_lds = static_cast<size_t>(kG) * lds_stride(a.capacity) * sizeof(float);
     // LDS: up to 160 KB per workgroup on gfx950 (the value ring's 2 KB
     // static slots included).
     constexpr size_t kLdsLimit = 160 * 1024 - 2048 - 64;
-    if (softmax_lds > kLdsLimit || values_lds > kLdsLimit) return hipErrorInvalidValue;
+    if (head_lds > kLdsLimit) return hipErrorInvalidValue;
     static bool configured = false;
     if (!configured) {
-        hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_softmax_kernel<kExact>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsLimit));
-        if (st != hipSuccess) return st;
-        st = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_values_kernel<kExact, kG>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsLimit));
+        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_head_kernel<kExact, kG>),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(kLdsLimit));
         if (st != hipSuccess) return st;
         configured = true;
     }
@@ -441,8 +493,7 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
     }
     const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.key_value_heads, rows);
     attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
-    attention_softmax_kernel<kExact><<<dim3(a.query_heads, rows), kSoftmaxThreads, softmax_lds, stream>>>(a);
-    attention_values_kernel<kExact, kG><<<dim3(a.key_value_heads * 2 * kG, rows), 64, values_lds, stream>>>(a);
+    attention_head_kernel<kExact, kG><<<dim3(a.key_value_heads * 2 * kG, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
 }
 

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     __shared__ int s_above;
     __shared__ int s_count;
     __shared__ int s_best;
+    __shared__ double s_target;
 
     const int tid = threadIdx.x;
     const int V = a.vocabulary;
@@ -195,18 +196,47 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                 }
             }
             __syncthreads();
-            if (tid == 0) {
-                int cumulative = s_above;
-                int chosen = 0;
-                for (int b = 255; b >= 0; --b) {
-                    if (cumulative + static_cast<int>(hist[b]) >= selections) {
-                        chosen = b;
-                        break;
-                    }
-                    cumulative += static_cast<int>(hist[b]);
+            if (tid < 64) {
+                // Scan the bins from the top (bin 255 first) in wave 0: lane l
+                // holds bins 255-4l .. 252-4l.  Integer counts, so the
+                // parallel prefix equals the sequential scan.
+                const int lane = tid;
+                int h[4];
+                int lane_total = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    h[j] = static_cast<int>(hist[255 - 4 * lane - j]);
+                    lane_total += h[j];
                 }
-                s_above = cumulative;
-                s_prefix = prefix | (static_cast<uint32_t>(chosen) << shift);
+                int inclusive = lane_total;
+#pragma unroll
+                for (int offset = 1; offset < 64; offset <<= 1) {
+                    const int other = __shfl_up(inclusive, offset, 64);
+                    if (lane >= offset) inclusive += other;
+                }
+                const int base_above = s_above;
+                int before = base_above + inclusive - lane_total;
+                int found = -1;
+                int found_before = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (found < 0 && before + h[j] >= selections) {
+                        found = j;
+                        found_before = before;
+                    }
+                    before += h[j];
+                }
+                const unsigned long long hits = __ballot(found >= 0);
+                const int first = hits ? __ffsll(static_cast<long long>(hits)) - 1 : -1;
+                if (first < 0) {
+                    if (lane == 63) {  // no bin reaches the count: chosen 0, all bins above
+                        s_above = before;
+                        s_prefix = prefix;
+                    }
+                } else if (lane == first) {
+                    s_above = found_before;
+                    s_prefix = prefix | (static_cast<uint32_t>(255 - 4 * lane - found) << shift);
+                }
             }
             __syncthreads();
         }
@@ -249,7 +279,46 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
             weights[r] = exp(static_cast<double>(sorted_v[r] / a.temperature - maximum));
         }
         __syncthreads();
-        if (tid == 0) {
+        if (selections <= 64) {
+            // Wave 0 runs the reference's sequential double sums as uniform
+            // loops, reading weight r from lane r (no memory round trip per
+            // term); every lane computes the same values.
+            if (tid < 64) {
+                const double own = tid < selections ? weights[tid] : 0.0;
+                const int own_lo = __double2loint(own);
+                const int own_hi = __double2hiint(own);
+                auto weight = [&](int r) {
+                    return __hiloint2double(__builtin_amdgcn_readlane(own_hi, r), __builtin_amdgcn_readlane(own_lo, r));
+                };
+                double denominator = 0.0;
+                for (int r = 0; r < selections; ++r) denominator += weight(r);
+                double cumulative = 0.0;
+                int retained = selections;
+                for (int r = 0; r < selections; ++r) {
+                    cumulative += weight(r) / denominator;
+                    if (cumulative >= static_cast<double>(a.top_p)) {
+                        retained = r + 1;
+                        break;
+                    }
+                }
+                double retained_total = 0.0;
+                for (int r = 0; r < retained; ++r) retained_total += weight(r);
+                if (tid == 0) s_target = static_cast<double>(uniform_random(a.random_state)) * retained_total;
+                // the draw is made by lane 0 only; broadcast it through LDS
+                __builtin_amdgcn_wave_barrier();
+                const double target = s_target;
+                cumulative = 0.0;
+                int choice = sorted_i[retained - 1];
+                for (int r = 0; r < retained; ++r) {
+                    cumulative += weight(r);
+                    if (cumulative >= target) {
+                        choice = sorted_i[r];
+                        break;
+                    }
+                }
+                if (tid == 0) s_best = choice;
+            }
+        } else if (tid == 0) {
             double denominator = 0.0;
             for (int r = 0; r < selections; ++r) denominator += weights[r];
             double cumulative = 0.0;
