@@ -385,6 +385,21 @@ QWEN3_TTS_API int32_t qwen3_tts_op_attention(
     uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
     int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
     int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
+/* qk_norm_rope_kv_append followed by attention, as one fused decode step:
+ * qkv holds the raw fused q|k|v rows (row stride qkv_stride); query heads are
+ * head-normalized and rotated, the key of position positions[row] is
+ * normalized, rotated and appended to the caches with its value, then
+ * attention runs over positions 0..positions[row].  Results and cache
+ * contents are identical to the two separate ops; the query part of qkv is
+ * left unrotated.  Replaces the head norm / RoPE / cache append / attention
+ * sequence at talker.cu:3298-3380 (single session) and talker.cu:2100-2195
+ * (batched). */
+QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention(
+    int32_t exact, const uint16_t* qkv, int32_t qkv_stride, const uint16_t* q_norm,
+    const uint16_t* k_norm, const uint16_t* rope_table, float epsilon, uint16_t* const* key_bases,
+    uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
+    int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
+    int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
 QWEN3_TTS_API int32_t qwen3_tts_op_kv_scatter_rows(
     const uint16_t* rows_data, uint16_t* const* cache_bases, const int32_t* positions,
     int32_t rows, int32_t width, int32_t row_stride, void* stream, char* error,

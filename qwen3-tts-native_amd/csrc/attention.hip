@@ -31,13 +31,13 @@
 // bit of the result.
 #include "q3_common.hpp"
 #include "q3_math.h"
+#include "head_device.hpp"
 
 namespace q3 {
 namespace {
 
 constexpr int kDim = 128;
 constexpr int kScoreLanes = 64;   // positions per score block
-constexpr int kSoftmaxThreads = 256;
 constexpr int kRing = 16;         // value loads in flight per lane
 constexpr int kMaxCapacity = 12288;
 
@@ -57,6 +57,14 @@ struct AttnArgs {
     float scale;
     float* scores;   // [rows][query_heads][capacity]
     float* inverse;  // [rows][query_heads] (fast variant)
+    // Fused QKV epilogue: `query` is the raw fused q|k|v row; the query heads
+    // are normalized and rotated here, and the current position's key
+    // (normalized, rotated) and value are appended to the caches and used
+    // directly.  Null q_norm: `query` is final and the caches are complete.
+    const bf16_t* q_norm;
+    const bf16_t* k_norm;
+    const bf16_t* rope_table;  // [positions][64][cos, sin] bf16
+    float epsilon;
 };
 
 __device__ __forceinline__ int row_length(const AttnArgs& a, int row) {
@@ -80,6 +88,30 @@ __device__ __forceinline__ uint4 load_global16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Appends the current position's key and value of kv head `kvh` (one full
+// wave); returns this lane's key and value elements lane and lane+64.
+__device__ __forceinline__ void append_kv(const AttnArgs& a, int row, int kvh, int position, bf16_t& k0,
+                                          bf16_t& k1, bf16_t& v0, bf16_t& v1) {
+    constexpr int kDim = 128;
+    const int lane = threadIdx.x & 63;
+    const int kv_width = a.key_value_heads * kDim;
+    const bf16_t* raw = a.query + static_cast<size_t>(row) * a.query_stride +
+                        static_cast<size_t>(a.query_heads) * kDim;
+    head_detail::norm_rope_head(raw + static_cast<size_t>(kvh) * kDim, a.k_norm,
+                                a.rope_table + static_cast<size_t>(position) * kDim, a.epsilon, k0, k1);
+    const bf16_t* vraw = raw + kv_width + static_cast<size_t>(kvh) * kDim;
+    v0 = vraw[lane];
+    v1 = vraw[lane + 64];
+    bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
+                   static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+    bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
+                   static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+    kdst[lane] = k0;
+    kdst[lane + 64] = k1;
+    vdst[lane] = v0;
+    vdst[lane + 64] = v1;
+}
+
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
@@ -94,14 +126,14 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     const int p0 = blockIdx.x * kScoreLanes;
     if (p0 >= length) return;
     __shared__ float q_lds[kG][kDim];
+    __shared__ uint32_t knew_lds[kDim / 2];
     const int lane = threadIdx.x;
-    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
-    for (int i = lane; i < kG * kDim; i += kScoreLanes) q_lds[i / kDim][i % kDim] = bf2f(q[i]);
-    __syncthreads();
+    const int position = length - 1;
     const int p = p0 + lane;
-    if (p >= length) return;
     const int kv_width = a.key_value_heads * kDim;
-    const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(p) * kv_width +
+    // key row first (independent of the query)
+    const int prow = p < length ? p : position;
+    const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(prow) * kv_width +
                                                      static_cast<size_t>(kvh) * kDim);
     uint32_t kw[64];
 #pragma unroll
@@ -111,6 +143,32 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
         kw[4 * v + 1] = t.y;
         kw[4 * v + 2] = t.z;
         kw[4 * v + 3] = t.w;
+    }
+    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
+    const bool fused = a.q_norm != nullptr;
+    if (fused) {
+        const bf16_t* cs = a.rope_table + static_cast<size_t>(position) * kDim;
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+            bf16_t q0, q1;
+            head_detail::norm_rope_head(q + g * kDim, a.q_norm, cs, a.epsilon, q0, q1);
+            q_lds[g][lane] = bf2f(q0);
+            q_lds[g][lane + 64] = bf2f(q1);
+        }
+        if (position >= p0 && position < p0 + kScoreLanes) {
+            bf16_t k0, k1, v0, v1;
+            append_kv(a, row, kvh, position, k0, k1, v0, v1);
+            reinterpret_cast<bf16_t*>(knew_lds)[lane] = k0;
+            reinterpret_cast<bf16_t*>(knew_lds)[lane + 64] = k1;
+        }
+    } else {
+        for (int i = lane; i < kG * kDim; i += kScoreLanes) q_lds[i / kDim][i % kDim] = bf2f(q[i]);
+    }
+    __syncthreads();
+    if (p >= length) return;
+    if (fused && p == position) {
+#pragma unroll
+        for (int i = 0; i < 64; ++i) kw[i] = knew_lds[i];
     }
     float* out = a.scores + (static_cast<size_t>(row) * a.query_heads + static_cast<size_t>(kvh) * kG) * a.capacity + p;
 #pragma unroll
@@ -381,22 +439,53 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     const int tid = threadIdx.x;
     const int length = row_length(a, row);
     const int kv_width = a.key_value_heads * kDim;
+    const int position = length - 1;
+    __shared__ uint32_t knew_lds[kDim / 2];
+    __shared__ bf16_t vnew_lds[kDim];
+    // key row of this lane's (g, p) first
+    const int g_score = tid / length;
+    const int p_score = tid % length;
+    const int krow = tid < kG * length ? p_score : position;
+    const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(krow) * kv_width +
+                                                     static_cast<size_t>(kvh) * kDim);
+    uint32_t kw[64];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const uint4 t = load_global16(k4 + v);
+        kw[4 * v + 0] = t.x;
+        kw[4 * v + 1] = t.y;
+        kw[4 * v + 2] = t.z;
+        kw[4 * v + 3] = t.w;
+    }
     const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
-    q_lds[tid / kDim][tid % kDim] = bf2f(q[tid]);
+    const bool fused = a.q_norm != nullptr;
+    if (fused) {
+        const int wave = tid >> 6;
+        const int lane = tid & 63;
+        if (wave < kG) {
+            bf16_t q0, q1;
+            head_detail::norm_rope_head(q + wave * kDim, a.q_norm, a.rope_table + static_cast<size_t>(position) * kDim,
+                                        a.epsilon, q0, q1);
+            q_lds[wave][lane] = bf2f(q0);
+            q_lds[wave][lane + 64] = bf2f(q1);
+        } else if (wave == kG) {
+            bf16_t k0, k1, v0, v1;
+            append_kv(a, row, kvh, position, k0, k1, v0, v1);
+            reinterpret_cast<bf16_t*>(knew_lds)[lane] = k0;
+            reinterpret_cast<bf16_t*>(knew_lds)[lane + 64] = k1;
+            vnew_lds[lane] = v0;
+            vnew_lds[lane + 64] = v1;
+        }
+    } else {
+        q_lds[tid / kDim][tid % kDim] = bf2f(q[tid]);
+    }
     __syncthreads();
     if (tid < kG * length) {
-        const int g = tid / length;
-        const int p = tid % length;
-        const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(p) * kv_width +
-                                                         static_cast<size_t>(kvh) * kDim);
-        uint32_t kw[64];
+        const int g = g_score;
+        const int p = p_score;
+        if (fused && p == position) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint4 t = load_global16(k4 + v);
-            kw[4 * v + 0] = t.x;
-            kw[4 * v + 1] = t.y;
-            kw[4 * v + 2] = t.z;
-            kw[4 * v + 3] = t.w;
+            for (int i = 0; i < 64; ++i) kw[i] = knew_lds[i];
         }
         const float* qg = q_lds[g];
         float score;
@@ -456,16 +545,20 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     }
     __syncthreads();
     const bf16_t* vcol = row_values(a, row) + static_cast<size_t>(kvh) * kDim + d;
+    // fused: the current position's value comes from LDS (its cache row is
+    // written by this block)
+    const int cached = fused ? position : length;
     float acc = 0.0f;
     int p = 0;
-    for (; p + 8 <= length; p += 8) {
+    for (; p + 8 <= cached; p += 8) {
         float vv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) vv[u] = bf2f(vcol[static_cast<size_t>(p + u) * kv_width]);
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc = fmaf(prob[g][p + u], vv[u], acc);
     }
-    for (; p < length; ++p) acc = fmaf(prob[g][p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
+    for (; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
+    if (fused) acc = fmaf(prob[g][position], bf2f(vnew_lds[d]), acc);
     const int head = kvh * kG + g;
     float y = acc;
     if constexpr (!kExact) y = acc * inverse_lds[g];
@@ -503,13 +596,53 @@ size_t attention_workspace_bytes(int rows, int query_heads, int capacity) {
     return static_cast<size_t>(rows) * query_heads * (static_cast<size_t>(capacity) + 1) * sizeof(float);
 }
 
+namespace {
+
+hipError_t dispatch(bool exact, const AttnArgs& a, int rows, hipStream_t stream) {
+    switch (a.query_heads / a.key_value_heads) {
+        case 1: return exact ? launch_variant<true, 1>(a, rows, stream) : launch_variant<false, 1>(a, rows, stream);
+        case 2: return exact ? launch_variant<true, 2>(a, rows, stream) : launch_variant<false, 2>(a, rows, stream);
+        case 4: return exact ? launch_variant<true, 4>(a, rows, stream) : launch_variant<false, 4>(a, rows, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool valid_shape(int rows, int query_heads, int key_value_heads, int head_dimension, int capacity,
+                 const float* workspace) {
+    return head_dimension == kDim && key_value_heads > 0 && query_heads % key_value_heads == 0 && rows > 0 &&
+           capacity > 0 && capacity <= kMaxCapacity && workspace != nullptr;
+}
+
+AttnArgs base_args(const bf16_t* query, int query_stride, bf16_t* const* key_bases, bf16_t* const* value_bases,
+                   const bf16_t* key_cache, const bf16_t* value_cache, const int* positions, int fixed_length,
+                   bf16_t* output, int rows, int query_heads, int key_value_heads, int capacity, float* workspace) {
+    AttnArgs a{};
+    a.query = query;
+    a.query_stride = query_stride;
+    a.key_bases = key_bases;
+    a.value_bases = value_bases;
+    a.key_cache = key_cache;
+    a.value_cache = value_cache;
+    a.positions = positions;
+    a.fixed_length = fixed_length;
+    a.output = output;
+    a.query_heads = query_heads;
+    a.key_value_heads = key_value_heads;
+    a.capacity = capacity;
+    a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
+    a.scores = workspace;
+    a.inverse = workspace + static_cast<size_t>(rows) * query_heads * capacity;
+    return a;
+}
+
+}  // namespace
+
 hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride, bf16_t* const* key_bases,
                             bf16_t* const* value_bases, const bf16_t* key_cache, const bf16_t* value_cache,
                             const int* positions, int fixed_sequence_length, bf16_t* output, int rows,
                             int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,
                             float* workspace, hipStream_t stream) {
-    if (head_dimension != kDim || key_value_heads <= 0 || query_heads % key_value_heads != 0 || rows <= 0 ||
-        max_sequence_length <= 0 || max_sequence_length > kMaxCapacity || workspace == nullptr ||
+    if (!valid_shape(rows, query_heads, key_value_heads, head_dimension, max_sequence_length, workspace) ||
         query == nullptr || output == nullptr) {
         return hipErrorInvalidValue;
     }
@@ -518,29 +651,32 @@ hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride, b
     if (positions == nullptr && (fixed_sequence_length <= 0 || fixed_sequence_length > max_sequence_length)) {
         return hipErrorInvalidValue;
     }
-    AttnArgs a;
-    a.query = query;
-    a.query_stride = query_stride;
-    a.key_bases = key_bases;
-    a.value_bases = value_bases;
-    a.key_cache = key_cache;
-    a.value_cache = value_cache;
-    a.positions = positions;
-    a.fixed_length = fixed_sequence_length;
-    a.output = output;
-    a.query_heads = query_heads;
-    a.key_value_heads = key_value_heads;
-    a.capacity = max_sequence_length;
-    a.scale = 1.0f / sqrtf(static_cast<float>(head_dimension));
-    a.scores = workspace;
-    a.inverse = workspace + static_cast<size_t>(rows) * query_heads * max_sequence_length;
-    const int group = query_heads / key_value_heads;
-    switch (group) {
-        case 1: return exact ? launch_variant<true, 1>(a, rows, stream) : launch_variant<false, 1>(a, rows, stream);
-        case 2: return exact ? launch_variant<true, 2>(a, rows, stream) : launch_variant<false, 2>(a, rows, stream);
-        case 4: return exact ? launch_variant<true, 4>(a, rows, stream) : launch_variant<false, 4>(a, rows, stream);
-        default: return hipErrorInvalidValue;
+    const AttnArgs a = base_args(query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
+                                 fixed_sequence_length, output, rows, query_heads, key_value_heads,
+                                 max_sequence_length, workspace);
+    return dispatch(exact, a, rows, stream);
+}
+
+hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                   const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                   bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
+                                   const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
+                                   int query_heads, int key_value_heads, int head_dimension, int capacity,
+                                   float* workspace, hipStream_t stream) {
+    if (!valid_shape(rows, query_heads, key_value_heads, head_dimension, capacity, workspace) || qkv == nullptr ||
+        output == nullptr || q_norm == nullptr || k_norm == nullptr || rope_table == nullptr ||
+        positions == nullptr) {
+        return hipErrorInvalidValue;
     }
+    if ((key_bases == nullptr) != (value_bases == nullptr)) return hipErrorInvalidValue;
+    if (key_bases == nullptr && (key_cache == nullptr || value_cache == nullptr)) return hipErrorInvalidValue;
+    AttnArgs a = base_args(qkv, qkv_stride, key_bases, value_bases, key_cache, value_cache, positions, 0, output,
+                           rows, query_heads, key_value_heads, capacity, workspace);
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.rope_table = rope_table;
+    a.epsilon = epsilon;
+    return dispatch(exact, a, rows, stream);
 }
 
 }  // namespace q3

@@ -292,12 +292,6 @@ __global__ __launch_bounds__(kThreads, 1) void persistent_chain_kernel(const Cha
     }
 }
 
-__global__ void zero_sync_kernel(unsigned* barrier, int* status) {
-    if (threadIdx.x == 0) {
-        *barrier = 0u;
-        *status = 0;
-    }
-}
 
 // Zeroes a larger synchronization area (counters, group counters, flags).
 __global__ void zero_words_kernel(unsigned* words, int count) {

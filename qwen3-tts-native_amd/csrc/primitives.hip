@@ -7,25 +7,14 @@
 // positions so a frame can be replayed as a hipGraph).
 #include "q3_common.hpp"
 #include "q3_math.h"
+#include "head_device.hpp"
 
 namespace q3 {
 namespace {
 
 constexpr int kThreads = 256;
 
-// Exact emulation of the reference's 256-thread block_sum tree
-// (talker_kernels.cu:14-25) by one wave64: `part[j]` is virtual thread
-// lane + 64*j.  Result is broadcast to every lane.
-__device__ __forceinline__ float wave_tree256(float p0, float p1, float p2, float p3) {
-    p0 += p2;
-    p1 += p3;
-    float value = p0 + p1;
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 64);
-    }
-    return __shfl(value, 0, 64);
-}
+using head_detail::wave_tree256;
 
 // rms_norm_kernel (talker_kernels.cu:27-48), one wave64 per row.
 __global__ __launch_bounds__(64) void rms_norm_rows_kernel(const bf16_t* input, const bf16_t* weight,
@@ -83,22 +72,8 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(
     }
     const bool is_query = head < query_heads;
     const bf16_t* gain = is_query ? q_norm : k_norm;
-    const float x0 = bf2f(base[lane]);
-    const float x1 = bf2f(base[lane + kHalf]);
-    // 256-thread tree over 128 squares; virtual threads 128..255 hold 0.
-    const float total = wave_tree256(fmaf(x0, x0, 0.0f), fmaf(x1, x1, 0.0f), 0.0f, 0.0f);
-    const float inverse = 1.0f / sqrtf(total / static_cast<float>(kDim) + epsilon);
-    const float first = round_bf(round_bf(x0 * inverse) * bf2f(gain[lane]));
-    const float second = round_bf(round_bf(x1 * inverse) * bf2f(gain[lane + kHalf]));
-    const bf16_t* cs = rope_table + (static_cast<size_t>(position) * kHalf + lane) * 2;
-    const float c = bf2f(cs[0]);
-    const float s = bf2f(cs[1]);
-    const float fc = round_bf(first * c);
-    const float ss = round_bf(second * s);
-    const float sc = round_bf(second * c);
-    const float fs = round_bf(first * s);
-    const bf16_t out0 = f2bf(fc - ss);
-    const bf16_t out1 = f2bf(sc + fs);
+    bf16_t out0, out1;
+    head_detail::norm_rope_head(base, gain, rope_table + static_cast<size_t>(position) * kDim, epsilon, out0, out1);
     if (is_query) {
         base[lane] = out0;
         base[lane + kHalf] = out1;
@@ -325,6 +300,26 @@ hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride
     return attention_with_temporary(exact, query, query_stride, key_bases, value_bases, nullptr, nullptr, positions,
                                     0, output, rows, query_heads, key_value_heads, head_dimension,
                                     max_sequence_length, stream);
+}
+
+hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                      const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                      bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
+                                      bf16_t* output, int rows, int query_heads, int key_value_heads,
+                                      int head_dimension, int max_sequence_length, hipStream_t stream) {
+    if (rows <= 0 || query_heads <= 0 || max_sequence_length <= 0 || key_bases == nullptr ||
+        value_bases == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    void* workspace = nullptr;
+    hipError_t st =
+        hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, max_sequence_length), stream);
+    if (st != hipSuccess) return st;
+    st = launch_decode_attention(exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases, value_bases,
+                                 nullptr, nullptr, positions, output, rows, query_heads, key_value_heads,
+                                 head_dimension, max_sequence_length, static_cast<float*>(workspace), stream);
+    const hipError_t freed = hipFreeAsync(workspace, stream);
+    return st != hipSuccess ? st : freed;
 }
 
 hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,

@@ -148,6 +148,21 @@ hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
                             const int* positions, int fixed_sequence_length, bf16_t* output,
                             int rows, int query_heads, int key_value_heads, int head_dimension,
                             int max_sequence_length, float* workspace, hipStream_t stream);
+// Decode attention with the QKV epilogue fused in: qkv holds the raw fused
+// q|k|v rows; query heads are normalized and rotated, the key of position
+// positions[row] is normalized, rotated and appended with its value, then
+// attention runs over positions 0..positions[row].
+hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                   const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                   bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
+                                   const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
+                                   int query_heads, int key_value_heads, int head_dimension, int capacity,
+                                   float* workspace, hipStream_t stream);
+hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                      const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                      bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
+                                      bf16_t* output, int rows, int query_heads, int key_value_heads,
+                                      int head_dimension, int max_sequence_length, hipStream_t stream);
 hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride, bf16_t* const* key_bases,
                                bf16_t* const* value_bases, const int* positions, bf16_t* output, int rows,
                                int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,

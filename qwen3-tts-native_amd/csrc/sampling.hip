@@ -292,10 +292,15 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                 };
                 double denominator = 0.0;
                 for (int r = 0; r < selections; ++r) denominator += weight(r);
+                // the quotients do not depend on the running sum: one per lane
+                const double share = own / denominator;
+                const int share_lo = __double2loint(share);
+                const int share_hi = __double2hiint(share);
                 double cumulative = 0.0;
                 int retained = selections;
                 for (int r = 0; r < selections; ++r) {
-                    cumulative += weight(r) / denominator;
+                    cumulative += __hiloint2double(__builtin_amdgcn_readlane(share_hi, r),
+                                                   __builtin_amdgcn_readlane(share_lo, r));
                     if (cumulative >= static_cast<double>(a.top_p)) {
                         retained = r + 1;
                         break;

@@ -877,21 +877,16 @@ private:
         const std::vector<Layer>& layers = predictor ? m_.predictor_layers_ : m_.talker_layers_;
         bf16_t* hidden = predictor ? p_hidden_.as<bf16_t>() : hidden_.as<bf16_t>();
         const int cache_rows = predictor ? kCodebooks : max_seq_;
-        bf16_t* const* kb = kv_bases_.as<bf16_t*>() + (predictor ? 2 * cfg_.talker.layers : 0);
-        bf16_t* const* vb = kb + d.layers;
         for (int l = 0; l < d.layers; ++l) {
             const Layer& L = layers[l];
             Gemv(L.qkv, hidden, d.hidden, d.qkv_width(), kEpiStore).norm(L.input_norm, cfg_.eps).to(qkv_.as<bf16_t>()).run(stream_, "QKV GEMV");
-            check_hip(launch_qk_norm_rope_kv_append(qkv_.as<bf16_t>(), L.q_norm, L.k_norm, kb + l, vb + l, position,
-                                                    m_.rope_table_.as<bf16_t>(), 1, d.query_heads, d.key_value_heads,
-                                                    d.head_dimension, cfg_.eps, stream_),
-                      "q/k norm + RoPE + KV append");
             const bf16_t* kc = host_bases_[(predictor ? 2 * cfg_.talker.layers : 0) + l];
             const bf16_t* vc = host_bases_[(predictor ? 2 * cfg_.talker.layers : 0) + d.layers + l];
-            check_hip(launch_attention(true, qkv_.as<bf16_t>(), d.qkv_width(), nullptr, nullptr, kc, vc, position, 0,
-                                       attn_.as<bf16_t>(), 1, d.query_heads, d.key_value_heads, d.head_dimension,
-                                       cache_rows, attn_scratch_.as<float>(), stream_),
-                      "attention");
+            check_hip(launch_decode_attention(true, qkv_.as<bf16_t>(), d.qkv_width(), L.q_norm, L.k_norm,
+                                              m_.rope_table_.as<bf16_t>(), cfg_.eps, nullptr, nullptr, kc, vc, position,
+                                              attn_.as<bf16_t>(), 1, d.query_heads, d.key_value_heads,
+                                              d.head_dimension, cache_rows, attn_scratch_.as<float>(), stream_),
+                      "q/k norm + RoPE + KV append + attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddRounded).to(hidden).run(stream_, "O GEMV");
             Gemv(L.gate_up, hidden, d.hidden, d.intermediate, kEpiSiluRounded).norm(L.post_norm, cfg_.eps).to(act_.as<bf16_t>()).run(stream_, "gate/up GEMV");
             Gemv(L.down, act_.as<bf16_t>(), d.intermediate, d.hidden, kEpiAddRounded).to(hidden).run(stream_, "down GEMV");
@@ -1305,15 +1300,12 @@ private:
             const Layer& L = layers[l];
             Gemv(L.qkv, hidden, d.hidden, d.qkv_width(), kEpiStore).norm(L.input_norm, cfg_.eps).rows(n, mode)
                 .to(qkv_.as<bf16_t>()).run(stream_, "batch QKV GEMV");
-            check_hip(launch_qk_norm_rope_kv_append(qkv_.as<bf16_t>(), L.q_norm, L.k_norm, kv_table(slot0 + l, false),
-                                                    kv_table(slot0 + l, true), pos, m_.rope_table_.as<bf16_t>(), n,
-                                                    d.query_heads, d.key_value_heads, d.head_dimension, cfg_.eps, stream_),
-                      "batch q/k norm + RoPE + KV append");
-            check_hip(launch_attention(false, qkv_.as<bf16_t>(), d.qkv_width(), kv_table(slot0 + l, false),
-                                       kv_table(slot0 + l, true), nullptr, nullptr, pos, 0, attn_.as<bf16_t>(), n,
-                                       d.query_heads, d.key_value_heads, d.head_dimension, capacity,
-                                       attn_scratch_.as<float>(), stream_),
-                      "batch attention");
+            check_hip(launch_decode_attention(false, qkv_.as<bf16_t>(), d.qkv_width(), L.q_norm, L.k_norm,
+                                              m_.rope_table_.as<bf16_t>(), cfg_.eps, kv_table(slot0 + l, false),
+                                              kv_table(slot0 + l, true), nullptr, nullptr, pos, attn_.as<bf16_t>(), n,
+                                              d.query_heads, d.key_value_heads, d.head_dimension, capacity,
+                                              attn_scratch_.as<float>(), stream_),
+                      "batch q/k norm + RoPE + KV append + attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
                 .run(stream_, "batch O GEMV");
             Gemv(L.gate_up, hidden, d.hidden, d.intermediate, kEpiSiluFused).norm(L.post_norm, cfg_.eps).rows(n, mode)

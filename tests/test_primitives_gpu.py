@@ -133,6 +133,51 @@ def test_attention_groups_and_ring_edges(hip, orc, exact, qh, kvh, length, max_s
     assert np.array_equal(out.numpy(), ref)
 
 
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("qh,kvh", [(16, 8), (16, 4)])
+@pytest.mark.parametrize("positions,max_seq", [([0], 16), ([15], 16), ([63], 64), ([64], 100), ([700], 1024),
+                                               ([1023], 1024), ([3, 40, 99], 100)])
+def test_decode_attention_fused_matches_separate_ops(hip, orc, exact, qh, kvh, positions, max_seq):
+    """The fused decode step (head norm + RoPE + KV append + attention) equals
+    qk_norm_rope_kv_append followed by attention: same output, same caches."""
+    rng = np.random.default_rng(sum(positions) * 3 + max_seq + qh // kvh + exact)
+    d = 128
+    qw, kw = qh * d, kvh * d
+    rows = len(positions)
+    qkv = gen.activations(rng, rows, qw + 2 * kw)
+    qn, kn = gen.gains(rng, d), gen.gains(rng, d)
+    table = np.empty(max_seq * d, np.uint16)
+    hip.call("qwen3_tts_rope_table_v1", max_seq, d, C.c_float(1e6), table.ctypes.data)
+    dtable = dev(hip, table)
+    caches = [(gen.activations(rng, max_seq, kw), gen.activations(rng, max_seq, kw)) for _ in range(rows)]
+    pos = dev(hip, np.array(positions, np.int32))
+
+    def run(fused):
+        kcs = [dev(hip, k.copy()) for k, _ in caches]
+        vcs = [dev(hip, v.copy()) for _, v in caches]
+        kb, vb = ptr_array(hip, [c.ptr for c in kcs]), ptr_array(hip, [c.ptr for c in vcs])
+        dq = dev(hip, qkv.copy())
+        out = hip.DeviceArray((rows, qw), np.uint16)
+        if fused:
+            hip.call("qwen3_tts_op_decode_attention", exact, dq.ptr, qw + 2 * kw, dev(hip, qn).ptr, dev(hip, kn).ptr,
+                     dtable.ptr, C.c_float(1e-6), kb.ptr, vb.ptr, pos.ptr, out.ptr, rows, qh, kvh, d, max_seq, None)
+        else:
+            hip.call("qwen3_tts_op_qk_norm_rope_kv_append", dq.ptr, dev(hip, qn).ptr, dev(hip, kn).ptr, kb.ptr,
+                     vb.ptr, pos.ptr, dtable.ptr, rows, qh, kvh, d, C.c_float(1e-6), None)
+            hip.call("qwen3_tts_op_attention", exact, dq.ptr, qw + 2 * kw, kb.ptr, vb.ptr, pos.ptr, out.ptr, rows,
+                     qh, kvh, d, max_seq, None)
+        return out.numpy(), [c.numpy() for c in kcs], [c.numpy() for c in vcs], dq.numpy()
+
+    out_f, k_f, v_f, _ = run(True)
+    out_s, k_s, v_s, q_s = run(False)
+    assert np.array_equal(out_f, out_s)
+    for r in range(rows):
+        assert np.array_equal(k_f[r], k_s[r]) and np.array_equal(v_f[r], v_s[r])
+        n = positions[r] + 1
+        ref = orc.attention(q_s[r][:qw], k_s[r][:n], v_s[r][:n], qh, kvh, d, n, exact=bool(exact))
+        assert np.array_equal(out_f[r], ref)
+
+
 def test_attention_rows_with_own_caches(hip, orc):
     rng = np.random.default_rng(9)
     qh, kvh, d, max_seq, rows = 16, 8, 128, 64, 3
