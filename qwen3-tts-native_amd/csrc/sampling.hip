@@ -28,10 +28,28 @@ __device__ __forceinline__ bool before(float av, int ai, float bv, int bi) {
     return (av > bv) || (av == bv && ai < bi);
 }
 
+// Branch-free form for the rank counting loop (no short-circuit, so no
+// control flow around the LDS reads).
+__device__ __forceinline__ int before_bit(float av, int ai, float bv, int bi) {
+    return static_cast<int>(av > bv) | (static_cast<int>(av == bv) & static_cast<int>(ai < bi));
+}
+
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v);
     if (u == 0x80000000u) u = 0u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
+// row broadcasts (no LDS round trips).  Integer, so exact in any order.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+    return x;
 }
 
 __device__ uint64_t next_random(uint64_t* state) {
@@ -46,6 +64,13 @@ __device__ uint64_t next_random(uint64_t* state) {
 
 __device__ float uniform_random(uint64_t* state) {
     const uint64_t value = next_random(state);
+    return static_cast<float>(static_cast<double>(value >> 11) * (1.0 / 9007199254740992.0));
+}
+
+// Same draw from a state value already in registers; the caller stores the
+// advanced state.
+__device__ float uniform_random_from(uint64_t& state) {
+    const uint64_t value = next_random(&state);
     return static_cast<float>(static_cast<double>(value >> 11) * (1.0 / 9007199254740992.0));
 }
 
@@ -79,7 +104,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     __shared__ int cand_i[kCandidateCap];
     __shared__ float sorted_v[kMaxVocabulary];
     __shared__ int sorted_i[kMaxVocabulary];
-    __shared__ uint32_t hist[256];
+    __shared__ uint32_t hist2[512];
     __shared__ float red_v[kSampleThreads / 64];
     __shared__ int red_i[kSampleThreads / 64];
     __shared__ uint32_t s_prefix;
@@ -87,12 +112,23 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     __shared__ int s_count;
     __shared__ int s_best;
     __shared__ double s_target;
+    __shared__ double shares[72];
 
     const int tid = threadIdx.x;
     const int V = a.vocabulary;
     const int count = a.history_count ? *a.history_count : a.history_count_fallback;
+    // the generator state, requested now and used at the very end
+    uint64_t random_state = (tid == 0 && a.random_state != nullptr) ? *a.random_state : 0ull;
     const bool penalize = a.suppress && a.penalty != 1.0f;
 
+    // The logits are requested first (they do not depend on the history).
+    constexpr int kPerThread = kMaxVocabulary / kSampleThreads;
+    float logit[kPerThread];
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+        const int t = tid + j * kSampleThreads;
+        logit[j] = t < V ? bf2f(a.logits[t]) : 0.0f;
+    }
     for (int t = tid; t < V; t += kSampleThreads) marked[t] = 0;
     __syncthreads();
     if (penalize) {
@@ -102,12 +138,15 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         }
         __syncthreads();
     }
-    for (int t = tid; t < V; t += kSampleThreads) {
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+        const int t = tid + j * kSampleThreads;
+        if (t >= V) break;
         float value;
         if (a.suppress && t >= 2048 && t != a.eos) {
             value = -INFINITY;
         } else {
-            value = bf2f(a.logits[t]);
+            value = logit[j];
             if (penalize && marked[t]) value = value < 0.0f ? value * a.penalty : value / a.penalty;
         }
         values[t] = value;
@@ -180,13 +219,17 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         }
     } else {
         // Threshold key of the selections-th largest value (radix select).
+        // Two histogram buffers: the next pass's is cleared while this
+        // pass's is scanned, two barriers per pass.
         if (tid == 0) {
             s_prefix = 0u;
             s_above = 0;
         }
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0u;
-            __syncthreads();
+        for (int b = tid; b < 512; b += kSampleThreads) hist2[b] = 0u;
+        __syncthreads();
+        int buffer = 0;
+        for (int shift = 24; shift >= 0; shift -= 8, buffer ^= 1) {
+            uint32_t* hist = hist2 + 256 * buffer;
             const uint32_t prefix = s_prefix;
             const int high = shift + 8;
             for (int t = tid; t < V; t += kSampleThreads) {
@@ -208,12 +251,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                     h[j] = static_cast<int>(hist[255 - 4 * lane - j]);
                     lane_total += h[j];
                 }
-                int inclusive = lane_total;
-#pragma unroll
-                for (int offset = 1; offset < 64; offset <<= 1) {
-                    const int other = __shfl_up(inclusive, offset, 64);
-                    if (lane >= offset) inclusive += other;
-                }
+                const int inclusive = wave_inclusive_scan(lane_total);
                 const int base_above = s_above;
                 int before = base_above + inclusive - lane_total;
                 int found = -1;
@@ -237,6 +275,8 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                     s_above = found_before;
                     s_prefix = prefix | (static_cast<uint32_t>(255 - 4 * lane - found) << shift);
                 }
+            } else if (tid >= 256 && tid < 512) {
+                hist2[256 * (buffer ^ 1) + (tid - 256)] = 0u;  // next pass's buffer
             }
             __syncthreads();
         }
@@ -260,7 +300,12 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                 const float v = cand_v[c];
                 const int i = cand_i[c];
                 int rank = 0;
-                for (int j = 0; j < n; ++j) rank += before(cand_v[j], cand_i[j], v, i) ? 1 : 0;
+                int j = 0;
+                for (; j + 8 <= n; j += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) rank += before_bit(cand_v[j + u], cand_i[j + u], v, i);
+                }
+                for (; j < n; ++j) rank += before_bit(cand_v[j], cand_i[j], v, i);
                 sorted_v[rank] = v;
                 sorted_i[rank] = i;
             }
@@ -280,48 +325,55 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         }
         __syncthreads();
         if (selections <= 64) {
-            // Wave 0 runs the reference's sequential double sums as uniform
-            // loops, reading weight r from lane r (no memory round trip per
-            // term); every lane computes the same values.
+            // Wave 0.  Every running sum of the reference is a prefix sum in
+            // rank order, so one sequential pass (all lanes, LDS broadcast
+            // reads) produces them; lane r keeps prefix r, and each "first r
+            // with cumulative >= x" loop becomes a ballot over the lanes.
             if (tid < 64) {
-                const double own = tid < selections ? weights[tid] : 0.0;
-                const int own_lo = __double2loint(own);
-                const int own_hi = __double2hiint(own);
-                auto weight = [&](int r) {
-                    return __hiloint2double(__builtin_amdgcn_readlane(own_hi, r), __builtin_amdgcn_readlane(own_lo, r));
-                };
-                double denominator = 0.0;
-                for (int r = 0; r < selections; ++r) denominator += weight(r);
-                // the quotients do not depend on the running sum: one per lane
-                const double share = own / denominator;
-                const int share_lo = __double2loint(share);
-                const int share_hi = __double2hiint(share);
-                double cumulative = 0.0;
-                int retained = selections;
-                for (int r = 0; r < selections; ++r) {
-                    cumulative += __hiloint2double(__builtin_amdgcn_readlane(share_hi, r),
-                                                   __builtin_amdgcn_readlane(share_lo, r));
-                    if (cumulative >= static_cast<double>(a.top_p)) {
-                        retained = r + 1;
-                        break;
+                const int lane = tid;
+                double running = 0.0;
+                double prefix_mine = 0.0;
+                for (int r0 = 0; r0 < selections; r0 += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        // unconditional read, selected add: no branch around
+                        // the LDS traffic (entries past `selections` unused)
+                        const int r = r0 + u;
+                        const double w = weights[r];
+                        running = r < selections ? running + w : running;
+                        prefix_mine = lane == r ? running : prefix_mine;
                     }
                 }
-                double retained_total = 0.0;
-                for (int r = 0; r < retained; ++r) retained_total += weight(r);
-                if (tid == 0) s_target = static_cast<double>(uniform_random(a.random_state)) * retained_total;
-                // the draw is made by lane 0 only; broadcast it through LDS
+                const double denominator = running;
+                if (lane < selections) shares[lane] = weights[lane] / denominator;
+                __builtin_amdgcn_wave_barrier();
+                double share_running = 0.0;
+                double share_mine = 0.0;
+                for (int r0 = 0; r0 < selections; r0 += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int r = r0 + u;
+                        const double q = shares[r];
+                        share_running = r < selections ? share_running + q : share_running;
+                        share_mine = lane == r ? share_running : share_mine;
+                    }
+                }
+                const unsigned long long cut =
+                    __ballot(lane < selections && share_mine >= static_cast<double>(a.top_p));
+                const int retained = cut ? __ffsll(static_cast<long long>(cut)) : selections;
+                // sum of weights[0..retained) in order: prefix retained-1
+                const double retained_total =
+                    __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(prefix_mine), retained - 1),
+                                     __builtin_amdgcn_readlane(__double2loint(prefix_mine), retained - 1));
+                if (lane == 0) {
+                    s_target = static_cast<double>(uniform_random_from(random_state)) * retained_total;
+                    *a.random_state = random_state;
+                }
                 __builtin_amdgcn_wave_barrier();
                 const double target = s_target;
-                cumulative = 0.0;
-                int choice = sorted_i[retained - 1];
-                for (int r = 0; r < retained; ++r) {
-                    cumulative += weight(r);
-                    if (cumulative >= target) {
-                        choice = sorted_i[r];
-                        break;
-                    }
-                }
-                if (tid == 0) s_best = choice;
+                const unsigned long long hit = __ballot(lane < retained && prefix_mine >= target);
+                const int r = hit ? __ffsll(static_cast<long long>(hit)) - 1 : retained - 1;
+                if (lane == 0) s_best = sorted_i[r];
             }
         } else if (tid == 0) {
             double denominator = 0.0;
