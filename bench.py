@@ -42,6 +42,36 @@ def step_benchmark(hip, steps, warmup, kernel_filter=0, use_graph=1, rows=1, mod
     return b
 
 
+def single_gemv(hip, iterations: int = 2000):
+    """Config 1: one 6144x2048 int8 GEMV at batch 1 (bf16 y), rotating weight
+    copies so every launch streams from HBM; mean launch time over
+    `iterations` back-to-back launches (hipEvents on the launching stream)."""
+    out = hip.GemvBenchmark()
+    hip.call("qwen3_tts_benchmark_int8_gemv", 0, 2048, 6144, iterations, C.byref(out))
+    bytes_ = 6144 * 2048 + 4 * 6144 + 2 * 2048 + 2 * 6144
+    return {"shape": "6144x2048", "rows": 1, "us_per_launch": round(out.mean_launch_microseconds, 3),
+            "achieved_gbs": round(bytes_ / (out.mean_launch_microseconds * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(bytes_ / (out.mean_launch_microseconds * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def batched(hip, steps: int, warmup: int):
+    """Config 4: N concurrent sessions as a skinny GEMM on MFMA, for the two
+    shapes of the config (gate+up 12288x2048 with its RMSNorm prologue and
+    fused SiLU; down 2048x6144 with the residual epilogue), 28 distinct
+    layers so the weights stream from HBM."""
+    result = {}
+    for n in (2, 4, 8):
+        for name, filt, out_f, in_f in (("gate_up_12288x2048", 3, 2 * INTER, HIDDEN), ("down_2048x6144", 4, HIDDEN, INTER)):
+            b = step_benchmark(hip, steps, warmup, kernel_filter=filt, rows=n, mode=2)
+            us = b.milliseconds_per_step * 1000.0 / LAYERS
+            bytes_ = b.algorithmic_bytes_per_step / LAYERS
+            flops = 2.0 * n * out_f * in_f
+            result[f"n{n}_{name}"] = {"us_per_launch": round(us, 3),
+                                      "achieved_gbs": round(bytes_ / (us * 1e-6) / 1e9, 1),
+                                      "tflops": round(flops / (us * 1e-6) / 1e12, 2)}
+    return result
+
+
 def cpu_baseline(seconds: float = 10.0):
     """Oracle exact-order int8 GEMV chain on the host cores (bounded sample)."""
     import numpy as np
@@ -247,6 +277,8 @@ def main() -> int:
                      "kernel": "gemv_exact_fixed<4, SiluRounded, norm> (gate+up 12288x2048)",
                      "bytes_per_launch": int(launch_bytes), "us_per_launch": round(launch_us, 3)},
     }
+    line["single_gemv_config1"] = single_gemv(hip)
+    line["batched_config4"] = batched(hip, max(args.steps // 4, 5), max(args.warmup // 2, 2))
     if not args.no_frames:
         try:
             line["frame_step"] = frame_benchmark(hip, frames=args.frames)

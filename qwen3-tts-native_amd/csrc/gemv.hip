@@ -248,22 +248,23 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_generic(GemvArgs a) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
+// int8 -> bf16 is exact; per byte one sign-extending convert to fp32 and half
+// a packed fp32 -> bf16 convert (v_cvt_pk_bf16_f32 on gfx950).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bf16x8_t bytes_to_bf16x8(uint32_t lo, uint32_t hi) {
-    // int8 values are exactly representable in bf16: convert via fp32 and
-    // keep the upper half (exact, no rounding needed).
     union {
         uint32_t u[4];
         bf16x8_t v;
     } r;
-    const uint32_t words[2] = {lo, hi};
+    const uint32_t w[2] = {lo, hi};
 #pragma unroll
-    for (int w = 0; w < 2; ++w) {
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t a = __float_as_uint(byte_f(static_cast<int>(words[w]), 2 * p));
-            const uint32_t b = __float_as_uint(byte_f(static_cast<int>(words[w]), 2 * p + 1));
-            r.u[2 * w + p] = (a >> 16) | (b & 0xffff0000u);
-        }
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t word = w[p >> 1];
+        const int shift = 16 * (p & 1);
+        const float f0 = static_cast<float>(static_cast<int>(static_cast<int8_t>((word >> shift) & 0xffu)));
+        const float f1 = static_cast<float>(static_cast<int>(static_cast<int8_t>((word >> (shift + 8)) & 0xffu)));
+        const bf16x2_t pair = {static_cast<__bf16>(f0), static_cast<__bf16>(f1)};
+        r.u[p] = __builtin_bit_cast(uint32_t, pair);
     }
     return r.v;
 }
@@ -374,6 +375,219 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Batched rows (2..8 sessions) on MFMA, K = 64 * kWaves * kIters known at
+// compile time.  A block owns 16 output channels (16 gate + 16 up rows for the
+// SiLU epilogues); its 4 or 8 waves split K.  Latency order: with the RMSNorm
+// prologue the session rows are requested first; then every weight vector of
+// the wave's K slice (8 lanes per row, 128 contiguous bytes per row per load),
+// held in registers; the epilogue operands.  The rows are staged in LDS (and
+// normalized there with the RMSNorm prologue: statistic per row by one wave
+// with the reference's 256-thread tree) as the MFMA B operands.  Each 16-row
+// x 128-byte weight step is transposed through a per-wave LDS tile into the
+// v_mfma_f32_16x16x32_bf16 A operand layout.
+// ---------------------------------------------------------------------------
+template <int kIters, int kWaves, int kEpi, bool kNorm>
+__global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
+    constexpr int kBlock = 64 * kWaves;
+    if (a.input_row_index != nullptr) {
+        a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
+    }
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    constexpr int kTiles = kSilu ? 2 : 1;
+    static_assert(kIters % 2 == 0, "weight steps come in pairs of 8-row loads");
+    constexpr int kIn = 64 * kWaves * kIters;
+    constexpr int kStride = kIn + 8;  // bf16 elements per LDS row (16-byte pad)
+    extern __shared__ __align__(16) bf16_t xs[];  // [rows][kStride]
+    __shared__ float fold[kWaves][kTiles][16][16];
+    constexpr int kTileRow = 136;
+    __shared__ __align__(16) int8_t wtile[kWaves * kTiles * 16 * kTileRow];
+    __shared__ float inverse_lds[8];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int rows = a.rows;
+    const int c0 = blockIdx.x * 16;
+    const int m = lane & 15;
+    const int group = lane >> 4;
+    constexpr int kChunks = kIn / 8;  // 16-byte chunks per row
+
+    // 0. With the RMSNorm prologue the session rows are needed before any
+    //    MFMA: request them ahead of the weights (memory returns in order).
+    // The session rows (up to 8 of them) are requested ahead of the weights
+    // (memory returns in order) and staged in LDS as the MFMA B operands.
+    constexpr int kXPer = (8 * kChunks + kBlock - 1) / kBlock;
+    static_assert(kXPer <= 12, "x staging holds at most 12 chunks per thread");
+    // named registers, not an array (an array here is placed in scratch)
+    uint4 x0{}, x1{}, x2{}, x3{}, x4{}, x5{}, x6{}, x7{}, x8{}, x9{}, x10{}, x11{};
+    // Chunk j of this thread is row (tid + j*block) / kChunks; threads past
+    // the last row load nothing (a masked load issues no request).
+    auto x_load = [&](int j) {
+        const int idx = threadIdx.x + j * kBlock;
+        const int r = idx / kChunks;
+        const int c = idx % kChunks;
+        uint4 v{};
+        if (r < rows) v = *reinterpret_cast<const uint4*>(a.input + static_cast<size_t>(r) * kIn + 8 * c);
+        return v;
+    };
+    if constexpr (kXPer > 0) x0 = x_load(0);
+    if constexpr (kXPer > 1) x1 = x_load(1);
+    if constexpr (kXPer > 2) x2 = x_load(2);
+    if constexpr (kXPer > 3) x3 = x_load(3);
+    if constexpr (kXPer > 4) x4 = x_load(4);
+    if constexpr (kXPer > 5) x5 = x_load(5);
+    if constexpr (kXPer > 6) x6 = x_load(6);
+    if constexpr (kXPer > 7) x7 = x_load(7);
+    if constexpr (kXPer > 8) x8 = x_load(8);
+    if constexpr (kXPer > 9) x9 = x_load(9);
+    if constexpr (kXPer > 10) x10 = x_load(10);
+    if constexpr (kXPer > 11) x11 = x_load(11);
+    // When kChunks divides the block, all of a thread's chunks share the
+    // column c = tid % kChunks: one RMSNorm gain chunk, requested early too.
+    constexpr bool kOneGain = kNorm && kBlock % kChunks == 0;
+    uint4 gain_chunk{};
+    if constexpr (kOneGain) gain_chunk = reinterpret_cast<const uint4*>(a.norm_weight)[threadIdx.x % kChunks];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 1. weights of this wave's K slice.  Loaded 8 lanes per row: one load
+    //    instruction covers 128 contiguous bytes of each of 8 rows (64 bytes
+    //    of 16 rows runs at ~60% of the bandwidth); load i = 2*step + half
+    //    holds rows 8*half .. 8*half+7, bytes 128*step .. 128*step+127.
+    const int load_row = lane >> 3;
+    const int load_part = lane & 7;
+    int4 wq[kTiles][kIters];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const int ch = c0 + 8 * (i & 1) + load_row;
+            const int row = (t == 0 ? 0 : a.out_features) + (ch < a.out_features ? ch : 0);
+            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + wave * (kIn / kWaves) + 128 * (i >> 1) +
+                                16 * load_part;
+            wq[t][i] = stream_load(reinterpret_cast<const int4*>(src));
+        }
+    }
+    // epilogue operands of this thread's (channel, session) output
+    const int out_row = threadIdx.x >> 4;
+    const int out_col = threadIdx.x & 15;
+    const int out_ch = c0 + out_row;
+    const bool writes = threadIdx.x < 256 && out_col < rows && out_ch < a.out_features;
+    GemvArgs out_args = a;
+    out_args.out16 = a.out16 ? a.out16 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
+    out_args.out32 = a.out32 ? a.out32 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
+    const EpiInputs epi = prefetch_epi<kEpi>(out_args, writes ? out_ch : 0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. session rows into LDS
+    {
+        auto x_store = [&](int j, const uint4& v) {
+            const int idx = threadIdx.x + j * kBlock;
+            const int r = idx / kChunks;
+            const int c = idx % kChunks;
+            if (r < rows) *reinterpret_cast<uint4*>(xs + r * kStride + 8 * c) = v;
+        };
+        if constexpr (kXPer > 0) x_store(0, x0);
+        if constexpr (kXPer > 1) x_store(1, x1);
+        if constexpr (kXPer > 2) x_store(2, x2);
+        if constexpr (kXPer > 3) x_store(3, x3);
+        if constexpr (kXPer > 4) x_store(4, x4);
+        if constexpr (kXPer > 5) x_store(5, x5);
+        if constexpr (kXPer > 6) x_store(6, x6);
+        if constexpr (kXPer > 7) x_store(7, x7);
+        if constexpr (kXPer > 8) x_store(8, x8);
+        if constexpr (kXPer > 9) x_store(9, x9);
+        if constexpr (kXPer > 10) x_store(10, x10);
+        if constexpr (kXPer > 11) x_store(11, x11);
+    }
+    __syncthreads();
+    if constexpr (kNorm) {
+        for (int r = wave; r < rows; r += kWaves) {
+            const float inverse = wave_inverse_rms(xs + r * kStride, kIn, a.norm_epsilon);
+            if (lane == 0) inverse_lds[r] = inverse;
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < rows * kChunks; idx += kBlock) {
+            const int r = idx / kChunks;
+            const int c = idx % kChunks;
+            uint4* p = reinterpret_cast<uint4*>(xs + r * kStride + 8 * c);
+            const uint4 g = kOneGain ? gain_chunk : reinterpret_cast<const uint4*>(a.norm_weight)[c];
+            *p = normalize_chunk(*p, g, inverse_lds[r]);
+        }
+        __syncthreads();
+    }
+
+    // 3. MFMAs: columns m < rows are sessions, the rest zero
+    const bool real_col = m < rows;
+    // without the norm the MFMA operands come straight from global memory
+    // (the rows are L2-resident): no staging round trip behind the weights
+    const bf16_t* xrow = xs + (real_col ? m : 0) * kStride;
+    floatx4_t acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    // per-wave LDS tile [16 rows][136 bytes] per tile: written as loaded,
+    // read back in the MFMA operand layout (lane (m, g): 8 bytes of row m);
+    // the 8-byte row pad spreads the 16 rows over all banks
+    int8_t* tile = wtile + wave * (kTiles * 16 * kTileRow);
+#pragma unroll
+    for (int step = 0; step < kIters / 2; ++step) {
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                *reinterpret_cast<int4*>(tile + t * 16 * kTileRow + (8 * h + load_row) * kTileRow + 16 * load_part) =
+                    wq[t][2 * step + h];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = wave * (kIn / kWaves) + 128 * step + 32 * j + 8 * group;
+            bf16x8_t b = {};
+            if (real_col) b = load_bf16x8(xrow + k);
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) {
+                const uint2 q = *reinterpret_cast<const uint2*>(tile + t * 16 * kTileRow + m * kTileRow + 32 * j + 8 * group);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bytes_to_bf16x8(q.x, q.y), b, acc[t], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fold[wave][t][4 * group + j][m] = acc[t][j];  // [channel][session]
+    }
+    __syncthreads();
+    if (writes) {
+        float value[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            float v = fold[0][t][out_row][out_col];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) v += fold[w][t][out_row][out_col];
+            value[t] = v;
+        }
+        if constexpr (kSilu) {
+            finish_gate_up<kEpi>(out_args, out_ch, value[0], value[kTiles - 1], epi);
+        } else {
+            finish_channel<kEpi>(out_args, out_ch, value[0], epi);
+        }
+    }
+}
+
+template <int kIters, int kWaves, int kEpi, bool kNorm>
+hipError_t launch_mfma_fixed(const GemvArgs& a, hipStream_t s) {
+    constexpr int kIn = 64 * kWaves * kIters;
+    const size_t lds = static_cast<size_t>(a.rows) * (kIn + 8) * sizeof(bf16_t);
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm>),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  static_cast<int>(8 * (kIn + 8) * sizeof(bf16_t)));
+        if (st != hipSuccess) return st;
+        configured = true;
+    }
+    gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm><<<(a.out_features + 15) / 16, 64 * kWaves, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Per-row symmetric quantizer (int8_gemv.cu:20-52): absmax -> scale ->
 // lrint(clamp(w / scale)).  One 256-thread block per output row.
 // ---------------------------------------------------------------------------
@@ -452,6 +666,14 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
     if (mfma) {
         if (a.in_features % 256 != 0 || (kNorm && a.in_features > 6144)) {
             return hipErrorInvalidValue;
+        }
+        switch (a.in_features) {
+            // kIters = K / (64 * waves); 8 waves where K is long
+            case 1024: return launch_mfma_fixed<4, 4, kEpi, kNorm>(a, s);
+            case 2048: return launch_mfma_fixed<8, 4, kEpi, kNorm>(a, s);
+            case 3072: return launch_mfma_fixed<6, 8, kEpi, kNorm>(a, s);
+            case 6144: return launch_mfma_fixed<12, 8, kEpi, kNorm>(a, s);
+            default: break;
         }
         const int grid = (a.out_features + 15) / 16;
         gemv_mfma<kEpi, kNorm><<<grid, kThreads, 0, s>>>(a);
