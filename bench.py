@@ -42,6 +42,20 @@ def step_benchmark(hip, steps, warmup, kernel_filter=0, use_graph=1, rows=1, mod
     return b
 
 
+def pmc_traffic():
+    """HBM bytes per launch of the dominant kernel from the two rocprofv3 PMC
+    passes (FETCH_SIZE, WRITE_SIZE, calibrated on a 256 MiB copy) recorded in
+    profiles/gemv_gate_up_hbm_traffic_pmc.md; None if that record is absent."""
+    path = ROOT / "profiles" / "gemv_gate_up_hbm_traffic_pmc.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def single_gemv(hip, iterations: int = 2000):
     """Config 1: one 6144x2048 int8 GEMV at batch 1 (bf16 y), rotating weight
     copies so every launch streams from HBM; mean launch time over
@@ -237,6 +251,9 @@ def main() -> int:
     ap.add_argument("--frames", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
+    ap.add_argument("--only-dominant", action="store_true",
+                    help="run only the dominant kernel's workload (the 28 gate/up GEMVs of a step) and a "
+                         "256 MiB device-to-device copy that calibrates the HBM byte counters; for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the decode path on a single MI355X "
@@ -245,6 +262,17 @@ def main() -> int:
     import qwen3_tts_hip as hip
 
     hip.load()
+    if args.only_dominant:
+        import numpy as np
+
+        step_benchmark(hip, args.steps, args.warmup, kernel_filter=3)
+        size = 256 << 20
+        src = hip.DeviceArray(size, np.uint8)
+        dst = hip.DeviceArray(size, np.uint8)
+        hip.call("qwen3_tts_device_memcpy", dst.ptr, src.ptr, size)
+        hip.synchronize()
+        print(json.dumps({"dominant_kernel_launches": 28 * (args.steps + args.warmup), "copy_bytes": size}))
+        return 0
     main_run = step_benchmark(hip, args.steps, args.warmup)
     ms = main_run.milliseconds_per_step
     value = main_run.algorithmic_bytes_per_step / (ms * 1e-3) / 1e9
@@ -273,7 +301,7 @@ def main() -> int:
                    "weight_bytes_per_step": int(main_run.weight_bytes)},
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
                      "kernel": "gemv_exact_fixed<4, SiluRounded, norm> (gate+up 12288x2048)",
                      "bytes_per_launch": int(launch_bytes), "us_per_launch": round(launch_us, 3)},
     }
