@@ -430,47 +430,86 @@ constexpr int kSmallCapacity = 64;
 
 template <bool kExact, int kG>
 __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) {
+    constexpr int kPrefetch = 16;  // value rows each lane requests up front
     __shared__ float q_lds[kG][kDim];
     __shared__ float prob[kG][kSmallCapacity];
-    __shared__ float partial[kG][256];
     __shared__ float inverse_lds[kG];
+    __shared__ uint32_t knew_lds[kDim / 2];
+    __shared__ bf16_t vnew_lds[kDim];
     const int row = blockIdx.y;
     const int kvh = blockIdx.x;
     const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
     const int length = row_length(a, row);
     const int kv_width = a.key_value_heads * kDim;
     const int position = length - 1;
-    __shared__ uint32_t knew_lds[kDim / 2];
-    __shared__ bf16_t vnew_lds[kDim];
-    // key row of this lane's (g, p) first
+    const bool fused = a.q_norm != nullptr;
+    // With the QKV epilogue fused, the current position's key and value come
+    // from qkv (and are written to the caches here), not from the caches.
+    const int cached = fused ? position : length;
+    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
+    const bf16_t* cs = a.rope_table + static_cast<size_t>(position) * kDim;
+
+    // 1. everything this block reads, requested up front in the order it is
+    //    needed: the head-norm operands, the key rows, the value columns.
+    head_detail::HeadInputs head_in{};
+    if (fused) {
+        if (wave < kG) {
+            head_in = head_detail::load_head(q + wave * kDim, a.q_norm, cs);
+        } else if (wave == kG) {
+            const bf16_t* kraw = a.query + static_cast<size_t>(row) * a.query_stride +
+                                 static_cast<size_t>(a.query_heads + kvh) * kDim;
+            head_in = head_detail::load_head(kraw, a.k_norm, cs);
+        }
+    }
     const int g_score = tid / length;
     const int p_score = tid % length;
-    const int krow = tid < kG * length ? p_score : position;
-    const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(krow) * kv_width +
-                                                     static_cast<size_t>(kvh) * kDim);
+    const bool scores_lane = tid < kG * length;
     uint32_t kw[64];
+    if (scores_lane && p_score < cached) {
+        const uint4* k4 = reinterpret_cast<const uint4*>(row_keys(a, row) + static_cast<size_t>(p_score) * kv_width +
+                                                         static_cast<size_t>(kvh) * kDim);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const uint4 t = load_global16(k4 + v);
-        kw[4 * v + 0] = t.x;
-        kw[4 * v + 1] = t.y;
-        kw[4 * v + 2] = t.z;
-        kw[4 * v + 3] = t.w;
+        for (int v = 0; v < 16; ++v) {
+            const uint4 t = load_global16(k4 + v);
+            kw[4 * v + 0] = t.x;
+            kw[4 * v + 1] = t.y;
+            kw[4 * v + 2] = t.z;
+            kw[4 * v + 3] = t.w;
+        }
     }
-    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
-    const bool fused = a.q_norm != nullptr;
+    const int g = tid / kDim;
+    const int d = tid % kDim;
+    const bf16_t* vcol = row_values(a, row) + static_cast<size_t>(kvh) * kDim + d;
+    float vpre[kPrefetch];
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+        vpre[p] = p < cached ? bf2f(vcol[static_cast<size_t>(p) * kv_width]) : 0.0f;
+    }
+
+    // 2. head norms, RoPE, KV append
     if (fused) {
-        const int wave = tid >> 6;
-        const int lane = tid & 63;
         if (wave < kG) {
             bf16_t q0, q1;
-            head_detail::norm_rope_head(q + wave * kDim, a.q_norm, a.rope_table + static_cast<size_t>(position) * kDim,
-                                        a.epsilon, q0, q1);
+            head_detail::norm_rope_from(head_in, a.epsilon, q0, q1);
             q_lds[wave][lane] = bf2f(q0);
             q_lds[wave][lane + 64] = bf2f(q1);
         } else if (wave == kG) {
-            bf16_t k0, k1, v0, v1;
-            append_kv(a, row, kvh, position, k0, k1, v0, v1);
+            bf16_t k0, k1;
+            head_detail::norm_rope_from(head_in, a.epsilon, k0, k1);
+            const bf16_t* vraw = a.query + static_cast<size_t>(row) * a.query_stride +
+                                 static_cast<size_t>(a.query_heads) * kDim + kv_width + static_cast<size_t>(kvh) * kDim;
+            const bf16_t v0 = vraw[lane];
+            const bf16_t v1 = vraw[lane + 64];
+            bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
+                           static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+            bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
+                           static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+            kdst[lane] = k0;
+            kdst[lane + 64] = k1;
+            vdst[lane] = v0;
+            vdst[lane + 64] = v1;
             reinterpret_cast<bf16_t*>(knew_lds)[lane] = k0;
             reinterpret_cast<bf16_t*>(knew_lds)[lane + 64] = k1;
             vnew_lds[lane] = v0;
@@ -480,14 +519,14 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
         q_lds[tid / kDim][tid % kDim] = bf2f(q[tid]);
     }
     __syncthreads();
-    if (tid < kG * length) {
-        const int g = g_score;
-        const int p = p_score;
-        if (fused && p == position) {
+
+    // 3. scores, lane = (g, p)
+    if (scores_lane) {
+        if (p_score >= cached) {
 #pragma unroll
             for (int i = 0; i < 64; ++i) kw[i] = knew_lds[i];
         }
-        const float* qg = q_lds[g];
+        const float* qg = q_lds[g_score];
         float score;
         if constexpr (kExact) {
             float sv[64];
@@ -512,52 +551,45 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
             }
             score = dot * a.scale;
         }
-        prob[g][p] = score;
+        prob[g_score][p_score] = score;
     }
     __syncthreads();
-    const int g = tid / kDim;
-    const int d = tid % kDim;
-    if (d == 0) {
-        float* sg = prob[g];
-        float maximum = -INFINITY;
-        for (int p = 0; p < length; ++p) maximum = fmaxf(maximum, sg[p]);
+
+    // 4. softmax per head, one wave per head, lane = position: the max is
+    //    order independent, the exponentials are per element, and the
+    //    normalizer keeps the reference's order (exact: a sequential sum read
+    //    lane by lane; fast: the 256-thread tree, whose levels 128 and 64
+    //    only add zeros here).
+    if (wave < kG) {
+        float* sg = prob[wave];
+        const bool live = lane < length;
+        const float s = live ? sg[lane] : -INFINITY;
+        float maximum = s;
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, offset, 64));
+        const float e = live ? q3_expf(s - maximum) : 0.0f;
         if constexpr (kExact) {
             float denominator = 0.0f;
-            for (int p = 0; p < length; ++p) {
-                sg[p] = q3_expf(sg[p] - maximum);
-                denominator += sg[p];
-            }
+            for (int p = 0; p < length; ++p) denominator += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
             const float inverse = 1.0f / denominator;
-            for (int p = 0; p < length; ++p) sg[p] = round_bf(sg[p] * inverse);
+            if (live) sg[lane] = round_bf(e * inverse);
         } else {
-            // 256 strided partials (one term each here) and their tree
-            float* part = partial[g];
-            for (int t = 0; t < 256; ++t) part[t] = 0.0f;
-            for (int p = 0; p < length; ++p) {
-                sg[p] = q3_expf(sg[p] - maximum);
-                part[p] += sg[p];
-            }
-            for (int w = 128; w > 0; w >>= 1) {
-                for (int t = 0; t < w; ++t) part[t] += part[t + w];
-            }
-            inverse_lds[g] = 1.0f / part[0];
+            float value = e;
+#pragma unroll
+            for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_down(value, offset, 64);
+            if (live) sg[lane] = e;
+            if (lane == 0) inverse_lds[wave] = 1.0f / value;
         }
     }
     __syncthreads();
-    const bf16_t* vcol = row_values(a, row) + static_cast<size_t>(kvh) * kDim + d;
-    // fused: the current position's value comes from LDS (its cache row is
-    // written by this block)
-    const int cached = fused ? position : length;
+
+    // 5. value chain, lane = (g, d)
     float acc = 0.0f;
-    int p = 0;
-    for (; p + 8 <= cached; p += 8) {
-        float vv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) vv[u] = bf2f(vcol[static_cast<size_t>(p + u) * kv_width]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fmaf(prob[g][p + u], vv[u], acc);
+    for (int p = 0; p < kPrefetch; ++p) {
+        if (p < cached) acc = fmaf(prob[g][p], vpre[p], acc);
     }
-    for (; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
+    for (int p = kPrefetch; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
     if (fused) acc = fmaf(prob[g][position], bf2f(vnew_lds[d]), acc);
     const int head = kvh * kG + g;
     float y = acc;
