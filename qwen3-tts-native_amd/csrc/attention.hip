@@ -315,20 +315,28 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
         // thread 0 of the reference's block: one sequential sum per head, the
         // G heads in G lanes of the same instructions
         if (lane < kG) {
+            // 32 values per step; the next step's reads are issued before
+            // this step's adds (the add chain, not LDS latency, sets the pace)
             const float* e = p_lds + lane * stride;
             float denominator = 0.0f;
             int p = 0;
-            for (; p + 16 <= length; p += 16) {
-                float4 v[4];
+            float4 cur[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(e + p + 4 * u);
+            for (int u = 0; u < 8; ++u) cur[u] = *reinterpret_cast<const float4*>(e + 4 * u);
+            for (; p + 32 <= length; p += 32) {
+                const int next = p + 64 <= length ? p + 32 : p;  // re-read in the last step
+                float4 nxt[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    denominator += v[u].x;
-                    denominator += v[u].y;
-                    denominator += v[u].z;
-                    denominator += v[u].w;
+                for (int u = 0; u < 8; ++u) nxt[u] = *reinterpret_cast<const float4*>(e + next + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    denominator += cur[u].x;
+                    denominator += cur[u].y;
+                    denominator += cur[u].z;
+                    denominator += cur[u].w;
                 }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
             }
             for (; p < length; ++p) denominator += e[p];
             inverse_lds[lane] = 1.0f / denominator;
@@ -337,7 +345,17 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
 #pragma unroll
         for (int gg = 0; gg < kG; ++gg) {
             const float inverse = inverse_lds[gg];
-            for (int p = lane; p < length; p += 64) eg[gg * stride + p] = round_bf(eg[gg * stride + p] * inverse);
+            // 8 positions per lane per batch: reads first, then the products
+            for (int base = 0; base < length; base += 8 * 64) {
+                float t[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) t[u] = eg[gg * stride + min(base + u * 64 + lane, length - 1)];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int p = base + u * 64 + lane;
+                    if (p < length) eg[gg * stride + p] = round_bf(t[u] * inverse);
+                }
+            }
         }
     } else {
         // 256 strided partials: lane l holds those of threads l, l+64,

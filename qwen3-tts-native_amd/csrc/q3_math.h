@@ -25,9 +25,10 @@
 #endif
 
 Q3_FN float q3_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.72284f) return INFINITY;
-    if (x < -103.97208f) return 0.0f;
+    /* Branch-free: the polynomial path is evaluated for every input and the
+     * special cases are selected at the end (on the GPU a branch per case
+     * would serialize the lanes).  For -103.97208 <= x <= 88.72284 the result
+     * is the polynomial path; outside it exactly the special value. */
     const float n = rintf(x * 1.44269504088896341f);
     /* ln2 split: hi has 16 significant bits so n*hi is exact for |n| <= 2^8. */
     float r = fmaf(-n, 0.693145751953125f, x);
@@ -40,9 +41,14 @@ Q3_FN float q3_expf(float x) {
     p = fmaf(p, r, 0.5f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    const int e = (int)n;
+    /* n is in [-150, 128] on the polynomial path; the clamp only keeps the
+     * integer conversion defined for the discarded inputs (and NaN). */
+    const int e = (int)fminf(fmaxf(n, -200.0f), 200.0f);
     const int e1 = e / 2;
-    return ldexpf(ldexpf(p, e1), e - e1);
+    const float poly = ldexpf(ldexpf(p, e1), e - e1);
+    const float big = x > 88.72284f ? INFINITY : poly;
+    const float ranged = x < -103.97208f ? 0.0f : big;
+    return x != x ? x : ranged;
 }
 
 #endif
