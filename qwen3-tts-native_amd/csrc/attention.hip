@@ -365,9 +365,7 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
         for (int gg = 0; gg < kG; ++gg) {
             float p0 = partial[gg][0] + partial[gg][2];
             float p1 = partial[gg][1] + partial[gg][3];
-            float value = p0 + p1;
-#pragma unroll
-            for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_down(value, offset, 64);
+            const float value = wave_sum_down<64>(p0 + p1);
             if (lane == 0) inverse_lds[gg] = 1.0f / value;
         }
     }
@@ -592,9 +590,7 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
             const float inverse = 1.0f / denominator;
             if (live) sg[lane] = round_bf(e * inverse);
         } else {
-            float value = e;
-#pragma unroll
-            for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_down(value, offset, 64);
+            const float value = wave_sum_down<64>(e);
             if (live) sg[lane] = e;
             if (lane == 0) inverse_lds[wave] = 1.0f / value;
         }

@@ -29,12 +29,12 @@ __device__ __forceinline__ int4 stream_load(const void* p) {
 }
 
 // Reference 32-lane shuffle-down fold, offsets 16..1 (int8_gemv.cu:114-118).
-__device__ __forceinline__ float fold32(float value) {
-#pragma unroll
-    for (int offset = 16; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 32);
-    }
-    return value;
+// The sum is valid in lane 0 of each half-wave.
+__device__ __forceinline__ float fold32(float value) { return wave_sum_down<32>(value); }
+
+// Lane 0's value, for every lane (the whole wave must be active).
+__device__ __forceinline__ float from_lane0(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
 // inv_rms of x[0..width) with the exact 256-thread tree of the reference's
@@ -54,11 +54,7 @@ __device__ inline float wave_inverse_rms(const bf16_t* x, int width, float epsil
     part[0] += part[2];
     part[1] += part[3];
     float value = part[0] + part[1];
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 64);
-    }
-    const float total = __shfl(value, 0, 64);
+    const float total = from_lane0(wave_sum_down<64>(value));
     return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
 }
 
@@ -67,12 +63,16 @@ __device__ inline float wave_inverse_rms(const bf16_t* x, int width, float epsil
 // partial is sum(x[i]^2, i = t, t+256, ...) as one fma chain, written to
 // partial[t]; after a barrier every wave folds the 256 partials in the tree
 // order of wave_inverse_rms and gets the same inverse.
-__device__ __forceinline__ float block_partial_sq(const bf16_t* x, int width) {
+template <int kWidth>
+__device__ __forceinline__ float block_partial_sq(const bf16_t* x) {
+    static_assert(kWidth % 256 == 0, "whole rounds of 256 threads");
+    constexpr int kCount = kWidth / 256;
+    float v[kCount];
+#pragma unroll
+    for (int j = 0; j < kCount; ++j) v[j] = bf2f(x[threadIdx.x + 256 * j]);  // all reads first
     float s = 0.0f;
-    for (int i = threadIdx.x; i < width; i += 256) {
-        const float v = bf2f(x[i]);
-        s = fmaf(v, v, s);
-    }
+#pragma unroll
+    for (int j = 0; j < kCount; ++j) s = fmaf(v[j], v[j], s);
     return s;
 }
 
@@ -83,11 +83,7 @@ __device__ __forceinline__ float fold_partials256(const float* partial, int widt
     p0 += p2;
     p1 += p3;
     float value = p0 + p1;
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 64);
-    }
-    const float total = __shfl(value, 0, 64);
+    const float total = from_lane0(wave_sum_down<64>(value));
     return 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
 }
 
@@ -271,6 +267,94 @@ __device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, fl
     finish_gate_up<kEpi, kCoherent>(a, channel, g, u, prefetch_epi<kEpi, kCoherent>(a, channel));
 }
 
+// Epilogue operands that never change during a chain (scales, bias): a linked
+// launch requests them with its weights, before it waits; the residual is
+// read after the wait (it is the previous launches' output).
+template <int kEpi>
+__device__ __forceinline__ EpiInputs prefetch_constants(const GemvArgs& a, int channel) {
+    EpiInputs e;
+    e.scale0 = a.scales[channel];
+    if constexpr (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded) {
+        e.scale1 = a.scales[a.out_features + channel];
+    } else if constexpr (kEpi == kEpiBias || kEpi == kEpiBiasSilu || kEpi == kEpiBiasAdd) {
+        e.extra = bf2f(a.bias[channel]);
+    }
+    return e;
+}
+
+template <int kEpi>
+__device__ __forceinline__ void load_residual(const GemvArgs& a, int channel, EpiInputs& e) {
+    if constexpr (kEpi == kEpiAddFma || kEpi == kEpiAddRounded) {
+        e.extra = load_out<true>(a.out16 + channel);
+    } else if constexpr (kEpi == kEpiBiasAdd) {
+        e.prior = load_out<true>(a.out16 + channel);
+    }
+}
+
+// 16 bytes written by other workgroups of earlier launches that may still be
+// resident: two device-coherent 8-byte loads.
+__device__ __forceinline__ uint4 coherent_load16(const uint4* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_uint4(static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32), static_cast<uint32_t>(hi),
+                      static_cast<uint32_t>(hi >> 32));
+}
+
+// ---------------------------------------------------------------------------
+// Launch links.  Workgroup b belongs to group b % 8 (members: the workgroups
+// of that residue).  A workgroup arrives on its group counter after its
+// stores have completed; the last member of a group arrives on the total
+// counter; the last group writes the completion flag (= completed steps) into
+// 8 lines, which the next launch's workgroups poll (group g its copy g).
+// All counters only grow, so a workgroup's step is its group counter, read
+// before it arrives, divided by the group's members.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned link_members(int group) {
+    return (gridDim.x - static_cast<unsigned>(group) + 7u) / 8u;
+}
+
+__device__ __forceinline__ unsigned link_read_group(const unsigned* counters, int group) {
+    return __hip_atomic_load(counters + group * kLinkLineWords, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait of one thread for flag >= target (wrap-safe compare).  Gives
+// up after ~0.2 s, or when another wait gave up, and records it in `status`,
+// so every workgroup always finishes.
+__device__ inline void link_wait_flag(const unsigned* flag, unsigned target, int* status) {
+    const uint64_t start = wall_clock64();
+    unsigned spins = 0;
+    while (static_cast<int>(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+        __builtin_amdgcn_s_sleep(1);
+        if ((++spins & 63u) == 0u) {
+            if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
+            if (wall_clock64() - start > 20000000ull) {  // 100 MHz clock
+                __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+        }
+    }
+}
+
+// Called by one thread after every thread's stores of this workgroup have
+// completed (s_waitcnt + barrier).  Returns true for the arrival that
+// completed the launch.
+__device__ inline bool link_arrive(unsigned* counters, int group) {
+    const unsigned members = link_members(group);
+    const unsigned groups = gridDim.x < 8u ? gridDim.x : 8u;
+    const unsigned before =
+        __hip_atomic_fetch_add(counters + group * kLinkLineWords, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((before + 1u) % members != 0u) return false;
+    const unsigned total =
+        __hip_atomic_fetch_add(counters + 8 * kLinkLineWords, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (total % groups != 0u) return false;
+    const unsigned completed = total / groups;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        __hip_atomic_store(counters + (9 + c) * kLinkLineWords, completed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+}
 
 }  // namespace gemv_detail
 }  // namespace q3

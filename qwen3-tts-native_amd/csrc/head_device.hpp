@@ -8,16 +8,13 @@ namespace head_detail {
 
 // Exact emulation of the reference's 256-thread block_sum tree
 // (talker_kernels.cu:14-25) by one wave64: `p<j>` is virtual thread
-// lane + 64*j.  Result is broadcast to every lane.
+// lane + 64*j.  Result is broadcast to every lane (whole wave active).
 __device__ __forceinline__ float wave_tree256(float p0, float p1, float p2, float p3) {
     p0 += p2;
     p1 += p3;
     float value = p0 + p1;
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        value += __shfl_down(value, offset, 64);
-    }
-    return __shfl(value, 0, 64);
+    value = wave_sum_down<64>(value);
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(value)));
 }
 
 // Head RMSNorm (talker_kernels.cu:50-70) followed by rotate-half RoPE

@@ -48,6 +48,46 @@ __host__ __device__ inline bf16_t f2bf(float f) {
 __host__ __device__ inline float round_bf(float f) { return bf2f(f2bf(f)); }
 
 // ---------------------------------------------------------------------------
+// Shuffle-down sum tree over groups of kWidth lanes (64 or 32) without the LDS
+// crossbar.  Lane 0 of each group ends with exactly what
+//   for (d = kWidth / 2; d > 0; d /= 2) v += __shfl_down(v, d, kWidth);
+// leaves there: the same additions in the same order (lane i < d adds lane
+// i + d at level d).  Other lanes hold partial values and must not be used.
+// Level 32 uses v_permlane32_swap, level 16 v_permlane16_swap (gfx950), levels
+// 8..1 a DPP row shift; each is a VALU operation instead of a ds_bpermute
+// round trip.
+// ---------------------------------------------------------------------------
+#if defined(__HIP_DEVICE_COMPILE__)
+template <int kShift>
+__device__ __forceinline__ float row_from_higher(float v) {
+    // row_shl:kShift -- lane i reads lane i + kShift of its 16-lane row (0 past the row's end)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + kShift, 0xf, 0xf, true));
+}
+#endif
+
+template <int kWidth>
+__device__ __forceinline__ float wave_sum_down(float v) {
+    static_assert(kWidth == 64 || kWidth == 32, "wave_sum_down width");
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned bits = __float_as_uint(v);
+    if constexpr (kWidth == 64) {
+        // second result: lanes 0-31 hold the old lanes 32-63
+        v += __uint_as_float(__builtin_amdgcn_permlane32_swap(bits, bits, false, false)[1]);
+    }
+    {
+        // second result: rows 0 and 2 hold the old rows 1 and 3
+        const unsigned b = __float_as_uint(v);
+        v += __uint_as_float(__builtin_amdgcn_permlane16_swap(b, b, false, false)[1]);
+    }
+    v += row_from_higher<8>(v);
+    v += row_from_higher<4>(v);
+    v += row_from_higher<2>(v);
+    v += row_from_higher<1>(v);
+#endif
+    return v;
+}
+
+// ---------------------------------------------------------------------------
 // Errors: internal code throws; the C ABI maps exceptions to status codes.
 // ---------------------------------------------------------------------------
 class DeviceFailure final : public std::runtime_error {
@@ -101,9 +141,29 @@ struct GemvArgs {
     int rows = 1;
     int epilogue = kEpiStore;
     int mode = kModeAuto;
+    // Linked launch (rows == 1, exact order, K a multiple of 1024 up to 6144):
+    // the kernel may start while the previous launch of a chain is still
+    // running.  It requests its weights, waits until the previous launch's
+    // completion flag reaches (its step + link_bias), reads activations with
+    // device-coherent loads, stores with device-coherent stores and signals
+    // its own completion.  Counters are monotone (zeroed once at creation,
+    // never reset), so the same links serve every replay of a chain.
+    unsigned* link_counters = nullptr;    // this launch's kLinkWords words
+    const unsigned* link_wait = nullptr;  // the previous launch's counters (nullptr: no wait)
+    unsigned link_bias = 1;               // 1 within a step; 0 for a step's first launch
+    int* link_status = nullptr;           // set to 1 when a wait gave up (results invalid)
+    unsigned long long* link_trace = nullptr;  // optional diagnostics: 4 clock values per launch
 };
 
+// Words of one launch's link counters: 8 group counters, a total counter and 8
+// copies of the completion flag, each on its own 128-byte line.
+constexpr int kLinkLineWords = 32;
+constexpr int kLinkWords = 17 * kLinkLineWords;
+
 hipError_t launch_int8_gemv(const GemvArgs& args, hipStream_t stream);
+// Workgroups and resident workgroups per CU of the kernel launch_int8_gemv
+// would use for `args` (used to check that two linked launches fit at once).
+hipError_t gemv_launch_footprint(const GemvArgs& args, int* workgroups, int* per_cu);
 
 hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,
                                        int in_features, int out_features, hipStream_t stream);
