@@ -123,15 +123,36 @@ def cpu_baseline(seconds: float = 10.0):
     }
 
 
-def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3):
+# Config 3's algorithmic bytes: 15 steps x (5 predictor layers + the
+# 2048x1024 LM head), weights + scales + activations.
+PREDICTOR_CHAIN_BYTES = 1_218_232_320
+
+
+def predictor_chain_entry(ms):
+    """Median predictor GPU time of the greedy frames, as config 3's
+    effective bandwidth (its unique weights stay in the 256 MB Infinity
+    Cache across the 15 steps)."""
+    if not ms:
+        return None
+    med = sorted(ms)[len(ms) // 2]
+    return {"frames": len(ms), "sampling": "greedy argmax", "passes": 16,
+            "gpu_ms_median": round(med, 4),
+            "effective_gbs": round(PREDICTOR_CHAIN_BYTES / (med * 1e6), 1)}
+
+
+def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, greedy: int = 20):
     """Config 5 through the reference C ABI: VoiceDesign geometry, synthetic
     bf16 weights quantized to int8 at finalize, prompt of `prompt` tokens,
     then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed.  The
     prompt fills the KV cache so that the timed frames run at context
-    max_seq - frames .. max_seq (attention reads up to 1024 positions)."""
+    max_seq - frames .. max_seq (attention reads up to 1024 positions).
+    Before the timed frames, `greedy` frames run the code predictor with
+    greedy argmax (config 3: the 15-step predictor chain); its GPU time per
+    frame is reported separately (it covers 16 passes through the 5 layers:
+    the chain's 15 steps plus the pass that seeds it from the talker)."""
     import numpy as np
 
-    prompt = max_seq - frames - warm
+    prompt = max_seq - frames - warm - greedy
     lib = hip.load()
     cfg = hip.default_config()
     model = C.c_void_p()
@@ -203,22 +224,27 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3):
             codes = (C.c_uint16 * 16)()
             info = hip.CodecFrameInfo()
             nxt = C.c_uint16()
-            trailing = rng.integers(0, cfg.text_vocabulary, frames + 8).astype(np.int32)
+            trailing = rng.integers(0, cfg.text_vocabulary, frames + warm + greedy + 8).astype(np.int32)
             done = 0
             pred_ms = talk_ms = 0.0
+            greedy_ms = []
             eos = 0
             t_start = None
-            for f in range(frames + warm):
-                if f == warm:
+            greedy_ps = hip.sampling(0, 0, 1.0, 1.0, 1.0)
+            for f in range(frames + warm + greedy):
+                if f == warm + greedy:
                     hip.synchronize()
                     t_start = time.perf_counter()
                 if semantic.value == cfg.codec_eos_token:
                     eos += 1
                     break
-                hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts, ps, codes, 16,
-                         C.byref(nxt), C.byref(info))
+                chain = warm <= f < warm + greedy
+                hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts,
+                         greedy_ps if chain else ps, codes, 16, C.byref(nxt), C.byref(info))
                 semantic = C.c_uint16(nxt.value)
-                if f >= warm:
+                if chain:
+                    greedy_ms.append(info.predictor_gpu_milliseconds)
+                if f >= warm + greedy:
                     done += 1
                     pred_ms += info.predictor_gpu_milliseconds
                     talk_ms += info.talker_gpu_milliseconds
@@ -234,6 +260,7 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3):
                 "prefill_seconds": round(prefill_s, 3),
                 "ended_by_eos_early": bool(eos),
                 "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9; seed 42",
+                "predictor_chain_config3": predictor_chain_entry(greedy_ms),
             }
         finally:
             lib.qwen3_tts_session_destroy(session)

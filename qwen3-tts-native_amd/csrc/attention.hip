@@ -115,6 +115,28 @@ __device__ __forceinline__ void append_kv(const AttnArgs& a, int row, int kvh, i
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Exact score of one (query head, position): the reference's block_sum over
+// 256 threads where thread t < 128 holds q[t]k[t] and the rest zero.  Level
+// 128 adds zeros (a no-op up to the sign of a zero dot, which no later step
+// can observe); level 64 pairs t with t+64; then halves down to 1.  The dot
+// is rounded to bf16, scaled and rounded again.  kw: the key row as 64
+// packed bf16 pairs.
+__device__ __forceinline__ float exact_score(const float* qg, const uint32_t (&kw)[64], float scale) {
+    float s[64];
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+        const float kl = (t & 1) ? hi_bf(kw[t >> 1]) : lo_bf(kw[t >> 1]);
+        const float kh = (t & 1) ? hi_bf(kw[32 + (t >> 1)]) : lo_bf(kw[32 + (t >> 1)]);
+        s[t] = fmaf(qg[t], kl, 0.0f) + fmaf(qg[t + 64], kh, 0.0f);
+    }
+#pragma unroll
+    for (int w = 32; w > 0; w >>= 1) {
+#pragma unroll
+        for (int t = 0; t < w; ++t) s[t] += s[t + w];
+    }
+    return round_bf(round_bf(s[0]) * scale);
+}
+
 // ---------------------------------------------------------------------------
 // scores: grid (position blocks, kv heads, rows), 64 threads, lane = position
 // ---------------------------------------------------------------------------
@@ -176,23 +198,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
         const float* qg = q_lds[g];
         float score;
         if constexpr (kExact) {
-            // block_sum over 256 threads: thread t < 128 holds q[t]k[t],
-            // the rest zero.  Level 128 adds zeros (a no-op up to the sign of
-            // a zero dot, which no later step can observe); level 64 pairs
-            // t with t+64; then halves down to 1.
-            float s[64];
-#pragma unroll
-            for (int t = 0; t < 64; ++t) {
-                const float kl = (t & 1) ? hi_bf(kw[t >> 1]) : lo_bf(kw[t >> 1]);
-                const float kh = (t & 1) ? hi_bf(kw[32 + (t >> 1)]) : lo_bf(kw[32 + (t >> 1)]);
-                s[t] = fmaf(qg[t], kl, 0.0f) + fmaf(qg[t + 64], kh, 0.0f);
-            }
-#pragma unroll
-            for (int w = 32; w > 0; w >>= 1) {
-#pragma unroll
-                for (int t = 0; t < w; ++t) s[t] += s[t + w];
-            }
-            score = round_bf(round_bf(s[0]) * a.scale);
+            score = exact_score(qg, kw, a.scale);
         } else {
             float dot = 0.0f;
 #pragma unroll
@@ -211,10 +217,9 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
 __host__ __device__ constexpr int lds_stride(int capacity) { return (capacity + 31) / 32 * 32 + 4; }
 
 // Wave-wide max (order independent).
+// Maximum over the wave, in every lane (the whole wave must be active).
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
-    return v;
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_max_down(v))));
 }
 
 // ---------------------------------------------------------------------------
@@ -545,19 +550,7 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
         const float* qg = q_lds[g_score];
         float score;
         if constexpr (kExact) {
-            float sv[64];
-#pragma unroll
-            for (int t = 0; t < 64; ++t) {
-                const float kl = (t & 1) ? hi_bf(kw[t >> 1]) : lo_bf(kw[t >> 1]);
-                const float kh = (t & 1) ? hi_bf(kw[32 + (t >> 1)]) : lo_bf(kw[32 + (t >> 1)]);
-                sv[t] = fmaf(qg[t], kl, 0.0f) + fmaf(qg[t + 64], kh, 0.0f);
-            }
-#pragma unroll
-            for (int w = 32; w > 0; w >>= 1) {
-#pragma unroll
-                for (int t = 0; t < w; ++t) sv[t] += sv[t + w];
-            }
-            score = round_bf(round_bf(sv[0]) * a.scale);
+            score = exact_score(qg, kw, a.scale);
         } else {
             float dot = 0.0f;
 #pragma unroll
@@ -611,6 +604,216 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     a.output[(static_cast<size_t>(row) * a.query_heads + head) * kDim + d] = f2bf(y);
 }
 
+// ---------------------------------------------------------------------------
+// The code predictor's caches (<= 16 positions), exact order, fused QKV
+// epilogue: one wave per (query head, row) does everything, with no block
+// barrier.  Lane l holds elements l and l+64 of every 128-wide vector, which
+// is the layout the reference's tree needs: the exact score's
+// s[t] = q[t]k[t] + q[t+64]k[t+64] sits in lane t and its halving tree is a
+// wave shuffle-down tree (wave_sum_down).  The wave normalizes and rotates its
+// query head and (redundantly with the other waves of its GQA group) the new
+// key; the group's first wave appends the key and value to the caches.  All
+// key and value rows (the cache holds <= 16), and the rope rows of every
+// position, are requested before the position is known, so no load waits
+// for another.
+// ---------------------------------------------------------------------------
+constexpr int kShortCapacity = 16;
+
+template <int kG>
+__global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
+    const int row = blockIdx.y;
+    const int head = blockIdx.x;
+    const int kvh = head / kG;
+    const int lane = threadIdx.x;
+    const int kv_width = a.key_value_heads * kDim;
+    const bf16_t* raw = a.query + static_cast<size_t>(row) * a.query_stride;
+    const bf16_t* kraw = raw + static_cast<size_t>(a.query_heads + kvh) * kDim;
+    const bf16_t* vraw = raw + static_cast<size_t>(a.query_heads) * kDim + kv_width + static_cast<size_t>(kvh) * kDim;
+    const bf16_t* keys = row_keys(a, row) + static_cast<size_t>(kvh) * kDim;
+    const bf16_t* values = row_values(a, row) + static_cast<size_t>(kvh) * kDim;
+
+    // 1. every operand, with 16-byte loads (lane l: chunk l % 16 of row
+    //    4i + l / 16), staged through LDS into the lane-l / lane-(l+64)
+    //    layout; only the selections below depend on the position
+    __shared__ uint4 rows_lds[3][kShortCapacity][kDim / 8];  // rope, keys, values
+    __shared__ uint4 head_lds[5][kDim / 8];                  // q, k, v, q gain, k gain
+    const int position = a.positions[row];
+    const int chunk = lane & 15;
+    uint4 hv0, hv1 = make_uint4(0, 0, 0, 0);
+    {
+        const int part = lane >> 4;  // q, k, v, q gain
+        const bf16_t* src = part == 0 ? raw + head * kDim : part == 1 ? kraw : part == 2 ? vraw : a.q_norm;
+        hv0 = load_global16(src + chunk * 8);
+        if (lane < 16) hv1 = load_global16(a.k_norm + chunk * 8);
+    }
+    uint4 rv[4], kv4[4], vv4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = 4 * i + (lane >> 4);
+        const int pc = p < a.capacity ? p : a.capacity - 1;  // rows past the capacity: a valid row, unused
+        rv[i] = load_global16(a.rope_table + static_cast<size_t>(pc) * kDim + chunk * 8);
+        kv4[i] = load_global16(keys + static_cast<size_t>(pc) * kv_width + chunk * 8);
+        vv4[i] = load_global16(values + static_cast<size_t>(pc) * kv_width + chunk * 8);
+    }
+    head_lds[lane >> 4][chunk] = hv0;
+    if (lane < 16) head_lds[4][chunk] = hv1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = 4 * i + (lane >> 4);
+        rows_lds[0][p][chunk] = rv[i];
+        rows_lds[1][p][chunk] = kv4[i];
+        rows_lds[2][p][chunk] = vv4[i];
+    }
+    // one wave: its LDS writes precede its reads
+    const bf16_t* hl = reinterpret_cast<const bf16_t*>(head_lds);
+    head_detail::HeadInputs q_in, k_in;
+    q_in.x0 = bf2f(hl[lane]);
+    q_in.x1 = bf2f(hl[lane + 64]);
+    k_in.x0 = bf2f(hl[kDim + lane]);
+    k_in.x1 = bf2f(hl[kDim + lane + 64]);
+    const float v_new0 = bf2f(hl[2 * kDim + lane]);
+    const float v_new1 = bf2f(hl[2 * kDim + lane + 64]);
+    q_in.g0 = bf2f(hl[3 * kDim + lane]);
+    q_in.g1 = bf2f(hl[3 * kDim + lane + 64]);
+    k_in.g0 = bf2f(hl[4 * kDim + lane]);
+    k_in.g1 = bf2f(hl[4 * kDim + lane + 64]);
+    const bf16_t* rl = reinterpret_cast<const bf16_t*>(rows_lds[0][position]);
+    q_in.c = k_in.c = bf2f(rl[2 * lane]);
+    q_in.s = k_in.s = bf2f(rl[2 * lane + 1]);
+    float v0[kShortCapacity], v1[kShortCapacity];
+#pragma unroll
+    for (int p = 0; p < kShortCapacity; ++p) {
+        const bf16_t* vl = reinterpret_cast<const bf16_t*>(rows_lds[2][p]);
+        v0[p] = bf2f(vl[lane]);
+        v1[p] = bf2f(vl[lane + 64]);
+    }
+
+    // 2. head norm + RoPE of the query head and the new key; the append
+    bf16_t q0b, q1b, kn0, kn1;
+    head_detail::norm_rope_from(q_in, a.epsilon, q0b, q1b);
+    head_detail::norm_rope_from(k_in, a.epsilon, kn0, kn1);
+    if (head % kG == 0) {
+        bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
+                       static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+        bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
+                       static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
+        kdst[lane] = kn0;
+        kdst[lane + 64] = kn1;
+        vdst[lane] = f2bf(v_new0);
+        vdst[lane + 64] = f2bf(v_new1);
+    }
+    // the current position's key and value come from qkv, not the cache
+    bf16_t* q_l = reinterpret_cast<bf16_t*>(head_lds[0]);
+    bf16_t* k_l = reinterpret_cast<bf16_t*>(rows_lds[1][position]);
+    q_l[lane] = q0b;
+    q_l[lane + 64] = q1b;
+    k_l[lane] = kn0;
+    k_l[lane + 64] = kn1;
+#pragma unroll
+    for (int p = 0; p < kShortCapacity; ++p) {
+        if (p == position) {
+            v0[p] = v_new0;
+            v1[p] = v_new1;
+        }
+    }
+
+    // 3. scores.  Lane L = 16 j + p works on position p and the tree's
+    //    entries t = 8 j + i (i < 8) of level 32: it forms
+    //    (P[t] + P[t+64]) + (P[t+32] + P[t+96]) itself (P = q*k), receives
+    //    level 16's partner (t + 16, lane L + 32) and level 8's (t + 8, lane
+    //    L + 16) through lane swaps, and folds levels 4, 2, 1 in registers --
+    //    the reference tree's additions in its order.  Lane p ends with
+    //    position p's dot.
+    const int length = position + 1;
+    const bool live = lane < length;
+    float score;
+    {
+        const int sp = lane & 15;
+        const int j = lane >> 4;
+        const uint4* qv = reinterpret_cast<const uint4*>(head_lds[0]);
+        const uint4* kv = rows_lds[1][sp];
+        float t8[8];
+        const uint4 qa = qv[j], qb = qv[4 + j], qc = qv[8 + j], qd = qv[12 + j];  // t, t+32, t+64, t+96
+        const uint4 ka = kv[j], kb = kv[4 + j], kc = kv[8 + j], kd = kv[12 + j];
+        const uint32_t qw[4][4] = {{qa.x, qa.y, qa.z, qa.w}, {qb.x, qb.y, qb.z, qb.w},
+                                   {qc.x, qc.y, qc.z, qc.w}, {qd.x, qd.y, qd.z, qd.w}};
+        const uint32_t kw4[4][4] = {{ka.x, ka.y, ka.z, ka.w}, {kb.x, kb.y, kb.z, kb.w},
+                                    {kc.x, kc.y, kc.z, kc.w}, {kd.x, kd.y, kd.z, kd.w}};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            auto el = [&](const uint32_t (&w)[4][4], int part) {
+                return (i & 1) ? hi_bf(w[part][i >> 1]) : lo_bf(w[part][i >> 1]);
+            };
+            const float lo = fmaf(el(qw, 0), el(kw4, 0), 0.0f) + fmaf(el(qw, 2), el(kw4, 2), 0.0f);  // level 64, t
+            const float hi = fmaf(el(qw, 1), el(kw4, 1), 0.0f) + fmaf(el(qw, 3), el(kw4, 3), 0.0f);  // level 64, t+32
+            t8[i] = lo + hi;                                                                            // level 32
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // level 16: lanes 0-31 add lanes 32-63
+            const unsigned b = __float_as_uint(t8[i]);
+            t8[i] += __uint_as_float(__builtin_amdgcn_permlane32_swap(b, b, false, false)[1]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // level 8: row 0 adds row 1
+            const unsigned b = __float_as_uint(t8[i]);
+            t8[i] += __uint_as_float(__builtin_amdgcn_permlane16_swap(b, b, false, false)[1]);
+        }
+#pragma unroll
+        for (int w = 4; w > 0; w >>= 1) {
+#pragma unroll
+            for (int i = 0; i < w; ++i) t8[i] += t8[i + w];
+        }
+        score = live ? round_bf(round_bf(t8[0]) * a.scale) : -INFINITY;
+    }
+
+    // 4. softmax, lane = position; the normalizer in position order
+    const float maximum = wave_max(score);
+    const float e = live ? q3_expf(score - maximum) : 0.0f;
+    // the 16 exponentials (0 past the current position) to every lane
+    // through LDS; adding the trailing zeros leaves the sequential sum as is
+    __shared__ float4 e_lds[kShortCapacity / 4], p_lds[kShortCapacity / 4];
+    if (lane < kShortCapacity) reinterpret_cast<float*>(e_lds)[lane] = e;
+    float ev[kShortCapacity];
+#pragma unroll
+    for (int i = 0; i < kShortCapacity / 4; ++i) {
+        const float4 t = e_lds[i];
+        ev[4 * i] = t.x;
+        ev[4 * i + 1] = t.y;
+        ev[4 * i + 2] = t.z;
+        ev[4 * i + 3] = t.w;
+    }
+    float denominator = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kShortCapacity; ++p) denominator += ev[p];
+    const float inverse = 1.0f / denominator;
+    const float prob = live ? round_bf(e * inverse) : 0.0f;
+    if (lane < kShortCapacity) reinterpret_cast<float*>(p_lds)[lane] = prob;
+    float pv[kShortCapacity];
+#pragma unroll
+    for (int i = 0; i < kShortCapacity / 4; ++i) {
+        const float4 t = p_lds[i];
+        pv[4 * i] = t.x;
+        pv[4 * i + 1] = t.y;
+        pv[4 * i + 2] = t.z;
+        pv[4 * i + 3] = t.w;
+    }
+
+    // 5. value chains for dimensions lane and lane + 64, positions in order.
+    //    Past the current position the value is replaced by 0 (and its
+    //    probability is 0): fmaf(0, 0, acc) == acc exactly, for every acc the
+    //    chain can hold (it starts at +0 and never becomes -0).
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kShortCapacity; ++p) {
+        const bool in = p <= position;
+        acc0 = fmaf(pv[p], in ? v0[p] : 0.0f, acc0);
+        acc1 = fmaf(pv[p], in ? v1[p] : 0.0f, acc1);
+    }
+    bf16_t* out = a.output + (static_cast<size_t>(row) * a.query_heads + head) * kDim;
+    out[lane] = f2bf(acc0);
+    out[lane + 64] = f2bf(acc1);
+}
+
 template <bool kExact, int kG>
 hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
     const size_t head_lds = static_cast<size_t>(kG) * lds_stride(a.capacity) * sizeof(float);
@@ -626,6 +829,10 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         if (st != hipSuccess) return st;
         configured = true;
     }
+    if (kExact && a.capacity <= kShortCapacity && a.q_norm != nullptr) {
+        attention_short_exact_kernel<kG><<<dim3(a.query_heads, rows), 64, 0, stream>>>(a);
+        return hipGetLastError();
+    }
     if (a.capacity <= kSmallCapacity) {
         attention_small_kernel<kExact, kG><<<dim3(a.key_value_heads, rows), kG * kDim, 0, stream>>>(a);
         return hipGetLastError();
@@ -637,6 +844,7 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
 }
 
 }  // namespace
+
 
 size_t attention_workspace_bytes(int rows, int query_heads, int capacity) {
     return static_cast<size_t>(rows) * query_heads * (static_cast<size_t>(capacity) + 1) * sizeof(float);

@@ -87,6 +87,22 @@ __device__ __forceinline__ float wave_sum_down(float v) {
     return v;
 }
 
+// Maximum over the wave (order independent), valid in lane 0; the same
+// cross-lane steps as wave_sum_down.
+__device__ __forceinline__ float wave_max_down(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const unsigned bits = __float_as_uint(v);
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_permlane32_swap(bits, bits, false, false)[1]));
+    const unsigned b = __float_as_uint(v);
+    v = fmaxf(v, __uint_as_float(__builtin_amdgcn_permlane16_swap(b, b, false, false)[1]));
+    v = fmaxf(v, row_from_higher<8>(v));
+    v = fmaxf(v, row_from_higher<4>(v));
+    v = fmaxf(v, row_from_higher<2>(v));
+    v = fmaxf(v, row_from_higher<1>(v));
+#endif
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // Errors: internal code throws; the C ABI maps exceptions to status codes.
 // ---------------------------------------------------------------------------

@@ -870,6 +870,7 @@ private:
         return v == nullptr || std::strcmp(v, "1") != 0;
     }
 
+
     // One decoder stack step (talker.cu:3251-3456) at the position held in
     // *position (device).  predictor selects the 5-layer code predictor.
     void run_decoder(bool predictor, const int* position, int) {

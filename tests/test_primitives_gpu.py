@@ -135,7 +135,8 @@ def test_attention_groups_and_ring_edges(hip, orc, exact, qh, kvh, length, max_s
 
 @pytest.mark.parametrize("exact", [1, 0])
 @pytest.mark.parametrize("qh,kvh", [(16, 8), (16, 4)])
-@pytest.mark.parametrize("positions,max_seq", [([0], 16), ([15], 16), ([63], 64), ([64], 100), ([700], 1024),
+@pytest.mark.parametrize("positions,max_seq", [([0], 16), ([1], 16), ([7], 16), ([15], 16), ([5], 8),
+                                               ([0, 9, 15], 16), ([63], 64), ([64], 100), ([700], 1024),
                                                ([1023], 1024), ([3, 40, 99], 100)])
 def test_decode_attention_fused_matches_separate_ops(hip, orc, exact, qh, kvh, positions, max_seq):
     """The fused decode step (head norm + RoPE + KV append + attention) equals
@@ -331,3 +332,4 @@ def test_device_buffer_sequential_upload(hip):
         assert lib.qwen3_tts_device_buffer_data(buf)
     finally:
         lib.qwen3_tts_device_buffer_destroy(buf)
+

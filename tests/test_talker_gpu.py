@@ -257,3 +257,36 @@ def test_model_contract_errors(hip):
             hip.call("qwen3_tts_session_create", model, 64, 0, C.byref(s), C.byref(smem))
     finally:
         lib.qwen3_tts_model_destroy(model)
+
+
+@pytest.fixture(scope="module")
+def toy_wide(hip, orc):
+    c = toy_model.TOY_WIDE_PREDICTOR
+    weights = toy_model.make_weights(c, seed=4)
+    model, mem = toy_model.upload(hip, c, weights)
+    om = toy_model.OracleModel(orc, c, weights)
+    yield model, om
+    hip.load().qwen3_tts_model_destroy(model)
+
+
+def test_wide_predictor_frames_match_oracle(hip, orc, toy_wide):
+    """The production predictor head geometry (16 query / 8 kv heads, the
+    one-wave-per-head short-cache attention) gives the oracle's frames."""
+    model, om = toy_wide
+    rng = np.random.default_rng(21)
+    text, codec = prompt(rng, 6)
+    s, _ = new_session(hip, model, max_seq=64, seed=13)
+    try:
+        osess = toy_model.OracleSession(om, 64, 13)
+        semantic = gpu_prefill(hip, s, text, codec, TALKER_TOPK).first_semantic_token
+        assert semantic == osess.prefill(text, codec, TALKER_TOPK)
+        for f in range(5):
+            if semantic == TOY["codec_eos_token"]:
+                break
+            codes, nxt, _ = gpu_frame(hip, s, semantic, 7 + f, TALKER_TOPK, PREDICTOR_TOPK)
+            ocodes, onxt = osess.frame(semantic, 7 + f, TALKER_TOPK, PREDICTOR_TOPK)
+            assert np.array_equal(codes, ocodes), (f, codes, ocodes)
+            assert nxt == onxt
+            semantic = nxt
+    finally:
+        hip.load().qwen3_tts_session_destroy(s)

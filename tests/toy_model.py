@@ -22,6 +22,10 @@ TOY = dict(talker_layers=2, talker_hidden=512, talker_intermediate=1024, talker_
            head_dimension=128, talker_vocabulary=3072, predictor_vocabulary=2048,
            text_vocabulary=1000, codec_eos_token=2150, rms_epsilon=1e-6, rope_theta=1e6)
 
+# The same, with the production predictor's head geometry (16 query / 8 kv
+# heads).
+TOY_WIDE_PREDICTOR = dict(TOY, predictor_query_heads=16, predictor_key_value_heads=8)
+
 
 def tensor_specs(c: dict):
     """(name, shape, kind) for every tensor of the checkpoint."""
