@@ -212,9 +212,10 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     }
 }
 
-// Row stride of the probability table in LDS: room for whole chunks, 16-byte
-// aligned, and offset by four banks between query heads.
-__host__ __device__ constexpr int lds_stride(int capacity) { return (capacity + 31) / 32 * 32 + 4; }
+// Row stride of the probability table in LDS: whole 64-position blocks plus
+// one (the exact normalizer's look-ahead block), 16-byte aligned, and offset
+// by four banks between query heads.
+__host__ __device__ constexpr int lds_stride(int capacity) { return ((capacity + 63) / 64 + 1) * 64 + 4; }
 
 // Wave-wide max (order independent).
 // Maximum over the wave, in every lane (the whole wave must be active).
@@ -290,62 +291,42 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
         maximum[gg] = wave_max(m);
     }
 
-    // 3. exponentials (each lane its own positions), then the normalizer
+    // 3. exponentials (each lane its own positions) and the normalizer
     float* eg = p_lds;
-    float partial[kG][4];
-#pragma unroll
-    for (int gg = 0; gg < kG; ++gg) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) partial[gg][j] = 0.0f;
-        for (int base = 0; base < length; base += 8 * 64) {
-            float t[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int p = base + u * 64 + lane;
-                t[u] = p < length ? eg[gg * stride + p] : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int p = base + u * 64 + lane;
-                if (p < length) {
-                    const float w = q3_expf(t[u] - maximum[gg]);
-                    eg[gg * stride + p] = w;
-                    if constexpr (!kExact) partial[gg][(p >> 6) & 3] += w;  // thread (p mod 256)'s partial
-                }
-            }
-        }
-    }
-    __syncthreads();
     if constexpr (kExact) {
         // thread 0 of the reference's block: one sequential sum per head, the
-        // G heads in G lanes of the same instructions
-        if (lane < kG) {
-            // 32 values per step; the next step's reads are issued before
-            // this step's adds (the add chain, not LDS latency, sets the pace)
-            const float* e = p_lds + lane * stride;
-            float denominator = 0.0f;
-            int p = 0;
-            float4 cur[8];
+        // G heads in lanes 0..G-1 of the same instructions.  Blocks of 64
+        // positions: the exponentials of block b+1 (all lanes) are computed
+        // in the same straight-line code as the sum over block b (a chain of
+        // dependent adds that leaves the issue slots free), so the two
+        // overlap.  Positions past the length hold exponential 0 (x + 0 == x
+        // for the non-negative running sum), up to one block past the end.
+        auto exps = [&](int block) {
+            const int p = block * 64 + lane;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) cur[u] = *reinterpret_cast<const float4*>(e + 4 * u);
-            for (; p + 32 <= length; p += 32) {
-                const int next = p + 64 <= length ? p + 32 : p;  // re-read in the last step
-                float4 nxt[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) nxt[u] = *reinterpret_cast<const float4*>(e + next + 4 * u);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    denominator += cur[u].x;
-                    denominator += cur[u].y;
-                    denominator += cur[u].z;
-                    denominator += cur[u].w;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+            for (int gg = 0; gg < kG; ++gg) {
+                const float t = eg[gg * stride + min(p, length - 1)];
+                eg[gg * stride + p] = p < length ? q3_expf(t - maximum[gg]) : 0.0f;
             }
-            for (; p < length; ++p) denominator += e[p];
-            inverse_lds[lane] = 1.0f / denominator;
+        };
+        const int blocks = (length + 63) / 64;
+        const float4* mine = reinterpret_cast<const float4*>(p_lds + (lane < kG ? lane : 0) * stride);
+        float denominator = 0.0f;
+        exps(0);
+        for (int b = 0; b < blocks; ++b) {
+            float4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = mine[b * 16 + u];  // block b, requested first
+            exps(b + 1);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                denominator += v[u].x;
+                denominator += v[u].y;
+                denominator += v[u].z;
+                denominator += v[u].w;
+            }
         }
+        if (lane < kG) inverse_lds[lane] = 1.0f / denominator;
         __syncthreads();
 #pragma unroll
         for (int gg = 0; gg < kG; ++gg) {
@@ -363,6 +344,29 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
             }
         }
     } else {
+        float partial[kG][4];
+#pragma unroll
+        for (int gg = 0; gg < kG; ++gg) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) partial[gg][j] = 0.0f;
+            for (int base = 0; base < length; base += 8 * 64) {
+                float t[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int p = base + u * 64 + lane;
+                    t[u] = p < length ? eg[gg * stride + p] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int p = base + u * 64 + lane;
+                    if (p < length) {
+                        const float w = q3_expf(t[u] - maximum[gg]);
+                        eg[gg * stride + p] = w;
+                        partial[gg][(p >> 6) & 3] += w;  // thread (p mod 256)'s partial
+                    }
+                }
+            }
+        }
         // 256 strided partials: lane l holds those of threads l, l+64,
         // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
         // local, the rest a wave tree.
