@@ -65,6 +65,12 @@ struct AttnArgs {
     const bf16_t* k_norm;
     const bf16_t* rope_table;  // [positions][64][cos, sin] bf16
     float epsilon;
+    // Value caches are dimension-major: element (position p, kv head h,
+    // dimension d) at [(h * 128 + d) * stride + p], so one (head, dimension)
+    // holds its positions contiguously.  stride >= capacity, a multiple of 8;
+    // per row from value_strides when that is set.
+    int value_stride;
+    const int* value_strides;
 };
 
 __device__ __forceinline__ int row_length(const AttnArgs& a, int row) {
@@ -77,6 +83,24 @@ __device__ __forceinline__ const bf16_t* row_keys(const AttnArgs& a, int row) {
 
 __device__ __forceinline__ const bf16_t* row_values(const AttnArgs& a, int row) {
     return a.value_bases != nullptr ? a.value_bases[row] : a.value_cache;
+}
+
+__device__ __forceinline__ int row_value_stride(const AttnArgs& a, int row) {
+    return a.value_strides != nullptr ? a.value_strides[row] : a.value_stride;
+}
+
+// Start of the positions of (kv head kvh, dimension d) in row's value cache.
+__device__ __forceinline__ bf16_t* value_run(const AttnArgs& a, int row, int kvh, int d) {
+    return const_cast<bf16_t*>(row_values(a, row)) +
+           static_cast<size_t>(kvh * kDim + d) * static_cast<size_t>(row_value_stride(a, row));
+}
+
+// Value of the current position, dimensions lane and lane + 64 of kv head
+// kvh, into the dimension-major cache.
+__device__ __forceinline__ void append_value(const AttnArgs& a, int row, int kvh, int position, int lane, bf16_t v0,
+                                             bf16_t v1) {
+    value_run(a, row, kvh, lane)[position] = v0;
+    value_run(a, row, kvh, lane + 64)[position] = v1;
 }
 
 // Cache rows are reached through pointer tables, which the compiler cannot
@@ -104,12 +128,9 @@ __device__ __forceinline__ void append_kv(const AttnArgs& a, int row, int kvh, i
     v1 = vraw[lane + 64];
     bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
                    static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
-    bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
-                   static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
     kdst[lane] = k0;
     kdst[lane + 64] = k1;
-    vdst[lane] = v0;
-    vdst[lane + 64] = v1;
+    append_value(a, row, kvh, position, lane, v0, v1);
 }
 
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
@@ -215,7 +236,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
 // Row stride of the probability table in LDS: whole 64-position blocks plus
 // one (the exact normalizer's look-ahead block), 16-byte aligned, and offset
 // by four banks between query heads.
-__host__ __device__ constexpr int lds_stride(int capacity) { return ((capacity + 63) / 64 + 1) * 64 + 4; }
+__host__ __device__ constexpr int lds_stride(int capacity) { return (capacity + 127) / 128 * 128 + 64; }
 
 // Wave-wide max (order independent).
 // Maximum over the wave, in every lane (the whole wave must be active).
@@ -224,99 +245,121 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// softmax + values: grid (kv heads * 2G slices, rows), one wave.
-// Lane = (g, dim): g = lane / (64/G), dim = slice * (64/G) + lane % (64/G).
-// One 16-byte load per lane covers 8 dims of one position, so one wave load
-// covers 8G positions ("a chunk").  The value ring is requested first; the
-// softmax of the group's G heads (redone by each of the 2G slice waves, in
-// parallel) runs while it is in flight.
+// softmax + values: grid (query heads * 2, rows), one wave per (row, query
+// head, half of the head dimension); lane = dimension.
+//   1. the lane's value run (dimension-major cache) is requested first,
+//      8 positions per 16-byte load, kRing loads ahead;
+//   2. the head's scores into LDS, the maximum;
+//   3. exponentials and the normalizer (exact: the sequential sum of one
+//      thread, overlapped with the exponentials of the next block; fast: the
+//      256-thread strided partials and tree), then the probabilities;
+//   4. the chain over positions: the probability of position 16k + j reaches
+//      every lane by a DPP row broadcast of a register holding positions
+//      16k .. 16k+15 in each row's 16 lanes, the value by a byte permute of the
+//      lane's own load -- three VALU operations per position.
+// Positions past the length carry probability 0 up to the end of the last
+// ring round; full rounds run in a loop without side exits, the last partial
+// round masks its values.
 // ---------------------------------------------------------------------------
+template <int kJ>
+__device__ __forceinline__ float row_broadcast(float v) {
+    // row_newbcast:kJ -- every lane reads lane kJ of its own 16-lane row
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + kJ, 0xf, 0xf, true));
+}
+
+template <int kJ0>
+__device__ __forceinline__ float chain8(float acc, const uint4& w, float q, int live) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float v = e < live ? __uint_as_float((e & 1) ? (words[e >> 1] & 0xffff0000u) : (words[e >> 1] << 16))
+                                 : 0.0f;
+        float p;
+        switch (kJ0 + e) {  // compile-time lane of the broadcast
+            case 0: p = row_broadcast<0>(q); break;
+            case 1: p = row_broadcast<1>(q); break;
+            case 2: p = row_broadcast<2>(q); break;
+            case 3: p = row_broadcast<3>(q); break;
+            case 4: p = row_broadcast<4>(q); break;
+            case 5: p = row_broadcast<5>(q); break;
+            case 6: p = row_broadcast<6>(q); break;
+            case 7: p = row_broadcast<7>(q); break;
+            case 8: p = row_broadcast<8>(q); break;
+            case 9: p = row_broadcast<9>(q); break;
+            case 10: p = row_broadcast<10>(q); break;
+            case 11: p = row_broadcast<11>(q); break;
+            case 12: p = row_broadcast<12>(q); break;
+            case 13: p = row_broadcast<13>(q); break;
+            case 14: p = row_broadcast<14>(q); break;
+            default: p = row_broadcast<15>(q); break;
+        }
+        acc = fmaf(p, v, acc);
+    }
+    return acc;
+}
+
 template <bool kExact, int kG>
 __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
-    constexpr int kSliceDims = 64 / kG;
-    constexpr int kLanesPerPos = kSliceDims / 8;
-    constexpr int kPos = 64 / kLanesPerPos;  // positions per chunk
-    extern __shared__ __align__(16) float p_lds[];  // [kG][stride]
-    __shared__ __align__(16) bf16_t v_lds[2][kPos * kSliceDims];
-    __shared__ float inverse_lds[kG];
+    extern __shared__ __align__(16) float p_lds[];  // scores, then exponentials, then probabilities
     const int row = blockIdx.y;
-    const int kvh = blockIdx.x / (2 * kG);
-    const int slice = blockIdx.x % (2 * kG);
+    const int head = blockIdx.x >> 1;
+    const int half = blockIdx.x & 1;
+    const int kvh = head / kG;
     const int lane = threadIdx.x;
-    const int g = lane / kSliceDims;
-    const int dl = lane % kSliceDims;
     const int length = row_length(a, row);
-    const int stride = lds_stride(a.capacity);
-    const int chunks = (length + kPos - 1) / kPos;
 
-    // 1. value ring: chunks 0..kRing-1 in flight
-    const int kv_width = a.key_value_heads * kDim;
-    const bf16_t* vbase = row_values(a, row) + static_cast<size_t>(kvh) * kDim + slice * kSliceDims +
-                          (lane % kLanesPerPos) * 8;
-    const int lane_pos = lane / kLanesPerPos;
-    auto load = [&](int c) {
-        int pos = c * kPos + lane_pos;
-        pos = pos < length ? pos : length - 1;  // never past this row's last written position
-        return load_global16(vbase + static_cast<size_t>(pos) * kv_width);
-    };
+    // 1. value ring
+    const bf16_t* vrun = value_run(a, row, kvh, half * 64 + lane);
+    const int last_group = row_value_stride(a, row) / 8 - 1;
+    auto load = [&](int i) { return load_global16(vrun + 8 * (i < last_group ? i : last_group)); };
     uint4 ring[kRing];
 #pragma unroll
     for (int k = 0; k < kRing; ++k) ring[k] = load(k);
     asm volatile("" ::: "memory");  // in flight before the scores are requested
 
-    // 2. scores of the group's heads into LDS, 16 loads in flight per lane
-    const float* scores = a.scores + (static_cast<size_t>(row) * a.query_heads + static_cast<size_t>(kvh) * kG) *
-                                         a.capacity;
-    float maximum[kG];
+    // 2. this head's scores into LDS, 16 loads in flight per lane
+    const float* src = a.scores + (static_cast<size_t>(row) * a.query_heads + head) * a.capacity;
+    float m = -INFINITY;
+    for (int base = 0; base < length; base += 16 * 64) {
+        float t[16];
 #pragma unroll
-    for (int gg = 0; gg < kG; ++gg) {
-        const float* src = scores + static_cast<size_t>(gg) * a.capacity;
-        float m = -INFINITY;
-        for (int base = 0; base < length; base += 16 * 64) {
-            float t[16];
+        for (int u = 0; u < 16; ++u) {
+            const int p = base + u * 64 + lane;
+            t[u] = src[p < length ? p : length - 1];
+        }
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int p = base + u * 64 + lane;
-                t[u] = src[p < length ? p : length - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int p = base + u * 64 + lane;
-                if (p < length) {
-                    p_lds[gg * stride + p] = t[u];
-                    m = fmaxf(m, t[u]);
-                }
+        for (int u = 0; u < 16; ++u) {
+            const int p = base + u * 64 + lane;
+            if (p < length) {
+                p_lds[p] = t[u];
+                m = fmaxf(m, t[u]);
             }
         }
-        maximum[gg] = wave_max(m);
     }
+    const float maximum = wave_max(m);
+    const int padded = (length + kRing * 8 - 1) / (kRing * 8) * (kRing * 8);  // end of the last ring round
 
-    // 3. exponentials (each lane its own positions) and the normalizer
-    float* eg = p_lds;
+    // 3. exponentials, normalizer, probabilities
+    float inverse = 1.0f;
     if constexpr (kExact) {
-        // thread 0 of the reference's block: one sequential sum per head, the
-        // G heads in lanes 0..G-1 of the same instructions.  Blocks of 64
-        // positions: the exponentials of block b+1 (all lanes) are computed
-        // in the same straight-line code as the sum over block b (a chain of
-        // dependent adds that leaves the issue slots free), so the two
-        // overlap.  Positions past the length hold exponential 0 (x + 0 == x
-        // for the non-negative running sum), up to one block past the end.
+        // thread 0 of the reference's block: one sequential sum (every lane
+        // runs the same additions on the same values).  Blocks of 64
+        // positions: the sum over block b is interleaved with the
+        // exponentials of block b+1; exponentials past the length are 0
+        // (x + 0 == x for the non-negative running sum).
         auto exps = [&](int block) {
             const int p = block * 64 + lane;
-#pragma unroll
-            for (int gg = 0; gg < kG; ++gg) {
-                const float t = eg[gg * stride + min(p, length - 1)];
-                eg[gg * stride + p] = p < length ? q3_expf(t - maximum[gg]) : 0.0f;
-            }
+            const float t = p_lds[p < length ? p : length - 1];
+            p_lds[p] = p < length ? q3_expf(t - maximum) : 0.0f;
         };
         const int blocks = (length + 63) / 64;
-        const float4* mine = reinterpret_cast<const float4*>(p_lds + (lane < kG ? lane : 0) * stride);
+        const float4* all = reinterpret_cast<const float4*>(p_lds);
         float denominator = 0.0f;
         exps(0);
         for (int b = 0; b < blocks; ++b) {
             float4 v[16];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = mine[b * 16 + u];  // block b, requested first
+            for (int u = 0; u < 16; ++u) v[u] = all[b * 16 + u];  // block b, requested first
             exps(b + 1);
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
@@ -326,124 +369,60 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
                 denominator += v[u].w;
             }
         }
-        if (lane < kG) inverse_lds[lane] = 1.0f / denominator;
-        __syncthreads();
-#pragma unroll
-        for (int gg = 0; gg < kG; ++gg) {
-            const float inverse = inverse_lds[gg];
-            // 8 positions per lane per batch: reads first, then the products
-            for (int base = 0; base < length; base += 8 * 64) {
-                float t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = eg[gg * stride + min(base + u * 64 + lane, length - 1)];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int p = base + u * 64 + lane;
-                    if (p < length) eg[gg * stride + p] = round_bf(t[u] * inverse);
-                }
-            }
-        }
+        const float inv = 1.0f / denominator;
+        for (int p = lane; p < padded; p += 64) p_lds[p] = p < length ? round_bf(p_lds[p] * inv) : 0.0f;
     } else {
-        float partial[kG][4];
-#pragma unroll
-        for (int gg = 0; gg < kG; ++gg) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) partial[gg][j] = 0.0f;
-            for (int base = 0; base < length; base += 8 * 64) {
-                float t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int p = base + u * 64 + lane;
-                    t[u] = p < length ? eg[gg * stride + p] : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int p = base + u * 64 + lane;
-                    if (p < length) {
-                        const float w = q3_expf(t[u] - maximum[gg]);
-                        eg[gg * stride + p] = w;
-                        partial[gg][(p >> 6) & 3] += w;  // thread (p mod 256)'s partial
-                    }
-                }
-            }
-        }
         // 256 strided partials: lane l holds those of threads l, l+64,
         // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
-        // local, the rest a wave tree.
+        // local, the rest a wave tree.  The weights stay unnormalized; the
+        // chain's result is scaled by 1/sum.
+        float partial[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int base = 0; base < padded; base += 8 * 64) {
+            float t[8];
 #pragma unroll
-        for (int gg = 0; gg < kG; ++gg) {
-            float p0 = partial[gg][0] + partial[gg][2];
-            float p1 = partial[gg][1] + partial[gg][3];
-            const float value = wave_sum_down<64>(p0 + p1);
-            if (lane == 0) inverse_lds[gg] = 1.0f / value;
+            for (int u = 0; u < 8; ++u) {
+                const int p = base + u * 64 + lane;
+                t[u] = p_lds[p < length ? p : length - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = base + u * 64 + lane;
+                if (p < padded) {
+                    const float w = p < length ? q3_expf(t[u] - maximum) : 0.0f;
+                    p_lds[p] = w;
+                    if (p < length) partial[(p >> 6) & 3] += w;  // thread (p mod 256)'s partial
+                }
+            }
         }
+        const float p0 = partial[0] + partial[2];
+        const float p1 = partial[1] + partial[3];
+        inverse = 1.0f / __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum_down<64>(p0 + p1))));
     }
-    __syncthreads();
 
-    // 4. the value chains.  Chunk c+1 is written to LDS and read into
-    // registers while chunk c is being accumulated.
-    const float* pg = p_lds + g * stride;
+    // 4. the value chain, rounds of kRing loads (8 positions each); the last,
+    //    partial round replaces values past the length by 0 (positions
+    //    there were never written for this sequence), so each fmaf adds
+    //    0 * 0 -- the running sum starts at +0 and never becomes -0.
+    const float* pq = p_lds + (lane & 15);
     float acc = 0.0f;
-    float vcur[kPos], pcur[kPos], vnext[kPos], pnext[kPos];
-    auto fetch = [&](const bf16_t* slot, int c, float* v, float* pv) {
+    auto round = [&](int base, int live) {
 #pragma unroll
-        for (int j = 0; j < kPos; ++j) v[j] = bf2f(slot[j * kSliceDims + dl]);
-#pragma unroll
-        for (int j = 0; j < kPos; j += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(pg + c * kPos + j);
-            pv[j] = t.x;
-            pv[j + 1] = t.y;
-            pv[j + 2] = t.z;
-            pv[j + 3] = t.w;
+        for (int k = 0; k < kRing; k += 2) {
+            const int i = base / 8 + k;  // groups i and i+1: positions 8i .. 8i+15
+            const float q = pq[8 * i];
+            const uint4 w0 = ring[k];
+            const uint4 w1 = ring[k + 1];
+            ring[k] = load(i + kRing);
+            ring[k + 1] = load(i + 1 + kRing);
+            acc = chain8<0>(acc, w0, q, live - 8 * k);
+            acc = chain8<8>(acc, w1, q, live - 8 * k - 8);
         }
     };
-    auto accumulate = [&](int c, const float* v, const float* pv) {
-        const int first = c * kPos;
-        if (first + kPos <= length) {
-#pragma unroll
-            for (int j = 0; j < kPos; ++j) acc = fmaf(pv[j], v[j], acc);
-        } else {
-#pragma unroll
-            for (int j = 0; j < kPos; ++j) {
-                if (first + j < length) acc = fmaf(pv[j], v[j], acc);
-            }
-        }
-    };
-    reinterpret_cast<uint4*>(v_lds[0])[lane] = ring[0];
-    ring[0] = load(kRing);
-    asm volatile("" ::: "memory");
-    fetch(v_lds[0], 0, vcur, pcur);
-    bool done = false;
-    for (int base = 0; !done; base += kRing) {
-#pragma unroll
-        for (int k = 0; k < kRing; ++k) {
-            const int c = base + k;
-            const int kNext = (k + 1) % kRing;
-            // stage chunk c+1 (its ring slot is kNext); past the last chunk
-            // this only re-reads valid rows and stays unused
-            bf16_t* slot = v_lds[(k + 1) & 1];
-            reinterpret_cast<uint4*>(slot)[lane] = ring[kNext];
-            ring[kNext] = load(c + 1 + kRing);
-            asm volatile("" ::: "memory");  // issue the refill here
-            const int next = c + 1 < chunks ? c + 1 : chunks - 1;
-            if (k % 2 == 0) {
-                fetch(slot, next, vnext, pnext);
-                accumulate(c, vcur, pcur);
-            } else {
-                fetch(slot, next, vcur, pcur);
-                accumulate(c, vnext, pnext);
-            }
-            if (c + 1 >= chunks) {
-                done = true;
-                break;
-            }
-        }
-    }
-    const int head = kvh * kG + g;
-    const int dim = slice * kSliceDims + dl;
-    float y = acc;
-    if constexpr (!kExact) y = acc * inverse_lds[g];
-    a.output[(static_cast<size_t>(row) * a.query_heads + head) * kDim + dim] = f2bf(y);
+    int base = 0;
+    for (; base + kRing * 8 <= length; base += kRing * 8) round(base, kRing * 8);
+    if (base < length) round(base, length - base);
+    const float y = kExact ? acc : acc * inverse;
+    a.output[(static_cast<size_t>(row) * a.query_heads + head) * kDim + half * 64 + lane] = f2bf(y);
 }
 
 // ---------------------------------------------------------------------------
@@ -506,11 +485,11 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     }
     const int g = tid / kDim;
     const int d = tid % kDim;
-    const bf16_t* vcol = row_values(a, row) + static_cast<size_t>(kvh) * kDim + d;
+    const bf16_t* vcol = value_run(a, row, kvh, d);
     float vpre[kPrefetch];
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
-        vpre[p] = p < cached ? bf2f(vcol[static_cast<size_t>(p) * kv_width]) : 0.0f;
+        vpre[p] = p < cached ? bf2f(vcol[p]) : 0.0f;
     }
 
     // 2. head norms, RoPE, KV append
@@ -529,12 +508,9 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
             const bf16_t v1 = vraw[lane + 64];
             bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
                            static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
-            bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
-                           static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
             kdst[lane] = k0;
             kdst[lane + 64] = k1;
-            vdst[lane] = v0;
-            vdst[lane + 64] = v1;
+            append_value(a, row, kvh, position, lane, v0, v1);
             reinterpret_cast<bf16_t*>(knew_lds)[lane] = k0;
             reinterpret_cast<bf16_t*>(knew_lds)[lane + 64] = k1;
             vnew_lds[lane] = v0;
@@ -600,7 +576,7 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     for (int p = 0; p < kPrefetch; ++p) {
         if (p < cached) acc = fmaf(prob[g][p], vpre[p], acc);
     }
-    for (int p = kPrefetch; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[static_cast<size_t>(p) * kv_width]), acc);
+    for (int p = kPrefetch; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[p]), acc);
     if (fused) acc = fmaf(prob[g][position], bf2f(vnew_lds[d]), acc);
     const int head = kvh * kG + g;
     float y = acc;
@@ -634,12 +610,14 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
     const bf16_t* kraw = raw + static_cast<size_t>(a.query_heads + kvh) * kDim;
     const bf16_t* vraw = raw + static_cast<size_t>(a.query_heads) * kDim + kv_width + static_cast<size_t>(kvh) * kDim;
     const bf16_t* keys = row_keys(a, row) + static_cast<size_t>(kvh) * kDim;
-    const bf16_t* values = row_values(a, row) + static_cast<size_t>(kvh) * kDim;
+    const bf16_t* vrun0 = value_run(a, row, kvh, lane);
+    const bf16_t* vrun1 = value_run(a, row, kvh, lane + 64);
 
-    // 1. every operand, with 16-byte loads (lane l: chunk l % 16 of row
-    //    4i + l / 16), staged through LDS into the lane-l / lane-(l+64)
-    //    layout; only the selections below depend on the position
-    __shared__ uint4 rows_lds[3][kShortCapacity][kDim / 8];  // rope, keys, values
+    // 1. every operand, with 16-byte loads: the query/key rows (lane l:
+    //    chunk l % 16 of row 4i + l / 16) staged through LDS into the
+    //    lane-l / lane-(l+64) layout; the values straight from the lane's two
+    //    dimension runs.  Only the selections below depend on the position.
+    __shared__ uint4 rows_lds[2][kShortCapacity][kDim / 8];  // rope, keys
     __shared__ uint4 head_lds[5][kDim / 8];                  // q, k, v, q gain, k gain
     const int position = a.positions[row];
     const int chunk = lane & 15;
@@ -650,14 +628,21 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
         hv0 = load_global16(src + chunk * 8);
         if (lane < 16) hv1 = load_global16(a.k_norm + chunk * 8);
     }
-    uint4 rv[4], kv4[4], vv4[4];
+    uint4 rv[4], kv4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int p = 4 * i + (lane >> 4);
         const int pc = p < a.capacity ? p : a.capacity - 1;  // rows past the capacity: a valid row, unused
         rv[i] = load_global16(a.rope_table + static_cast<size_t>(pc) * kDim + chunk * 8);
         kv4[i] = load_global16(keys + static_cast<size_t>(pc) * kv_width + chunk * 8);
-        vv4[i] = load_global16(values + static_cast<size_t>(pc) * kv_width + chunk * 8);
+    }
+    // value runs: groups of 8 positions inside the (8-aligned) stride
+    uint4 vg0[kShortCapacity / 8], vg1[kShortCapacity / 8];
+#pragma unroll
+    for (int i = 0; i < kShortCapacity / 8; ++i) {
+        const bool in = i * 8 < a.capacity;
+        vg0[i] = in ? load_global16(vrun0 + i * 8) : make_uint4(0, 0, 0, 0);
+        vg1[i] = in ? load_global16(vrun1 + i * 8) : make_uint4(0, 0, 0, 0);
     }
     head_lds[lane >> 4][chunk] = hv0;
     if (lane < 16) head_lds[4][chunk] = hv1;
@@ -666,7 +651,6 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
         const int p = 4 * i + (lane >> 4);
         rows_lds[0][p][chunk] = rv[i];
         rows_lds[1][p][chunk] = kv4[i];
-        rows_lds[2][p][chunk] = vv4[i];
     }
     // one wave: its LDS writes precede its reads
     const bf16_t* hl = reinterpret_cast<const bf16_t*>(head_lds);
@@ -686,10 +670,16 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
     q_in.s = k_in.s = bf2f(rl[2 * lane + 1]);
     float v0[kShortCapacity], v1[kShortCapacity];
 #pragma unroll
-    for (int p = 0; p < kShortCapacity; ++p) {
-        const bf16_t* vl = reinterpret_cast<const bf16_t*>(rows_lds[2][p]);
-        v0[p] = bf2f(vl[lane]);
-        v1[p] = bf2f(vl[lane + 64]);
+    for (int i = 0; i < kShortCapacity / 8; ++i) {
+        const uint32_t w0[4] = {vg0[i].x, vg0[i].y, vg0[i].z, vg0[i].w};
+        const uint32_t w1[4] = {vg1[i].x, vg1[i].y, vg1[i].z, vg1[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v0[8 * i + 2 * j] = lo_bf(w0[j]);
+            v0[8 * i + 2 * j + 1] = hi_bf(w0[j]);
+            v1[8 * i + 2 * j] = lo_bf(w1[j]);
+            v1[8 * i + 2 * j + 1] = hi_bf(w1[j]);
+        }
     }
 
     // 2. head norm + RoPE of the query head and the new key; the append
@@ -699,12 +689,9 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
     if (head % kG == 0) {
         bf16_t* kdst = (a.key_bases != nullptr ? a.key_bases[row] : const_cast<bf16_t*>(a.key_cache)) +
                        static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
-        bf16_t* vdst = (a.value_bases != nullptr ? a.value_bases[row] : const_cast<bf16_t*>(a.value_cache)) +
-                       static_cast<size_t>(position) * kv_width + static_cast<size_t>(kvh) * kDim;
         kdst[lane] = kn0;
         kdst[lane + 64] = kn1;
-        vdst[lane] = f2bf(v_new0);
-        vdst[lane + 64] = f2bf(v_new1);
+        append_value(a, row, kvh, position, lane, f2bf(v_new0), f2bf(v_new1));
     }
     // the current position's key and value come from qkv, not the cache
     bf16_t* q_l = reinterpret_cast<bf16_t*>(head_lds[0]);
@@ -820,10 +807,9 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
 
 template <bool kExact, int kG>
 hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
-    const size_t head_lds = static_cast<size_t>(kG) * lds_stride(a.capacity) * sizeof(float);
-    // LDS: up to 160 KB per workgroup on gfx950 (the value ring's 2 KB
-    // static slots included).
-    constexpr size_t kLdsLimit = 160 * 1024 - 2048 - 64;
+    const size_t head_lds = static_cast<size_t>(lds_stride(a.capacity)) * sizeof(float);
+    // LDS: up to 160 KB per workgroup on gfx950
+    constexpr size_t kLdsLimit = 160 * 1024;
     if (head_lds > kLdsLimit) return hipErrorInvalidValue;
     static bool configured = false;
     if (!configured) {
@@ -843,12 +829,14 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
     }
     const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.key_value_heads, rows);
     attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
-    attention_head_kernel<kExact, kG><<<dim3(a.key_value_heads * 2 * kG, rows), 64, head_lds, stream>>>(a);
+    attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
 
+
+int value_cache_stride(int capacity) { return (capacity + 7) / 8 * 8; }
 
 size_t attention_workspace_bytes(int rows, int query_heads, int capacity) {
     return static_cast<size_t>(rows) * query_heads * (static_cast<size_t>(capacity) + 1) * sizeof(float);
@@ -873,7 +861,8 @@ bool valid_shape(int rows, int query_heads, int key_value_heads, int head_dimens
 
 AttnArgs base_args(const bf16_t* query, int query_stride, bf16_t* const* key_bases, bf16_t* const* value_bases,
                    const bf16_t* key_cache, const bf16_t* value_cache, const int* positions, int fixed_length,
-                   bf16_t* output, int rows, int query_heads, int key_value_heads, int capacity, float* workspace) {
+                   bf16_t* output, int rows, int query_heads, int key_value_heads, int capacity, float* workspace,
+                   const int* value_strides) {
     AttnArgs a{};
     a.query = query;
     a.query_stride = query_stride;
@@ -890,6 +879,8 @@ AttnArgs base_args(const bf16_t* query, int query_stride, bf16_t* const* key_bas
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
     a.scores = workspace;
     a.inverse = workspace + static_cast<size_t>(rows) * query_heads * capacity;
+    a.value_stride = value_cache_stride(capacity);
+    a.value_strides = value_strides;
     return a;
 }
 
@@ -899,7 +890,7 @@ hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride, b
                             bf16_t* const* value_bases, const bf16_t* key_cache, const bf16_t* value_cache,
                             const int* positions, int fixed_sequence_length, bf16_t* output, int rows,
                             int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,
-                            float* workspace, hipStream_t stream) {
+                            float* workspace, const int* value_strides, hipStream_t stream) {
     if (!valid_shape(rows, query_heads, key_value_heads, head_dimension, max_sequence_length, workspace) ||
         query == nullptr || output == nullptr) {
         return hipErrorInvalidValue;
@@ -911,7 +902,7 @@ hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride, b
     }
     const AttnArgs a = base_args(query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
                                  fixed_sequence_length, output, rows, query_heads, key_value_heads,
-                                 max_sequence_length, workspace);
+                                 max_sequence_length, workspace, value_strides);
     return dispatch(exact, a, rows, stream);
 }
 
@@ -920,7 +911,7 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
                                    bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
                                    const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
                                    int query_heads, int key_value_heads, int head_dimension, int capacity,
-                                   float* workspace, hipStream_t stream) {
+                                   float* workspace, const int* value_strides, hipStream_t stream) {
     if (!valid_shape(rows, query_heads, key_value_heads, head_dimension, capacity, workspace) || qkv == nullptr ||
         output == nullptr || q_norm == nullptr || k_norm == nullptr || rope_table == nullptr ||
         positions == nullptr) {
@@ -929,7 +920,7 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
     if ((key_bases == nullptr) != (value_bases == nullptr)) return hipErrorInvalidValue;
     if (key_bases == nullptr && (key_cache == nullptr || value_cache == nullptr)) return hipErrorInvalidValue;
     AttnArgs a = base_args(qkv, qkv_stride, key_bases, value_bases, key_cache, value_cache, positions, 0, output,
-                           rows, query_heads, key_value_heads, capacity, workspace);
+                           rows, query_heads, key_value_heads, capacity, workspace, value_strides);
     a.q_norm = q_norm;
     a.k_norm = k_norm;
     a.rope_table = rope_table;

@@ -5,6 +5,7 @@
 // are bit-identical to the CPU restatement; the layouts and launch shapes are
 // this build's own (wave64 reductions, one wave per head, device-resident
 // positions so a frame can be replayed as a hipGraph).
+#include <algorithm>
 #include "q3_common.hpp"
 #include "q3_math.h"
 #include "head_device.hpp"
@@ -37,6 +38,51 @@ __global__ __launch_bounds__(64) void rms_norm_rows_kernel(const bf16_t* input, 
     for (int i = lane; i < width; i += 64) {
         const float normalized = round_bf(bf2f(in[i]) * inverse);
         out[i] = f2bf(normalized * bf2f(weight[i]));
+    }
+}
+
+// The same for rows whose width is a multiple of 8 up to kNormMaxWidth: 256
+// threads, the row staged into LDS with 16-byte loads, thread t's partial
+// over x[t], x[t+256], ... in that order, the 256 partials folded in the
+// block_sum tree order, then each thread normalizes 8-element chunks.
+constexpr int kNormMaxWidth = 8192;
+
+__global__ __launch_bounds__(kThreads) void rms_norm_rows_vec_kernel(const bf16_t* input, const bf16_t* weight,
+                                                                     bf16_t* output, int width, float epsilon) {
+    __shared__ uint4 x_lds[kNormMaxWidth / 8];
+    __shared__ float partial_lds[kThreads];
+    const uint4* in = reinterpret_cast<const uint4*>(input + static_cast<size_t>(blockIdx.x) * width);
+    uint4* out = reinterpret_cast<uint4*>(output + static_cast<size_t>(blockIdx.x) * width);
+    const uint4* gain = reinterpret_cast<const uint4*>(weight);
+    const int chunks = width / 8;
+    for (int c = threadIdx.x; c < chunks; c += kThreads) x_lds[c] = in[c];
+    __syncthreads();
+    const bf16_t* xs = reinterpret_cast<const bf16_t*>(x_lds);
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < width; i += kThreads) {
+        const float v = bf2f(xs[i]);
+        s = fmaf(v, v, s);
+    }
+    partial_lds[threadIdx.x] = s;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const float total = wave_tree256(partial_lds[lane], partial_lds[lane + 64], partial_lds[lane + 128],
+                                     partial_lds[lane + 192]);
+    const float inverse = 1.0f / sqrtf(total / static_cast<float>(width) + epsilon);
+    for (int c = threadIdx.x; c < chunks; c += kThreads) {
+        const uint4 xv = x_lds[c];
+        const uint4 gv = gain[c];
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float lo = round_bf(__uint_as_float(xw[i] << 16) * inverse) * __uint_as_float(gw[i] << 16);
+            const float hi = round_bf(__uint_as_float(xw[i] & 0xffff0000u) * inverse) *
+                             __uint_as_float(gw[i] & 0xffff0000u);
+            o[i] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+        }
+        out[c] = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -211,7 +257,14 @@ hipError_t launch_fill_bf16_normal(bf16_t* destination, uint64_t count, uint64_t
 hipError_t launch_rms_norm_rows(const bf16_t* input, const bf16_t* weight, bf16_t* output, int rows,
                                 int width, float epsilon, hipStream_t stream) {
     if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
-    rms_norm_rows_kernel<<<rows, 64, 0, stream>>>(input, weight, output, width, epsilon);
+    const bool vec = width % 8 == 0 && width <= kNormMaxWidth &&
+                     ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(weight) |
+                       reinterpret_cast<uintptr_t>(output)) & 15u) == 0;
+    if (vec) {
+        rms_norm_rows_vec_kernel<<<rows, kThreads, 0, stream>>>(input, weight, output, width, epsilon);
+    } else {
+        rms_norm_rows_kernel<<<rows, 64, 0, stream>>>(input, weight, output, width, epsilon);
+    }
     return hipGetLastError();
 }
 
@@ -253,21 +306,98 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
     return hipGetLastError();
 }
 
-// Stand-alone forms (primitive self-test and op exports): a stream-ordered
-// temporary workspace.
+// Stand-alone forms (primitive self-test and op exports).  Their value caches
+// have the reference's layout, [position][kv_width] per row; the attention
+// kernels read dimension-major values, so each call copies the written
+// positions of every row into a stream-ordered temporary of that form (and,
+// for the decode form, the appended position back).
+
+// temporary[row][c * stride + p] = cache(row)[p * kv_width + c] for
+// p < length(row), 0 beyond; value_table[row] = the row's temporary.
+__global__ __launch_bounds__(256) void values_to_dimension_major_kernel(
+    bf16_t* const* value_bases, const bf16_t* value_cache, const int* positions, int fixed_length, int kv_width,
+    int stride, bf16_t* temporary, bf16_t** value_table) {
+    const int row = blockIdx.y;
+    const size_t per_row = static_cast<size_t>(kv_width) * stride;
+    bf16_t* dst = temporary + row * per_row;
+    if (blockIdx.x == 0 && threadIdx.x == 0) value_table[row] = dst;
+    const bf16_t* src = value_bases != nullptr ? value_bases[row] : value_cache;
+    const int length = positions != nullptr ? positions[row] + 1 : fixed_length;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < per_row;
+         t += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int c = static_cast<int>(t / stride);
+        const int p = static_cast<int>(t % stride);
+        dst[t] = p < length ? src[static_cast<size_t>(p) * kv_width + c] : f2bf(0.0f);
+    }
+}
+
+// cache(row)[positions[row] * kv_width + c] = temporary[row][c * stride + positions[row]]
+__global__ __launch_bounds__(256) void appended_value_back_kernel(bf16_t* const* value_bases, const int* positions,
+                                                                  int kv_width, int stride,
+                                                                  const bf16_t* temporary) {
+    const int row = blockIdx.y;
+    const int position = positions[row];
+    const bf16_t* src = temporary + static_cast<size_t>(row) * kv_width * stride;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < kv_width; c += gridDim.x * blockDim.x) {
+        value_bases[row][static_cast<size_t>(position) * kv_width + c] = src[static_cast<size_t>(c) * stride + position];
+    }
+}
+
+namespace {
+
+struct ValueTemporary {
+    void* memory = nullptr;
+    bf16_t** table = nullptr;
+    bf16_t* values = nullptr;
+    int stride = 0;
+};
+
+hipError_t make_value_temporary(ValueTemporary& t, bf16_t* const* value_bases, const bf16_t* value_cache,
+                                const int* positions, int fixed_length, int rows, int kv_width, int capacity,
+                                hipStream_t stream) {
+    t.stride = value_cache_stride(capacity);
+    const size_t table_bytes = (static_cast<size_t>(rows) * sizeof(bf16_t*) + 255) / 256 * 256;
+    const size_t value_bytes = static_cast<size_t>(rows) * kv_width * t.stride * sizeof(bf16_t);
+    hipError_t st = hipMallocAsync(&t.memory, table_bytes + value_bytes, stream);
+    if (st != hipSuccess) return st;
+    t.table = static_cast<bf16_t**>(t.memory);
+    t.values = reinterpret_cast<bf16_t*>(static_cast<char*>(t.memory) + table_bytes);
+    const size_t per_row = static_cast<size_t>(kv_width) * t.stride;
+    const int blocks = static_cast<int>(std::min<size_t>((per_row + 255) / 256, 1024));
+    values_to_dimension_major_kernel<<<dim3(blocks, rows), 256, 0, stream>>>(
+        value_bases, value_cache, positions, fixed_length, kv_width, t.stride, t.values, t.table);
+    return hipGetLastError();
+}
+
+hipError_t free_value_temporary(ValueTemporary& t, hipStream_t stream, hipError_t st) {
+    if (t.memory == nullptr) return st;
+    const hipError_t freed = hipFreeAsync(t.memory, stream);
+    return st != hipSuccess ? st : freed;
+}
+
+}  // namespace
+
 static hipError_t attention_with_temporary(bool exact, const bf16_t* query, int query_stride,
                                            bf16_t* const* key_bases, bf16_t* const* value_bases,
                                            const bf16_t* key_cache, const bf16_t* value_cache,
                                            const int* positions, int fixed_length, bf16_t* output, int rows,
                                            int query_heads, int key_value_heads, int head_dimension, int capacity,
                                            hipStream_t stream) {
-    if (rows <= 0 || query_heads <= 0 || capacity <= 0) return hipErrorInvalidValue;
+    if (rows <= 0 || query_heads <= 0 || key_value_heads <= 0 || capacity <= 0) return hipErrorInvalidValue;
+    if (value_bases == nullptr && value_cache == nullptr) return hipErrorInvalidValue;
     void* workspace = nullptr;
     hipError_t st = hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, capacity), stream);
     if (st != hipSuccess) return st;
-    st = launch_attention(exact, query, query_stride, key_bases, value_bases, key_cache, value_cache, positions,
-                          fixed_length, output, rows, query_heads, key_value_heads, head_dimension, capacity,
-                          static_cast<float*>(workspace), stream);
+    ValueTemporary values;
+    st = make_value_temporary(values, value_bases, value_cache, positions, fixed_length, rows,
+                              key_value_heads * head_dimension, capacity, stream);
+    if (st == hipSuccess) {
+        st = launch_attention(exact, query, query_stride, key_bases, value_bases != nullptr ? values.table : nullptr,
+                              key_cache, values.values, positions, fixed_length, output, rows, query_heads,
+                              key_value_heads, head_dimension, capacity, static_cast<float*>(workspace), nullptr,
+                              stream);
+    }
+    st = free_value_temporary(values, stream, st);
     const hipError_t freed = hipFreeAsync(workspace, stream);
     return st != hipSuccess ? st : freed;
 }
@@ -311,13 +441,26 @@ hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_str
         value_bases == nullptr) {
         return hipErrorInvalidValue;
     }
+    if (key_value_heads <= 0 || head_dimension != 128 || positions == nullptr) return hipErrorInvalidValue;
     void* workspace = nullptr;
     hipError_t st =
         hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, max_sequence_length), stream);
     if (st != hipSuccess) return st;
-    st = launch_decode_attention(exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases, value_bases,
-                                 nullptr, nullptr, positions, output, rows, query_heads, key_value_heads,
-                                 head_dimension, max_sequence_length, static_cast<float*>(workspace), stream);
+    const int kv_width = key_value_heads * head_dimension;
+    ValueTemporary values;
+    st = make_value_temporary(values, value_bases, nullptr, positions, 0, rows, kv_width, max_sequence_length, stream);
+    if (st == hipSuccess) {
+        st = launch_decode_attention(exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
+                                     values.table, nullptr, nullptr, positions, output, rows, query_heads,
+                                     key_value_heads, head_dimension, max_sequence_length,
+                                     static_cast<float*>(workspace), nullptr, stream);
+    }
+    if (st == hipSuccess) {
+        appended_value_back_kernel<<<dim3((kv_width + 255) / 256, rows), 256, 0, stream>>>(
+            value_bases, positions, kv_width, values.stride, values.values);
+        st = hipGetLastError();
+    }
+    st = free_value_temporary(values, stream, st);
     const hipError_t freed = hipFreeAsync(workspace, stream);
     return st != hipSuccess ? st : freed;
 }

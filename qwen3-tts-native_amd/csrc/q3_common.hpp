@@ -218,12 +218,20 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
 // Decode attention (head dimension 128).  workspace: attention_workspace_bytes
 // of device memory owned by the caller's stream.
 size_t attention_workspace_bytes(int rows, int query_heads, int capacity);
+// Value caches of launch_attention / launch_decode_attention are
+// dimension-major: element (position p, kv head h, dimension d) at
+// [(h * 128 + d) * stride + p].  The stride of a cache of `capacity`
+// positions is value_cache_stride(capacity) unless value_strides (device,
+// one per row) gives it per row (each a multiple of 8, at least the row's
+// own capacity).  Key caches stay [position][kv_width].
+int value_cache_stride(int capacity);
 hipError_t launch_attention(bool exact, const bf16_t* query, int query_stride,
                             bf16_t* const* key_bases, bf16_t* const* value_bases,
                             const bf16_t* key_cache, const bf16_t* value_cache,
                             const int* positions, int fixed_sequence_length, bf16_t* output,
                             int rows, int query_heads, int key_value_heads, int head_dimension,
-                            int max_sequence_length, float* workspace, hipStream_t stream);
+                            int max_sequence_length, float* workspace, const int* value_strides,
+                            hipStream_t stream);
 // Decode attention with the QKV epilogue fused in: qkv holds the raw fused
 // q|k|v rows; query heads are normalized and rotated, the key of position
 // positions[row] is normalized, rotated and appended with its value, then
@@ -233,7 +241,7 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
                                    bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
                                    const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
                                    int query_heads, int key_value_heads, int head_dimension, int capacity,
-                                   float* workspace, hipStream_t stream);
+                                   float* workspace, const int* value_strides, hipStream_t stream);
 hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
                                       const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
                                       bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,

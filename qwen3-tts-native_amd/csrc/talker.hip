@@ -542,9 +542,10 @@ public:
             const Dims& P = cfg_.predictor;
             const size_t b = sizeof(bf16_t);
             talker_k_ = DeviceBuffer(static_cast<size_t>(T.layers) * max_seq_ * T.kv_width() * b);
-            talker_v_ = DeviceBuffer(talker_k_.bytes());
+            // value caches dimension-major: [layer][kv_width][value_cache_stride]
+            talker_v_ = DeviceBuffer(static_cast<size_t>(T.layers) * value_cache_stride(max_seq_) * T.kv_width() * b);
             pred_k_ = DeviceBuffer(static_cast<size_t>(P.layers) * kCodebooks * P.kv_width() * b);
-            pred_v_ = DeviceBuffer(pred_k_.bytes());
+            pred_v_ = DeviceBuffer(static_cast<size_t>(P.layers) * value_cache_stride(kCodebooks) * P.kv_width() * b);
             const int widest = std::max({T.hidden, P.hidden, T.qkv_width(), P.qkv_width(),
                                          T.intermediate, P.intermediate, cfg_.talker_vocab,
                                          cfg_.predictor_vocab});
@@ -567,9 +568,9 @@ public:
             // KV base pointer tables: [talker K | talker V | pred K | pred V]
             std::vector<bf16_t*> bases;
             for (int l = 0; l < T.layers; ++l) bases.push_back(talker_k_.as<bf16_t>() + static_cast<size_t>(l) * max_seq_ * T.kv_width());
-            for (int l = 0; l < T.layers; ++l) bases.push_back(talker_v_.as<bf16_t>() + static_cast<size_t>(l) * max_seq_ * T.kv_width());
+            for (int l = 0; l < T.layers; ++l) bases.push_back(talker_v_.as<bf16_t>() + static_cast<size_t>(l) * value_cache_stride(max_seq_) * T.kv_width());
             for (int l = 0; l < P.layers; ++l) bases.push_back(pred_k_.as<bf16_t>() + static_cast<size_t>(l) * kCodebooks * P.kv_width());
-            for (int l = 0; l < P.layers; ++l) bases.push_back(pred_v_.as<bf16_t>() + static_cast<size_t>(l) * kCodebooks * P.kv_width());
+            for (int l = 0; l < P.layers; ++l) bases.push_back(pred_v_.as<bf16_t>() + static_cast<size_t>(l) * value_cache_stride(kCodebooks) * P.kv_width());
             kv_bases_ = DeviceBuffer(bases.size() * sizeof(bf16_t*));
             check_hip(hipMemcpy(kv_bases_.as<void>(), bases.data(), kv_bases_.bytes(), hipMemcpyHostToDevice), "upload KV bases");
             host_bases_ = bases;
@@ -886,7 +887,7 @@ private:
             check_hip(launch_decode_attention(true, qkv_.as<bf16_t>(), d.qkv_width(), L.q_norm, L.k_norm,
                                               m_.rope_table_.as<bf16_t>(), cfg_.eps, nullptr, nullptr, kc, vc, position,
                                               attn_.as<bf16_t>(), 1, d.query_heads, d.key_value_heads,
-                                              d.head_dimension, cache_rows, attn_scratch_.as<float>(), stream_),
+                                              d.head_dimension, cache_rows, attn_scratch_.as<float>(), nullptr, stream_),
                       "q/k norm + RoPE + KV append + attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddRounded).to(hidden).run(stream_, "O GEMV");
             Gemv(L.gate_up, hidden, d.hidden, d.intermediate, kEpiSiluRounded).norm(L.post_norm, cfg_.eps).to(act_.as<bf16_t>()).run(stream_, "gate/up GEMV");
@@ -1114,7 +1115,7 @@ public:
         act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
         logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
         layers_ = T.layers + P.layers;
-        table_bytes_ = off_trail_values() + R * sizeof(int);
+        table_bytes_ = off_strides() + R * sizeof(int);
         tables_ = DeviceBuffer(table_bytes_);
         check_hip(hipHostMalloc(&pinned_, table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
         std::memset(pinned_, 0, table_bytes_);
@@ -1208,13 +1209,14 @@ private:
     // Table layout (identical in pinned host memory and in device memory):
     // positions int[kSlots][8] | K/V bases ptr[2*layers][8] | token bases ptr[8] |
     // trailing-token ptrs ptr[8] | last_hidden ptrs ptr[8] | position ptrs ptr[8] |
-    // trailing tokens int[8]
+    // trailing tokens int[8] | talker value-cache strides int[8]
     size_t off_kv() const { return kSlots * kCapacity * sizeof(int); }
     size_t off_tokens() const { return off_kv() + 2 * layers_ * kCapacity * sizeof(void*); }
     size_t off_trail_ptrs() const { return off_tokens() + kCapacity * sizeof(void*); }
     size_t off_last() const { return off_trail_ptrs() + kCapacity * sizeof(void*); }
     size_t off_pos_ptrs() const { return off_last() + kCapacity * sizeof(void*); }
     size_t off_trail_values() const { return off_pos_ptrs() + kCapacity * sizeof(void*); }
+    size_t off_strides() const { return off_trail_values() + kCapacity * sizeof(int); }
     template <typename T>
     T* dev_at(size_t offset) const { return reinterpret_cast<T*>(tables_.as<char>() + offset); }
     template <typename T>
@@ -1228,6 +1230,7 @@ private:
     const int* const* trailing_ptrs() const { return dev_at<const int*>(off_trail_ptrs()); }
     bf16_t* const* last_hidden_ptrs() const { return dev_at<bf16_t*>(off_last()); }
     int* const* position_ptrs() const { return dev_at<int*>(off_pos_ptrs()); }
+    const int* value_strides() const { return dev_at<int>(off_strides()); }
 
     void fill_tables(Session** s, int n, const int* trailing) {
         int* pos = host_at<int>(0);
@@ -1252,6 +1255,7 @@ private:
             host_at<bf16_t*>(off_last())[i] = s[i]->last_hidden_.as<bf16_t>();
             host_at<int*>(off_pos_ptrs())[i] = s[i]->position_ptr();
             host_at<int>(off_trail_values())[i] = trailing[i];
+            host_at<int>(off_strides())[i] = value_cache_stride(s[i]->max_seq_);
         }
     }
 
@@ -1305,7 +1309,7 @@ private:
                                               m_.rope_table_.as<bf16_t>(), cfg_.eps, kv_table(slot0 + l, false),
                                               kv_table(slot0 + l, true), nullptr, nullptr, pos, attn_.as<bf16_t>(), n,
                                               d.query_heads, d.key_value_heads, d.head_dimension, capacity,
-                                              attn_scratch_.as<float>(), stream_),
+                                              attn_scratch_.as<float>(), predictor ? nullptr : value_strides(), stream_),
                       "batch q/k norm + RoPE + KV append + attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
                 .run(stream_, "batch O GEMV");

@@ -32,9 +32,10 @@ def make_sessions(hip, model, om, n, sampling, max_seq=64):
     lib = hip.load()
     sessions, oracles, sems = [], [], []
     for i in range(n):
+        seq = max_seq[i] if isinstance(max_seq, (list, tuple)) else max_seq
         s = C.c_void_p()
         mem = hip.SessionMemory()
-        hip.call("qwen3_tts_session_create", model, max_seq, 100 + i, C.byref(s), C.byref(mem))
+        hip.call("qwen3_tts_session_create", model, seq, 100 + i, C.byref(s), C.byref(mem))
         rng = np.random.default_rng(200 + i)
         count = 4 + i
         text = rng.integers(0, TOY["text_vocabulary"], count).astype(np.int32)
@@ -42,7 +43,7 @@ def make_sessions(hip, model, om, n, sampling, max_seq=64):
         pre = hip.PrefillResult()
         hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
                  codec.ctypes.data_as(C.POINTER(C.c_int32)), count, hip.SamplingConfig(*sampling), C.byref(pre))
-        o = toy_model.OracleSession(om, max_seq, 100 + i)
+        o = toy_model.OracleSession(om, seq, 100 + i)
         om.model.batch_semantics = 0
         assert o.prefill(text, codec, sampling) == pre.first_semantic_token
         sessions.append(s)
@@ -96,6 +97,32 @@ def test_batched_frames_exact_mode_match_oracle(hip, orc, toy, monkeypatch, n, m
             st = hip.TalkerStateInfo()
             hip.call("qwen3_tts_session_state_info", s, C.byref(st))
             assert st.talker_position == 4 + i + st.frames_generated
+    finally:
+        om.model.batch_semantics = 0
+        for s in sessions:
+            lib.qwen3_tts_session_destroy(s)
+
+
+def test_batched_sessions_of_different_capacities(hip, orc, toy, monkeypatch):
+    """Sessions with different max_sequence_length (value caches of different
+    strides, 77 rounded up to 80) batched together."""
+    monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
+    model, om = toy
+    seqs = [64, 77, 200]
+    sessions, oracles, sems, lib = make_sessions(hip, model, om, 3, GREEDY, max_seq=seqs)
+    try:
+        for f in range(3):
+            live = [i for i in range(3) if sems[i] != TOY["codec_eos_token"]]
+            if not live:
+                break
+            trailing = [3 * f + i for i in live]
+            res = batch_frame(hip, model, [sessions[i] for i in live], trailing, GREEDY, GREEDY)
+            om.model.batch_semantics = 1
+            for k, i in enumerate(live):
+                ocodes, onxt = oracles[i].frame(sems[i], trailing[k], GREEDY, GREEDY)
+                assert np.array_equal(res[k][0], ocodes), (f, i)
+                assert res[k][1] == onxt
+                sems[i] = onxt
     finally:
         om.model.batch_semantics = 0
         for s in sessions:

@@ -35,7 +35,7 @@ def ptr_array(hip, pointers):
     return dev(hip, np.array(pointers, dtype=np.uint64))
 
 
-@pytest.mark.parametrize("rows,width", [(1, 2048), (3, 1024), (1, 128), (2, 300)])
+@pytest.mark.parametrize("rows,width", [(1, 2048), (3, 1024), (1, 128), (2, 300), (2, 6144), (1, 8192), (1, 8200)])
 def test_rms_norm_rows(hip, orc, rows, width):
     rng = np.random.default_rng(width + rows)
     x, g = gen.activations(rng, rows, width), gen.gains(rng, width)
