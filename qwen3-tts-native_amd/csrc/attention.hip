@@ -298,6 +298,44 @@ __device__ __forceinline__ float chain8(float acc, const uint4& w, float q, int 
     return acc;
 }
 
+// The exact chain with bf16 probabilities: acc = p * v + acc for each of the
+// 8 positions of a group as a bf16 dot2 whose other product is 0 * (the
+// neighbouring value).  A product of two bf16 values is exact in fp32, so
+// the dot2 rounds once, like the fma (values past `live` are masked to 0).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <int kJ0>
+__device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, uint32_t q, int live) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint32_t word = words[e >> 1];
+        const int first = e & ~1;  // the pair's even position
+        word = first + 1 < live ? word : (first < live ? (word & 0xffffu) : 0u);
+        float p;
+        switch (kJ0 + e) {  // compile-time lane of the broadcast
+            case 0: p = row_broadcast<0>(__uint_as_float(q)); break;
+            case 1: p = row_broadcast<1>(__uint_as_float(q)); break;
+            case 2: p = row_broadcast<2>(__uint_as_float(q)); break;
+            case 3: p = row_broadcast<3>(__uint_as_float(q)); break;
+            case 4: p = row_broadcast<4>(__uint_as_float(q)); break;
+            case 5: p = row_broadcast<5>(__uint_as_float(q)); break;
+            case 6: p = row_broadcast<6>(__uint_as_float(q)); break;
+            case 7: p = row_broadcast<7>(__uint_as_float(q)); break;
+            case 8: p = row_broadcast<8>(__uint_as_float(q)); break;
+            case 9: p = row_broadcast<9>(__uint_as_float(q)); break;
+            case 10: p = row_broadcast<10>(__uint_as_float(q)); break;
+            case 11: p = row_broadcast<11>(__uint_as_float(q)); break;
+            case 12: p = row_broadcast<12>(__uint_as_float(q)); break;
+            case 13: p = row_broadcast<13>(__uint_as_float(q)); break;
+            case 14: p = row_broadcast<14>(__uint_as_float(q)); break;
+            default: p = row_broadcast<15>(__uint_as_float(q)); break;
+        }
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, __float_as_uint(p)),
+                                              __builtin_bit_cast(bf16x2_t, word), acc, false);
+    }
+    return acc;
+}
+
 template <bool kExact, int kG>
 __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float p_lds[];  // scores, then exponentials, then probabilities
@@ -369,8 +407,7 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
                 denominator += v[u].w;
             }
         }
-        const float inv = 1.0f / denominator;
-        for (int p = lane; p < padded; p += 64) p_lds[p] = p < length ? round_bf(p_lds[p] * inv) : 0.0f;
+        inverse = 1.0f / denominator;  // the chain rounds bf16(e * inverse) per position
     } else {
         // 256 strided partials: lane l holds those of threads l, l+64,
         // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
@@ -409,13 +446,22 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < kRing; k += 2) {
             const int i = base / 8 + k;  // groups i and i+1: positions 8i .. 8i+15
-            const float q = pq[8 * i];
+            const float e = pq[8 * i];
             const uint4 w0 = ring[k];
             const uint4 w1 = ring[k + 1];
             ring[k] = load(i + kRing);
             ring[k + 1] = load(i + 1 + kRing);
-            acc = chain8<0>(acc, w0, q, live - 8 * k);
-            acc = chain8<8>(acc, w1, q, live - 8 * k - 8);
+            if constexpr (kExact) {
+                // the probability bf16(e * inverse) as one half of a bf16
+                // pair (the half of the position's parity, the other 0)
+                const uint32_t bits = __float_as_uint(round_bf(e * inverse));
+                const uint32_t q = (lane & 1) ? (bits & 0xffff0000u) : (bits >> 16);
+                acc = chain8_pairs<0>(acc, w0, q, live - 8 * k);
+                acc = chain8_pairs<8>(acc, w1, q, live - 8 * k - 8);
+            } else {
+                acc = chain8<0>(acc, w0, e, live - 8 * k);
+                acc = chain8<8>(acc, w1, e, live - 8 * k - 8);
+            }
         }
     };
     int base = 0;
