@@ -65,10 +65,12 @@ struct AttnArgs {
     const bf16_t* k_norm;
     const bf16_t* rope_table;  // [positions][64][cos, sin] bf16
     float epsilon;
-    // Value caches are dimension-major: element (position p, kv head h,
-    // dimension d) at [(h * 128 + d) * stride + p], so one (head, dimension)
-    // holds its positions contiguously.  stride >= capacity, a multiple of 8;
-    // per row from value_strides when that is set.
+    // Value caches are blocked dimension-major: element (position p, kv head
+    // h, dimension d) at [((h * stride / 8 + p / 8) * 128 + d) * 8 + p % 8]:
+    // 16-byte groups of 8 positions of one (head, dimension), the 128
+    // dimensions of a head side by side for each 8 positions (so a wave's
+    // 64 dimensions read 1 KB in one piece).  stride >= capacity, a multiple
+    // of 8; per row from value_strides when that is set.
     int value_stride;
     const int* value_strides;
 };
@@ -89,18 +91,24 @@ __device__ __forceinline__ int row_value_stride(const AttnArgs& a, int row) {
     return a.value_strides != nullptr ? a.value_strides[row] : a.value_stride;
 }
 
-// Start of the positions of (kv head kvh, dimension d) in row's value cache.
+// Elements between consecutive 8-position groups of one (head, dimension).
+constexpr int kGroupStep = kDim * 8;
+
+// Group 0 (positions 0..7) of (kv head kvh, dimension d) in row's value
+// cache; group g is kGroupStep * g elements further.
 __device__ __forceinline__ bf16_t* value_run(const AttnArgs& a, int row, int kvh, int d) {
     return const_cast<bf16_t*>(row_values(a, row)) +
-           static_cast<size_t>(kvh * kDim + d) * static_cast<size_t>(row_value_stride(a, row));
+           (static_cast<size_t>(kvh) * (row_value_stride(a, row) / 8) * kDim + d) * 8;
 }
 
+__device__ __forceinline__ int value_offset(int position) { return (position >> 3) * kGroupStep + (position & 7); }
+
 // Value of the current position, dimensions lane and lane + 64 of kv head
-// kvh, into the dimension-major cache.
+// kvh, into the blocked cache.
 __device__ __forceinline__ void append_value(const AttnArgs& a, int row, int kvh, int position, int lane, bf16_t v0,
                                              bf16_t v1) {
-    value_run(a, row, kvh, lane)[position] = v0;
-    value_run(a, row, kvh, lane + 64)[position] = v1;
+    value_run(a, row, kvh, lane)[value_offset(position)] = v0;
+    value_run(a, row, kvh, lane + 64)[value_offset(position)] = v1;
 }
 
 // Cache rows are reached through pointer tables, which the compiler cannot
@@ -247,7 +255,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // ---------------------------------------------------------------------------
 // softmax + values: grid (query heads * 2, rows), one wave per (row, query
 // head, half of the head dimension); lane = dimension.
-//   1. the lane's value run (dimension-major cache) is requested first,
+//   1. the lane's value run (blocked dimension-major cache) is requested first,
 //      8 positions per 16-byte load, kRing loads ahead;
 //   2. the head's scores into LDS, the maximum;
 //   3. exponentials and the normalizer (exact: the sequential sum of one
@@ -349,7 +357,7 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     // 1. value ring
     const bf16_t* vrun = value_run(a, row, kvh, half * 64 + lane);
     const int last_group = row_value_stride(a, row) / 8 - 1;
-    auto load = [&](int i) { return load_global16(vrun + 8 * (i < last_group ? i : last_group)); };
+    auto load = [&](int i) { return load_global16(vrun + kGroupStep * (i < last_group ? i : last_group)); };
     uint4 ring[kRing];
 #pragma unroll
     for (int k = 0; k < kRing; ++k) ring[k] = load(k);
@@ -449,8 +457,6 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
             const float e = pq[8 * i];
             const uint4 w0 = ring[k];
             const uint4 w1 = ring[k + 1];
-            ring[k] = load(i + kRing);
-            ring[k + 1] = load(i + 1 + kRing);
             if constexpr (kExact) {
                 // the probability bf16(e * inverse) as one half of a bf16
                 // pair (the half of the position's parity, the other 0)
@@ -462,6 +468,9 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
                 acc = chain8<0>(acc, w0, e, live - 8 * k);
                 acc = chain8<8>(acc, w1, e, live - 8 * k - 8);
             }
+            // refilled after use, so each slot keeps its registers
+            ring[k] = load(i + kRing);
+            ring[k + 1] = load(i + 1 + kRing);
         }
     };
     int base = 0;
@@ -535,7 +544,7 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     float vpre[kPrefetch];
 #pragma unroll
     for (int p = 0; p < kPrefetch; ++p) {
-        vpre[p] = p < cached ? bf2f(vcol[p]) : 0.0f;
+        vpre[p] = p < cached ? bf2f(vcol[value_offset(p)]) : 0.0f;
     }
 
     // 2. head norms, RoPE, KV append
@@ -622,7 +631,7 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
     for (int p = 0; p < kPrefetch; ++p) {
         if (p < cached) acc = fmaf(prob[g][p], vpre[p], acc);
     }
-    for (int p = kPrefetch; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[p]), acc);
+    for (int p = kPrefetch; p < cached; ++p) acc = fmaf(prob[g][p], bf2f(vcol[value_offset(p)]), acc);
     if (fused) acc = fmaf(prob[g][position], bf2f(vnew_lds[d]), acc);
     const int head = kvh * kG + g;
     float y = acc;
@@ -687,8 +696,8 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kShortCapacity / 8; ++i) {
         const bool in = i * 8 < a.capacity;
-        vg0[i] = in ? load_global16(vrun0 + i * 8) : make_uint4(0, 0, 0, 0);
-        vg1[i] = in ? load_global16(vrun1 + i * 8) : make_uint4(0, 0, 0, 0);
+        vg0[i] = in ? load_global16(vrun0 + i * kGroupStep) : make_uint4(0, 0, 0, 0);
+        vg1[i] = in ? load_global16(vrun1 + i * kGroupStep) : make_uint4(0, 0, 0, 0);
     }
     head_lds[lane >> 4][chunk] = hv0;
     if (lane < 16) head_lds[4][chunk] = hv1;

@@ -308,12 +308,18 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
 
 // Stand-alone forms (primitive self-test and op exports).  Their value caches
 // have the reference's layout, [position][kv_width] per row; the attention
-// kernels read dimension-major values, so each call copies the written
+// kernels read blocked dimension-major values, so each call copies the written
 // positions of every row into a stream-ordered temporary of that form (and,
 // for the decode form, the appended position back).
 
-// temporary[row][c * stride + p] = cache(row)[p * kv_width + c] for
-// p < length(row), 0 beyond; value_table[row] = the row's temporary.
+// Blocked dimension-major index of element (position p, column c = kv head
+// * 128 + dimension) in a row's value cache of the given stride.
+__device__ __forceinline__ size_t blocked_value_index(int c, int p, int stride) {
+    return ((static_cast<size_t>(c >> 7) * (stride >> 3) + (p >> 3)) * 128 + (c & 127)) * 8 + (p & 7);
+}
+
+// temporary[row] = cache(row) in the blocked layout for p < length(row), 0
+// beyond; value_table[row] = the row's temporary.
 __global__ __launch_bounds__(256) void values_to_dimension_major_kernel(
     bf16_t* const* value_bases, const bf16_t* value_cache, const int* positions, int fixed_length, int kv_width,
     int stride, bf16_t* temporary, bf16_t** value_table) {
@@ -325,13 +331,14 @@ __global__ __launch_bounds__(256) void values_to_dimension_major_kernel(
     const int length = positions != nullptr ? positions[row] + 1 : fixed_length;
     for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < per_row;
          t += static_cast<size_t>(gridDim.x) * blockDim.x) {
-        const int c = static_cast<int>(t / stride);
-        const int p = static_cast<int>(t % stride);
-        dst[t] = p < length ? src[static_cast<size_t>(p) * kv_width + c] : f2bf(0.0f);
+        const int c = static_cast<int>(t % kv_width);
+        const int p = static_cast<int>(t / kv_width);
+        dst[blocked_value_index(c, p, stride)] = p < length ? src[static_cast<size_t>(p) * kv_width + c] : f2bf(0.0f);
     }
 }
 
-// cache(row)[positions[row] * kv_width + c] = temporary[row][c * stride + positions[row]]
+// cache(row)[positions[row] * kv_width + c] = the temporary's element at
+// (positions[row], c)
 __global__ __launch_bounds__(256) void appended_value_back_kernel(bf16_t* const* value_bases, const int* positions,
                                                                   int kv_width, int stride,
                                                                   const bf16_t* temporary) {
@@ -339,7 +346,7 @@ __global__ __launch_bounds__(256) void appended_value_back_kernel(bf16_t* const*
     const int position = positions[row];
     const bf16_t* src = temporary + static_cast<size_t>(row) * kv_width * stride;
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < kv_width; c += gridDim.x * blockDim.x) {
-        value_bases[row][static_cast<size_t>(position) * kv_width + c] = src[static_cast<size_t>(c) * stride + position];
+        value_bases[row][static_cast<size_t>(position) * kv_width + c] = src[blocked_value_index(c, position, stride)];
     }
 }
 

@@ -218,9 +218,9 @@ hipError_t launch_qk_norm_rope_kv_append(bf16_t* qkv, const bf16_t* q_norm, cons
 // Decode attention (head dimension 128).  workspace: attention_workspace_bytes
 // of device memory owned by the caller's stream.
 size_t attention_workspace_bytes(int rows, int query_heads, int capacity);
-// Value caches of launch_attention / launch_decode_attention are
+// Value caches of launch_attention / launch_decode_attention are blocked
 // dimension-major: element (position p, kv head h, dimension d) at
-// [(h * 128 + d) * stride + p].  The stride of a cache of `capacity`
+// [((h * stride / 8 + p / 8) * 128 + d) * 8 + p % 8].  The stride of a cache of `capacity`
 // positions is value_cache_stride(capacity) unless value_strides (device,
 // one per row) gives it per row (each a multiple of 8, at least the row's
 // own capacity).  Key caches stay [position][kv_width].

@@ -542,7 +542,7 @@ public:
             const Dims& P = cfg_.predictor;
             const size_t b = sizeof(bf16_t);
             talker_k_ = DeviceBuffer(static_cast<size_t>(T.layers) * max_seq_ * T.kv_width() * b);
-            // value caches dimension-major: [layer][kv_width][value_cache_stride]
+            // value caches blocked dimension-major: [layer][kv_heads][stride / 8][128][8]
             talker_v_ = DeviceBuffer(static_cast<size_t>(T.layers) * value_cache_stride(max_seq_) * T.kv_width() * b);
             pred_k_ = DeviceBuffer(static_cast<size_t>(P.layers) * kCodebooks * P.kv_width() * b);
             pred_v_ = DeviceBuffer(static_cast<size_t>(P.layers) * value_cache_stride(kCodebooks) * P.kv_width() * b);
