@@ -171,12 +171,14 @@ __device__ __forceinline__ float exact_score(const float* qg, const uint32_t (&k
 // ---------------------------------------------------------------------------
 template <bool kExact, int kG>
 __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs a) {
+    // one wave per (64 positions, query head, row)
     const int row = blockIdx.z;
-    const int kvh = blockIdx.y;
+    const int head = blockIdx.y;
+    const int kvh = head / kG;
     const int length = row_length(a, row);
     const int p0 = blockIdx.x * kScoreLanes;
     if (p0 >= length) return;
-    __shared__ float q_lds[kG][kDim];
+    __shared__ float q_lds[kDim];
     __shared__ uint32_t knew_lds[kDim / 2];
     const int lane = threadIdx.x;
     const int position = length - 1;
@@ -195,25 +197,31 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
         kw[4 * v + 2] = t.z;
         kw[4 * v + 3] = t.w;
     }
-    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(kvh) * kG * kDim;
+    const bf16_t* q = a.query + static_cast<size_t>(row) * a.query_stride + static_cast<size_t>(head) * kDim;
     const bool fused = a.q_norm != nullptr;
     if (fused) {
         const bf16_t* cs = a.rope_table + static_cast<size_t>(position) * kDim;
-#pragma unroll
-        for (int g = 0; g < kG; ++g) {
-            bf16_t q0, q1;
-            head_detail::norm_rope_head(q + g * kDim, a.q_norm, cs, a.epsilon, q0, q1);
-            q_lds[g][lane] = bf2f(q0);
-            q_lds[g][lane + 64] = bf2f(q1);
-        }
+        bf16_t q0, q1;
+        head_detail::norm_rope_head(q, a.q_norm, cs, a.epsilon, q0, q1);
+        q_lds[lane] = bf2f(q0);
+        q_lds[lane + 64] = bf2f(q1);
         if (position >= p0 && position < p0 + kScoreLanes) {
+            // the current key; the group's first query head appends it (and
+            // the value) to the caches
             bf16_t k0, k1, v0, v1;
-            append_kv(a, row, kvh, position, k0, k1, v0, v1);
+            if (head % kG == 0) {
+                append_kv(a, row, kvh, position, k0, k1, v0, v1);
+            } else {
+                const bf16_t* kraw = a.query + static_cast<size_t>(row) * a.query_stride +
+                                     static_cast<size_t>(a.query_heads + kvh) * kDim;
+                head_detail::norm_rope_head(kraw, a.k_norm, cs, a.epsilon, k0, k1);
+            }
             reinterpret_cast<bf16_t*>(knew_lds)[lane] = k0;
             reinterpret_cast<bf16_t*>(knew_lds)[lane + 64] = k1;
         }
     } else {
-        for (int i = lane; i < kG * kDim; i += kScoreLanes) q_lds[i / kDim][i % kDim] = bf2f(q[i]);
+        q_lds[lane] = bf2f(q[lane]);
+        q_lds[lane + 64] = bf2f(q[lane + 64]);
     }
     __syncthreads();
     if (p >= length) return;
@@ -221,24 +229,19 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
 #pragma unroll
         for (int i = 0; i < 64; ++i) kw[i] = knew_lds[i];
     }
-    float* out = a.scores + (static_cast<size_t>(row) * a.query_heads + static_cast<size_t>(kvh) * kG) * a.capacity + p;
+    float score;
+    if constexpr (kExact) {
+        score = exact_score(q_lds, kw, a.scale);
+    } else {
+        float dot = 0.0f;
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-        const float* qg = q_lds[g];
-        float score;
-        if constexpr (kExact) {
-            score = exact_score(qg, kw, a.scale);
-        } else {
-            float dot = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 64; ++t) {
-                dot = fmaf(qg[2 * t], lo_bf(kw[t]), dot);
-                dot = fmaf(qg[2 * t + 1], hi_bf(kw[t]), dot);
-            }
-            score = dot * a.scale;
+        for (int t = 0; t < 64; ++t) {
+            dot = fmaf(q_lds[2 * t], lo_bf(kw[t]), dot);
+            dot = fmaf(q_lds[2 * t + 1], hi_bf(kw[t]), dot);
         }
-        out[static_cast<size_t>(g) * a.capacity] = score;
+        score = dot * a.scale;
     }
+    a.scores[(static_cast<size_t>(row) * a.query_heads + head) * a.capacity + p] = score;
 }
 
 // Row stride of the probability table in LDS: whole 64-position blocks plus
@@ -882,7 +885,7 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         attention_small_kernel<kExact, kG><<<dim3(a.key_value_heads, rows), kG * kDim, 0, stream>>>(a);
         return hipGetLastError();
     }
-    const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.key_value_heads, rows);
+    const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.query_heads, rows);
     attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
     attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
