@@ -29,6 +29,8 @@
 // The max is order independent, and every exponential is q3_expf of the same
 // operands as the oracle's, so splitting the phases over kernels changes no
 // bit of the result.
+#include <type_traits>
+
 #include "q3_common.hpp"
 #include "q3_math.h"
 #include "head_device.hpp"
@@ -263,48 +265,26 @@ __device__ __forceinline__ float wave_max(float v) {
 //   2. the head's scores into LDS, the maximum;
 //   3. exponentials and the normalizer (exact: the sequential sum of one
 //      thread, overlapped with the exponentials of the next block; fast: the
-//      256-thread strided partials and tree), then the probabilities;
-//   4. the chain over positions: the probability of position 16k + j reaches
-//      every lane by a DPP row broadcast of a register holding positions
-//      16k .. 16k+15 in each row's 16 lanes, the value by a byte permute of the
-//      lane's own load -- three VALU operations per position.
+//      256-thread strided partials and tree), then the probabilities (exact:
+//      bf16, stored as one half of a bf16 pair);
+//   4. the chain over positions: every lane reads the probabilities by LDS
+//      broadcast (four per read) and applies them to its own value loads --
+//      one VALU operation per position when exact (a bf16 dot2 on the packed
+//      value pair), two otherwise (unpack, fma).
 // Positions past the length carry probability 0 up to the end of the last
 // ring round; full rounds run in a loop without side exits, the last partial
 // round masks its values.
 // ---------------------------------------------------------------------------
-template <int kJ>
-__device__ __forceinline__ float row_broadcast(float v) {
-    // row_newbcast:kJ -- every lane reads lane kJ of its own 16-lane row
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + kJ, 0xf, 0xf, true));
-}
 
-template <int kJ0>
-__device__ __forceinline__ float chain8(float acc, const uint4& w, float q, int live) {
+// acc = fmaf(p[e], v[e], acc) for the 8 positions of a group (fp32
+// weights, values unpacked from bf16; values past `live` read 0).
+__device__ __forceinline__ float chain8(float acc, const uint4& w, const float* p, int live) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const float v = e < live ? __uint_as_float((e & 1) ? (words[e >> 1] & 0xffff0000u) : (words[e >> 1] << 16))
                                  : 0.0f;
-        float p;
-        switch (kJ0 + e) {  // compile-time lane of the broadcast
-            case 0: p = row_broadcast<0>(q); break;
-            case 1: p = row_broadcast<1>(q); break;
-            case 2: p = row_broadcast<2>(q); break;
-            case 3: p = row_broadcast<3>(q); break;
-            case 4: p = row_broadcast<4>(q); break;
-            case 5: p = row_broadcast<5>(q); break;
-            case 6: p = row_broadcast<6>(q); break;
-            case 7: p = row_broadcast<7>(q); break;
-            case 8: p = row_broadcast<8>(q); break;
-            case 9: p = row_broadcast<9>(q); break;
-            case 10: p = row_broadcast<10>(q); break;
-            case 11: p = row_broadcast<11>(q); break;
-            case 12: p = row_broadcast<12>(q); break;
-            case 13: p = row_broadcast<13>(q); break;
-            case 14: p = row_broadcast<14>(q); break;
-            default: p = row_broadcast<15>(q); break;
-        }
-        acc = fmaf(p, v, acc);
+        acc = fmaf(p[e], v, acc);
     }
     return acc;
 }
@@ -314,34 +294,14 @@ __device__ __forceinline__ float chain8(float acc, const uint4& w, float q, int 
 // neighbouring value).  A product of two bf16 values is exact in fp32, so
 // the dot2 rounds once, like the fma (values past `live` are masked to 0).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-template <int kJ0>
-__device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, uint32_t q, int live) {
+__device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, const float* p, int live) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         uint32_t word = words[e >> 1];
         const int first = e & ~1;  // the pair's even position
         word = first + 1 < live ? word : (first < live ? (word & 0xffffu) : 0u);
-        float p;
-        switch (kJ0 + e) {  // compile-time lane of the broadcast
-            case 0: p = row_broadcast<0>(__uint_as_float(q)); break;
-            case 1: p = row_broadcast<1>(__uint_as_float(q)); break;
-            case 2: p = row_broadcast<2>(__uint_as_float(q)); break;
-            case 3: p = row_broadcast<3>(__uint_as_float(q)); break;
-            case 4: p = row_broadcast<4>(__uint_as_float(q)); break;
-            case 5: p = row_broadcast<5>(__uint_as_float(q)); break;
-            case 6: p = row_broadcast<6>(__uint_as_float(q)); break;
-            case 7: p = row_broadcast<7>(__uint_as_float(q)); break;
-            case 8: p = row_broadcast<8>(__uint_as_float(q)); break;
-            case 9: p = row_broadcast<9>(__uint_as_float(q)); break;
-            case 10: p = row_broadcast<10>(__uint_as_float(q)); break;
-            case 11: p = row_broadcast<11>(__uint_as_float(q)); break;
-            case 12: p = row_broadcast<12>(__uint_as_float(q)); break;
-            case 13: p = row_broadcast<13>(__uint_as_float(q)); break;
-            case 14: p = row_broadcast<14>(__uint_as_float(q)); break;
-            default: p = row_broadcast<15>(__uint_as_float(q)); break;
-        }
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, __float_as_uint(p)),
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, __float_as_uint(p[e])),
                                               __builtin_bit_cast(bf16x2_t, word), acc, false);
     }
     return acc;
@@ -418,7 +378,24 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
                 denominator += v[u].w;
             }
         }
-        inverse = 1.0f / denominator;  // the chain rounds bf16(e * inverse) per position
+        inverse = 1.0f / denominator;
+        // probabilities bf16(e * inverse), each stored as one half of a bf16
+        // pair (the half of the position's parity, the other 0); reads first,
+        // then the conversions (padded is a multiple of 128)
+        auto convert = [&](int base, auto count) {
+            constexpr int kCount = decltype(count)::value;
+            float t[kCount];
+#pragma unroll
+            for (int u = 0; u < kCount; ++u) t[u] = p_lds[base + u * 64 + lane];
+#pragma unroll
+            for (int u = 0; u < kCount; ++u) {
+                const uint32_t bits = __float_as_uint(round_bf(t[u] * inverse));
+                p_lds[base + u * 64 + lane] = __uint_as_float((lane & 1) ? (bits & 0xffff0000u) : (bits >> 16));
+            }
+        };
+        int base = 0;
+        for (; base + 512 <= padded; base += 512) convert(base, std::integral_constant<int, 8>());
+        for (; base < padded; base += 128) convert(base, std::integral_constant<int, 2>());
     } else {
         // 256 strided partials: lane l holds those of threads l, l+64,
         // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
@@ -451,25 +428,28 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     //    partial round replaces values past the length by 0 (positions
     //    there were never written for this sequence), so each fmaf adds
     //    0 * 0 -- the running sum starts at +0 and never becomes -0.
-    const float* pq = p_lds + (lane & 15);
     float acc = 0.0f;
     auto round = [&](int base, int live) {
 #pragma unroll
         for (int k = 0; k < kRing; k += 2) {
             const int i = base / 8 + k;  // groups i and i+1: positions 8i .. 8i+15
-            const float e = pq[8 * i];
+            float pv[16];  // the 16 positions' probability words, LDS broadcast reads
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 t = reinterpret_cast<const float4*>(p_lds)[2 * i + j];
+                pv[4 * j] = t.x;
+                pv[4 * j + 1] = t.y;
+                pv[4 * j + 2] = t.z;
+                pv[4 * j + 3] = t.w;
+            }
             const uint4 w0 = ring[k];
             const uint4 w1 = ring[k + 1];
             if constexpr (kExact) {
-                // the probability bf16(e * inverse) as one half of a bf16
-                // pair (the half of the position's parity, the other 0)
-                const uint32_t bits = __float_as_uint(round_bf(e * inverse));
-                const uint32_t q = (lane & 1) ? (bits & 0xffff0000u) : (bits >> 16);
-                acc = chain8_pairs<0>(acc, w0, q, live - 8 * k);
-                acc = chain8_pairs<8>(acc, w1, q, live - 8 * k - 8);
+                acc = chain8_pairs(acc, w0, pv, live - 8 * k);
+                acc = chain8_pairs(acc, w1, pv + 8, live - 8 * k - 8);
             } else {
-                acc = chain8<0>(acc, w0, e, live - 8 * k);
-                acc = chain8<8>(acc, w1, e, live - 8 * k - 8);
+                acc = chain8(acc, w0, pv, live - 8 * k);
+                acc = chain8(acc, w1, pv + 8, live - 8 * k - 8);
             }
             // refilled after use, so each slot keeps its registers
             ring[k] = load(i + kRing);
