@@ -332,6 +332,16 @@ def main() -> int:
                      "kernel": "gemv_exact_fixed<4, SiluRounded, norm> (gate+up 12288x2048)",
                      "bytes_per_launch": int(launch_bytes), "us_per_launch": round(launch_us, 3)},
     }
+    # The launch-shape ceiling: the same 112 launches (same weight bytes,
+    # same graph) as plain 16-byte reads with no GEMV arithmetic.
+    ceiling = step_benchmark(hip, args.steps, args.warmup, use_graph=6)
+    ceiling_gbs = main_run.weight_bytes / (ceiling.milliseconds_per_step * 1e-3) / 1e9
+    gemv_weight_gbs = main_run.weight_bytes / (ms * 1e-3) / 1e9
+    line["launch_ceiling"] = {"what": "the step's 112 launches as plain reads of the same weights (one hipGraph)",
+                              "ms_per_step": round(ceiling.milliseconds_per_step, 4),
+                              "weight_gbs": round(ceiling_gbs, 1),
+                              "gemv_weight_gbs": round(gemv_weight_gbs, 1),
+                              "gemv_fraction_of_ceiling": round(gemv_weight_gbs / ceiling_gbs, 4)}
     line["single_gemv_config1"] = single_gemv(hip)
     line["batched_config4"] = batched(hip, max(args.steps // 4, 5), max(args.warmup // 2, 2))
     if not args.no_frames:

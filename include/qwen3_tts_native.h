@@ -453,7 +453,9 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     int32_t warmup;
     int32_t steps;
     int32_t use_graph;     /* 0 eager launches, 1 hipGraph per step, 2 persistent chain kernel, 3 warp-specialized streaming chain kernel,
-                              4 linked launches on two streams (one graph each), 5 linked launches, eager */
+                              4 linked launches on two streams (one graph each), 5 linked launches, eager,
+                              6 the same launches as plain 16-byte reads of the weights in one hipGraph
+                              (the launch-shape ceiling; no GEMV arithmetic, rows must be 1) */
     int32_t kernel_filter; /* 0 whole chain; 1 QKV, 2 O, 3 gate/up, 4 down GEMVs only */
     uint64_t weight_bytes;
     uint64_t algorithmic_bytes_per_step;

@@ -42,6 +42,21 @@ __global__ void fill_scale_kernel(float* out, uint64_t count, uint64_t seed) {
     }
 }
 
+// Plain read of `bytes` (a multiple of 16) with 16-byte nontemporal loads:
+// the launch-shape ceiling of a chain of streaming kernels (no arithmetic
+// beyond an xor, one conditional store).
+typedef int stream_i32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void read_weights_kernel(const int8_t* weights, uint64_t bytes, int* sink) {
+    const stream_i32x4* p = reinterpret_cast<const stream_i32x4*>(weights);
+    const uint64_t n = bytes / 16;
+    stream_i32x4 acc = {0, 0, 0, 0};
+#pragma unroll 4
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += gridDim.x * 256ull) {
+        acc ^= __builtin_nontemporal_load(p + i);
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5eed5eed) sink[0] = 1;
+}
+
 int grid_for(uint64_t n) {
     const uint64_t g = (n + 255) / 256;
     return static_cast<int>(std::min<uint64_t>(g, 65536));
@@ -148,7 +163,8 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                                                             char* error, size_t cap) {
     if (b == nullptr || b->struct_size != sizeof(Qwen3TtsStepBenchmarkV1) || b->layers <= 0 || b->hidden <= 0 ||
         b->intermediate <= 0 || b->query_width <= 0 || b->key_value_width <= 0 || b->rows < 1 || b->rows > 8 ||
-        b->steps <= 0 || b->warmup < 0 || b->kernel_filter < 0 || b->kernel_filter > 4) {
+        b->steps <= 0 || b->warmup < 0 || b->kernel_filter < 0 || b->kernel_filter > 4 || b->use_graph < 0 ||
+        b->use_graph > 6 || (b->use_graph == 6 && b->rows != 1)) {
         write_error(error, cap, "invalid step benchmark arguments");
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
     }
@@ -215,7 +231,15 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         int only_parity = -1;  // >= 0: launch only the kernels of this stream (graph capture)
         bool dry = false;                              // record footprints only
         std::vector<std::pair<int, int>> footprints;  // workgroups, per CU
+        int* read_sink = mem.get<int>(1);
         auto launch = [&](GemvArgs g, const char* what) {
+            if (b->use_graph == 6) {  // the same weight bytes, plain reads
+                const bool pair = g.epilogue == kEpiSiluRounded || g.epilogue == kEpiSiluFused;
+                const uint64_t bytes = static_cast<uint64_t>(g.in_features) * g.out_features * (pair ? 2 : 1);
+                read_weights_kernel<<<1536, 256, 0, stream>>>(g.weight, bytes, read_sink);
+                check_hip(hipGetLastError(), what);
+                return;
+            }
             if (!linked) {
                 check_hip(launch_int8_gemv(g, stream), what);
                 return;
@@ -372,7 +396,7 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             }
             only_parity = -1;
         }
-        if (b->use_graph == 1) {
+        if (b->use_graph == 1 || b->use_graph == 6) {
             check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             enqueue_step();
             hipGraph_t graph = nullptr;
