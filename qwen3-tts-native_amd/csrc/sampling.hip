@@ -28,11 +28,6 @@ __device__ __forceinline__ bool before(float av, int ai, float bv, int bi) {
     return (av > bv) || (av == bv && ai < bi);
 }
 
-// Branch-free form for the rank counting loop (no short-circuit, so no
-// control flow around the LDS reads).
-__device__ __forceinline__ int before_bit(float av, int ai, float bv, int bi) {
-    return static_cast<int>(av > bv) | (static_cast<int>(av == bv) & static_cast<int>(ai < bi));
-}
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v);
@@ -102,6 +97,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     __shared__ double weights[kMaxVocabulary];
     __shared__ float cand_v[kCandidateCap];
     __shared__ int cand_i[kCandidateCap];
+    __shared__ __align__(16) unsigned long long cand_key[kCandidateCap + 2];  // (order key, ~index): larger = earlier
     __shared__ float sorted_v[kMaxVocabulary];
     __shared__ int sorted_i[kMaxVocabulary];
     __shared__ uint32_t hist2[512];
@@ -113,6 +109,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     __shared__ int s_best;
     __shared__ double s_target;
     __shared__ double shares[72];
+    __shared__ double prefix_lds[64], cumulative_lds[64];
 
     const int tid = threadIdx.x;
     const int V = a.vocabulary;
@@ -129,9 +126,9 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         const int t = tid + j * kSampleThreads;
         logit[j] = t < V ? bf2f(a.logits[t]) : 0.0f;
     }
-    for (int t = tid; t < V; t += kSampleThreads) marked[t] = 0;
-    __syncthreads();
     if (penalize) {
+        for (int t = tid; t < V; t += kSampleThreads) marked[t] = 0;
+        __syncthreads();
         for (int h = tid; h < count; h += kSampleThreads) {
             const int token = a.history[h];
             if (token >= 0 && token < V) marked[token] = 1;
@@ -289,25 +286,30 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
                 if (slot < kCandidateCap) {
                     cand_v[slot] = values[t];
                     cand_i[slot] = t;
+                    cand_key[slot] = (static_cast<unsigned long long>(order_key(values[t])) << 32) |
+                                     static_cast<uint32_t>(~t);
                 }
             }
         }
         __syncthreads();
         const int n = s_count;
         if (n <= kCandidateCap) {
-            // Rank counting over the survivors: exact total order.
+            // Rank counting over the survivors: exact total order.  The
+            // packed key compares like (value desc, index asc) (order_key
+            // is monotone, -0 == +0); a 0 pad (below every key) makes the
+            // count even, two keys per LDS read.
+            if (tid == 0) cand_key[n] = 0ull;
+            __syncthreads();
             for (int c = tid; c < n; c += kSampleThreads) {
-                const float v = cand_v[c];
-                const int i = cand_i[c];
+                const unsigned long long mine = cand_key[c];
+                const ulonglong2* pairs = reinterpret_cast<const ulonglong2*>(cand_key);
                 int rank = 0;
-                int j = 0;
-                for (; j + 8 <= n; j += 8) {
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) rank += before_bit(cand_v[j + u], cand_i[j + u], v, i);
+                for (int j = 0; j < (n + 1) / 2; ++j) {
+                    const ulonglong2 k = pairs[j];
+                    rank += static_cast<int>(k.x > mine) + static_cast<int>(k.y > mine);
                 }
-                for (; j < n; ++j) rank += before_bit(cand_v[j], cand_i[j], v, i);
-                sorted_v[rank] = v;
-                sorted_i[rank] = i;
+                sorted_v[rank] = cand_v[c];
+                sorted_i[rank] = cand_i[c];
             }
         } else {
             for (int t = tid; t < V; t += kSampleThreads) {
@@ -320,8 +322,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
         }
         __syncthreads();
         const float maximum = sorted_v[0] / a.temperature;
-        for (int r = tid; r < selections; r += kSampleThreads) {
-            weights[r] = exp(static_cast<double>(sorted_v[r] / a.temperature - maximum));
+        // (entries selections .. 63 are 0 for the wave-0 sums below)
+        const int weight_count = selections <= 64 ? 64 : selections;
+        for (int r = tid; r < weight_count; r += kSampleThreads) {
+            weights[r] = r < selections ? exp(static_cast<double>(sorted_v[r] / a.temperature - maximum)) : 0.0;
         }
         __syncthreads();
         if (selections <= 64) {
@@ -331,33 +335,33 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
             // with cumulative >= x" loop becomes a ballot over the lanes.
             if (tid < 64) {
                 const int lane = tid;
+                // Whole steps of 8; the zero entries past `selections` leave
+                // the non-negative running sums as they are.  Each prefix is
+                // stored once (every lane writes the same value), so a step
+                // is one add.
+                const int steps = (selections + 7) & ~7;
                 double running = 0.0;
-                double prefix_mine = 0.0;
-                for (int r0 = 0; r0 < selections; r0 += 8) {
+                for (int r0 = 0; r0 < steps; r0 += 8) {
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        // unconditional read, selected add: no branch around
-                        // the LDS traffic (entries past `selections` unused)
-                        const int r = r0 + u;
-                        const double w = weights[r];
-                        running = r < selections ? running + w : running;
-                        prefix_mine = lane == r ? running : prefix_mine;
+                        running += weights[r0 + u];
+                        prefix_lds[r0 + u] = running;
                     }
                 }
                 const double denominator = running;
-                if (lane < selections) shares[lane] = weights[lane] / denominator;
+                shares[lane] = lane < selections ? weights[lane] / denominator : 0.0;
                 __builtin_amdgcn_wave_barrier();
                 double share_running = 0.0;
-                double share_mine = 0.0;
-                for (int r0 = 0; r0 < selections; r0 += 8) {
+                for (int r0 = 0; r0 < steps; r0 += 8) {
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        const int r = r0 + u;
-                        const double q = shares[r];
-                        share_running = r < selections ? share_running + q : share_running;
-                        share_mine = lane == r ? share_running : share_mine;
+                        share_running += shares[r0 + u];
+                        cumulative_lds[r0 + u] = share_running;
                     }
                 }
+                __builtin_amdgcn_wave_barrier();
+                const double prefix_mine = prefix_lds[lane];
+                const double share_mine = cumulative_lds[lane];
                 const unsigned long long cut =
                     __ballot(lane < selections && share_mine >= static_cast<double>(a.top_p));
                 const int retained = cut ? __ffsll(static_cast<long long>(cut)) : selections;

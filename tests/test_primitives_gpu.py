@@ -270,19 +270,25 @@ def test_sampler_greedy_matches_oracle(hip, orc, vocab):
             assert got == ref
 
 
-@pytest.mark.parametrize("top_k,top_p", [(50, 1.0), (50, 0.8), (1, 1.0), (0, 1.0), (0, 0.9), (700, 1.0)])
-def test_sampler_topk_matches_oracle(hip, orc, top_k, top_p):
-    """Same logits, same RNG state -> same token and same next state.  (The
-    draw compares double sums; exp in double on the device vs the host may
-    differ in the last ulp, which only matters at an exact boundary.)"""
-    rng = np.random.default_rng(top_k * 10 + int(top_p * 10))
+@pytest.mark.parametrize("top_k,top_p", [(50, 1.0), (50, 0.8), (1, 1.0), (0, 1.0), (0, 0.9), (700, 1.0), (64, 1.0)])
+@pytest.mark.parametrize("vocab,suppress,penalty", [(3072, True, 1.05), (2048, False, 1.0)])
+def test_sampler_topk_matches_oracle(hip, orc, top_k, top_p, vocab, suppress, penalty):
+    """Same logits, same RNG state -> same token and same next state, for the
+    talker's masked, penalized vocabulary and the predictor's plain one;
+    every fourth trial has heavily tied logits.  (The draw compares double
+    sums; exp in double on the device vs the host may differ in the last
+    ulp, which only matters at an exact boundary.)"""
+    rng = np.random.default_rng(top_k * 10 + int(top_p * 10) + vocab)
     state = 0x1234567
     for trial in range(12):
-        logits = gen.bf16(rng.standard_normal(3072).astype(np.float32) * 3)
+        raw = rng.standard_normal(vocab).astype(np.float32) * 3
+        if trial % 4 == 3:
+            raw = np.round(raw)
+        logits = gen.bf16(raw)
         history = list(rng.integers(0, 2048, 30))
-        cfg = hip.sampling(1, top_k, top_p, 0.9, 1.05)
-        got, gstate = sample_gpu(hip, logits, True, history, cfg, state)
-        ref, rstate = orc.sample_logits(logits, True, 2150, history, 1, top_k, top_p, 0.9, 1.05, state)
+        cfg = hip.sampling(1, top_k, top_p, 0.9, penalty)
+        got, gstate = sample_gpu(hip, logits, suppress, history, cfg, state)
+        ref, rstate = orc.sample_logits(logits, suppress, 2150, history, 1, top_k, top_p, 0.9, penalty, state)
         assert (got, gstate) == (ref, rstate), trial
         state = rstate
 
