@@ -248,6 +248,8 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
                     done += 1
                     pred_ms += info.predictor_gpu_milliseconds
                     talk_ms += info.talker_gpu_milliseconds
+            if t_start is None:
+                raise RuntimeError("the session sampled the end token before the timed frames")
             wall = time.perf_counter() - t_start
             frame_ms = wall * 1000.0 / max(done, 1)
             return {
