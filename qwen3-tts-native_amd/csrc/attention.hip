@@ -795,37 +795,22 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
         score = live ? round_bf(round_bf(t8[0]) * a.scale) : -INFINITY;
     }
 
-    // 4. softmax, lane = position; the normalizer in position order
+    // 4. softmax, lane = position; the normalizer in position order.  The 16
+    //    exponentials and then the 16 probabilities reach every lane as
+    //    scalar operands (lane reads); entries past the current position are
+    //    0, and adding them leaves the sequential sum as it is.
     const float maximum = wave_max(score);
     const float e = live ? q3_expf(score - maximum) : 0.0f;
-    // the 16 exponentials (0 past the current position) to every lane
-    // through LDS; adding the trailing zeros leaves the sequential sum as is
-    __shared__ float4 e_lds[kShortCapacity / 4], p_lds[kShortCapacity / 4];
-    if (lane < kShortCapacity) reinterpret_cast<float*>(e_lds)[lane] = e;
-    float ev[kShortCapacity];
-#pragma unroll
-    for (int i = 0; i < kShortCapacity / 4; ++i) {
-        const float4 t = e_lds[i];
-        ev[4 * i] = t.x;
-        ev[4 * i + 1] = t.y;
-        ev[4 * i + 2] = t.z;
-        ev[4 * i + 3] = t.w;
-    }
     float denominator = 0.0f;
 #pragma unroll
-    for (int p = 0; p < kShortCapacity; ++p) denominator += ev[p];
+    for (int p = 0; p < kShortCapacity; ++p) {
+        denominator += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
+    }
     const float inverse = 1.0f / denominator;
     const float prob = live ? round_bf(e * inverse) : 0.0f;
-    if (lane < kShortCapacity) reinterpret_cast<float*>(p_lds)[lane] = prob;
     float pv[kShortCapacity];
 #pragma unroll
-    for (int i = 0; i < kShortCapacity / 4; ++i) {
-        const float4 t = p_lds[i];
-        pv[4 * i] = t.x;
-        pv[4 * i + 1] = t.y;
-        pv[4 * i + 2] = t.z;
-        pv[4 * i + 3] = t.w;
-    }
+    for (int p = 0; p < kShortCapacity; ++p) pv[p] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), p));
 
     // 5. value chains for dimensions lane and lane + 64, positions in order.
     //    Past the current position the value is replaced by 0 (and its

@@ -555,7 +555,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
             const int c = idx % kChunks;
             uint4* p = reinterpret_cast<uint4*>(xs + r * kStride + 8 * c);
             const uint4 g = kOneGain ? gain_chunk : reinterpret_cast<const uint4*>(a.norm_weight)[c];
-            *p = normalize_chunk(*p, g, inverse_lds[r]);
+            *p = normalize_chunk_hw(*p, g, inverse_lds[r]);
         }
         __syncthreads();
     }

@@ -107,6 +107,27 @@ __device__ __forceinline__ uint4 normalize_chunk(const uint4 x, const uint4 g, f
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// normalize_chunk with the hardware float -> bf16 conversion (round to
+// nearest even, as round_bf for every finite value; only a NaN's payload can
+// differ).  Used by the batched MFMA path, whose results follow the
+// reference's batched (non-exact-order) semantics.
+__device__ __forceinline__ uint4 normalize_chunk_hw(const uint4 x, const uint4 g, float inverse) {
+    const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = __builtin_bit_cast(uint16_t, static_cast<__bf16>(__uint_as_float(xw[i] << 16) * inverse)) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(
+                                __uint_as_float(xw[i] & 0xffff0000u) * inverse))) << 16);
+        const float lo = __uint_as_float(a << 16) * __uint_as_float(gw[i] << 16);
+        const float hi = __uint_as_float(a & 0xffff0000u) * __uint_as_float(gw[i] & 0xffff0000u);
+        o[i] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(lo)) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // Load the 16 activations of vector `v` (bf16) as fp32, normalized if needed.
 template <bool kNorm>
 __device__ __forceinline__ void load_x16(const bf16_t* x, const bf16_t* gain, int v,
