@@ -140,20 +140,12 @@ def predictor_chain_entry(ms):
             "effective_gbs": round(PREDICTOR_CHAIN_BYTES / (med * 1e6), 1)}
 
 
-def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, greedy: int = 20):
-    """Config 5 through the reference C ABI: VoiceDesign geometry, synthetic
-    bf16 weights quantized to int8 at finalize, prompt of `prompt` tokens,
-    then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed.  The
-    prompt fills the KV cache so that the timed frames run at context
-    max_seq - frames .. max_seq (attention reads up to 1024 positions).
-    Before the timed frames, `greedy` frames run the code predictor with
-    greedy argmax (config 3: the 15-step predictor chain); its GPU time per
-    frame is reported separately (it covers 16 passes through the 5 layers:
-    the chain's 15 steps plus the pass that seeds it from the talker)."""
+def build_model(hip):
+    """The VoiceDesign-geometry model of config 5 with synthetic bf16 weights
+    (quantized to int8 at finalize), uploaded through the C ABI.  Returns the
+    model handle and the config; the caller destroys the model."""
     import numpy as np
 
-    prompt = max_seq - frames - warm - greedy
-    lib = hip.load()
     cfg = hip.default_config()
     model = C.c_void_p()
     hip.call("qwen3_tts_model_create", 0, C.byref(model))
@@ -206,6 +198,31 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
             hip.call("qwen3_tts_model_upload_tensor", model, name.encode(), buf.ptr, 2 * n, len(shape), shp)
         mem = hip.ModelMemory()
         hip.call("qwen3_tts_model_finalize", model, C.byref(mem))
+    except Exception:
+        hip.load().qwen3_tts_model_destroy(model)
+        raise
+    finally:
+        for b in scratch:
+            b.free()
+    return model, cfg
+
+
+def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, greedy: int = 20):
+    """Config 5 through the reference C ABI: VoiceDesign geometry, synthetic
+    bf16 weights quantized to int8 at finalize, prompt of `prompt` tokens,
+    then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed.  The
+    prompt fills the KV cache so that the timed frames run at context
+    max_seq - frames .. max_seq (attention reads up to 1024 positions).
+    Before the timed frames, `greedy` frames run the code predictor with
+    greedy argmax (config 3: the 15-step predictor chain); its GPU time per
+    frame is reported separately (it covers 16 passes through the 5 layers:
+    the chain's 15 steps plus the pass that seeds it from the talker)."""
+    import numpy as np
+
+    prompt = max_seq - frames - warm - greedy
+    lib = hip.load()
+    model, cfg = build_model(hip)
+    try:
         session = C.c_void_p()
         smem = hip.SessionMemory()
         hip.call("qwen3_tts_session_create", model, max_seq, 42, C.byref(session), C.byref(smem))
@@ -268,8 +285,84 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
             lib.qwen3_tts_session_destroy(session)
     finally:
         lib.qwen3_tts_model_destroy(model)
-        for b in scratch:
-            b.free()
+
+
+def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: int = 1024):
+    """Multi-session serving through the batch entry point
+    (qwen3_tts_model_batch_next_frame_begin_v2, the reference's lockstep
+    batch: batched GEMVs on MFMA, batched attention): max(ns) sessions are
+    prefilled once, then for each N the first N sessions step `warm` untimed
+    and `frames` timed batched frames (talker top-k 50 / T 0.9 / rep 1.05,
+    predictor top-k 50 / T 0.9).  The runs share the sessions, so contexts
+    grow from ~870 to ~1010 positions over the three runs.  A session that
+    samples the end token leaves the batch (counted)."""
+    import numpy as np
+
+    lib = hip.load()
+    model, cfg = build_model(hip)
+    sessions = []
+    try:
+        nmax = max(ns)
+        prompt = max_seq - len(ns) * (frames + warm) - 8
+        rng = np.random.default_rng(7)
+        ts = hip.sampling(1, 50, 1.0, 0.9, 1.05)
+        ps = hip.sampling(1, 50, 1.0, 0.9, 1.0)
+        semantic = []
+        for i in range(nmax):
+            s = C.c_void_p()
+            mem = hip.SessionMemory()
+            hip.call("qwen3_tts_session_create", model, max_seq, 100 + i, C.byref(s), C.byref(mem))
+            sessions.append(s)
+            text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
+            codec = rng.integers(0, 2048, prompt).astype(np.int32)
+            pre = hip.PrefillResult()
+            hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                     codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(pre))
+            semantic.append(pre.first_semantic_token)
+        ended = [semantic[i] == cfg.codec_eos_token for i in range(nmax)]
+        results = {"prompt_tokens": prompt, "frames": frames,
+                   "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9"}
+        for n in ns:
+            timed_frames = 0
+            timed_batches = 0
+            t_total = 0.0
+            for f in range(warm + frames):
+                live = [i for i in range(n) if not ended[i]]
+                if not live:
+                    break
+                k = len(live)
+                arr = (C.c_void_p * k)(*[sessions[i].value for i in live])
+                tr = (C.c_int32 * k)(*[int(x) for x in rng.integers(0, cfg.text_vocabulary, k)])
+                tsa = (hip.SamplingConfig * k)(*[ts] * k)
+                psa = (hip.SamplingConfig * k)(*[ps] * k)
+                views = (hip.DeviceFrameViewV2 * k)()
+                for v in views:
+                    v.struct_size = C.sizeof(hip.DeviceFrameViewV2)
+                t0 = time.perf_counter()
+                hip.call("qwen3_tts_model_batch_next_frame_begin_v2", model, arr, k, tr, tsa, psa, views)
+                for j, i in enumerate(live):
+                    nxt = C.c_uint16()
+                    info = hip.CodecFrameInfo()
+                    hip.call("qwen3_tts_session_next_frame_finish_v2", sessions[i], views[j].lease_id, None,
+                             C.byref(nxt), C.byref(info))
+                    semantic[i] = nxt.value
+                    ended[i] = ended[i] or bool(info.ended_by_eos) or nxt.value == cfg.codec_eos_token
+                dt = time.perf_counter() - t0
+                if f >= warm:
+                    timed_frames += k
+                    timed_batches += 1
+                    t_total += dt
+            ms = 1000.0 * t_total / max(1, timed_batches)
+            results[f"n{n}"] = {"ms_per_batched_frame": round(ms, 3),
+                                "session_frames_per_second": round(timed_frames / max(t_total, 1e-9), 1),
+                                "aggregate_rtf": round(t_total / max(timed_frames, 1) / 0.080, 4),
+                                "session_frames": timed_frames}
+        results["sessions_ended_by_eos"] = int(sum(ended))
+        return results
+    finally:
+        for s in sessions:
+            lib.qwen3_tts_session_destroy(s)
+        lib.qwen3_tts_model_destroy(model)
 
 
 def main() -> int:
@@ -351,6 +444,10 @@ def main() -> int:
             line["frame_step"] = frame_benchmark(hip, frames=args.frames)
         except Exception as e:  # report, never hide
             line["frame_step"] = {"error": str(e)}
+        try:
+            line["batched_frames"] = batched_frames(hip)
+        except Exception as e:  # report, never hide
+            line["batched_frames"] = {"error": str(e)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
