@@ -276,6 +276,35 @@ hipError_t launch_fill_bf16_normal(bf16_t* destination, uint64_t count, uint64_t
                                    float stddev, hipStream_t stream);
 
 // Sampling / frame glue (sampling_kernels.cu equivalents).
+// Arguments of one sampler invocation (sampling.hip documents the fields'
+// semantics; every pointer is a device pointer).
+struct SampleArgs {
+    const bf16_t* logits;
+    int vocabulary;
+    bool suppress;
+    int eos;
+    const int* history;
+    const int* history_count;
+    int history_count_fallback;
+    int do_sample;
+    int top_k;
+    float top_p;
+    float temperature;
+    float penalty;
+    uint64_t* random_state;
+    int* selected;
+    int* store_tokens;
+    const int* store_index;
+    int store_index_fallback;
+    int* append_history;   // history array to append to (talker), nullable
+    int* append_count;     // device history counter to increment, nullable
+};
+// Host check of one row's arguments (the launchers' validation).
+bool sample_args_valid(const SampleArgs& a);
+// One sampler block per row, rows in [1, 64], arguments read from device
+// memory (a table the caller uploads; each row validated with
+// sample_args_valid on the host).
+hipError_t launch_sample_rows(const SampleArgs* device_rows, int rows, hipStream_t stream);
 hipError_t launch_sample_logits(const bf16_t* logits, int vocabulary,
                                 bool suppress_talker_reserved, int codec_eos_token,
                                 const int* semantic_history, const int* semantic_history_count,

@@ -69,29 +69,8 @@ __device__ float uniform_random_from(uint64_t& state) {
     return static_cast<float>(static_cast<double>(value >> 11) * (1.0 / 9007199254740992.0));
 }
 
-struct SampleArgs {
-    const bf16_t* logits;
-    int vocabulary;
-    bool suppress;
-    int eos;
-    const int* history;
-    const int* history_count;
-    int history_count_fallback;
-    int do_sample;
-    int top_k;
-    float top_p;
-    float temperature;
-    float penalty;
-    uint64_t* random_state;
-    int* selected;
-    int* store_tokens;
-    const int* store_index;
-    int store_index_fallback;
-    int* append_history;   // history array to append to (talker), nullable
-    int* append_count;     // device history counter to increment, nullable
-};
 
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
+__device__ __forceinline__ void sample_one(const SampleArgs& a) {
     __shared__ float values[kMaxVocabulary];
     __shared__ unsigned char marked[kMaxVocabulary];
     __shared__ double weights[kMaxVocabulary];
@@ -423,6 +402,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) {
     }
 }
 
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(SampleArgs a) { sample_one(a); }
+
+// One block per row, each with its own arguments (the batch's sessions).
+__global__ __launch_bounds__(kSampleThreads) void sample_rows_kernel(const SampleArgs* rows) {
+    sample_one(rows[blockIdx.x]);
+}
+
 // bf16_argmax_kernel (runtime.cu:43-82): strided argmax + lower-index ties.
 __global__ __launch_bounds__(256) void argmax_kernel(const bf16_t* logits, int vocabulary,
                                                      int* selected) {
@@ -625,6 +611,17 @@ hipError_t launch_sample_logits_ex(const bf16_t* logits, int vocabulary, bool su
                  random_state, selected, store_tokens, store_index, store_index_fallback,
                  append_history, append_count};
     sample_kernel<<<1, kSampleThreads, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+bool sample_args_valid(const SampleArgs& a) {
+    return a.vocabulary > 0 && a.vocabulary <= kMaxVocabulary && a.top_k >= 0 && a.top_p > 0.0f &&
+           a.top_p <= 1.0f && a.temperature > 0.0f && a.penalty > 0.0f;
+}
+
+hipError_t launch_sample_rows(const SampleArgs* device_rows, int rows, hipStream_t stream) {
+    if (device_rows == nullptr || rows <= 0 || rows > 64) return hipErrorInvalidValue;
+    sample_rows_kernel<<<rows, kSampleThreads, 0, stream>>>(device_rows);
     return hipGetLastError();
 }
 

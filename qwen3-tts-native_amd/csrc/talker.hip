@@ -1115,7 +1115,7 @@ public:
         act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
         logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
         layers_ = T.layers + P.layers;
-        table_bytes_ = off_strides() + R * sizeof(int);
+        table_bytes_ = off_samples() + static_cast<size_t>(kCodebooks) * R * sizeof(SampleArgs);
         tables_ = DeviceBuffer(table_bytes_);
         check_hip(hipHostMalloc(&pinned_, table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
         std::memset(pinned_, 0, table_bytes_);
@@ -1151,7 +1151,7 @@ public:
             c->pending_lease_ = lease;
             c->pending_position_ = static_cast<uint32_t>(c->position_);
         }
-        fill_tables(s, n, trailing);
+        fill_tables(s, n, trailing, tp, pp);
         std::vector<uint64_t> key;
         key.push_back(static_cast<uint64_t>(n));
         for (int i = 0; i < n; ++i) {
@@ -1209,7 +1209,8 @@ private:
     // Table layout (identical in pinned host memory and in device memory):
     // positions int[kSlots][8] | K/V bases ptr[2*layers][8] | token bases ptr[8] |
     // trailing-token ptrs ptr[8] | last_hidden ptrs ptr[8] | position ptrs ptr[8] |
-    // trailing tokens int[8] | talker value-cache strides int[8]
+    // trailing tokens int[8] | talker value-cache strides int[8] |
+    // sampler arguments SampleArgs[16 samples per frame][8]
     size_t off_kv() const { return kSlots * kCapacity * sizeof(int); }
     size_t off_tokens() const { return off_kv() + 2 * layers_ * kCapacity * sizeof(void*); }
     size_t off_trail_ptrs() const { return off_tokens() + kCapacity * sizeof(void*); }
@@ -1217,6 +1218,10 @@ private:
     size_t off_pos_ptrs() const { return off_last() + kCapacity * sizeof(void*); }
     size_t off_trail_values() const { return off_pos_ptrs() + kCapacity * sizeof(void*); }
     size_t off_strides() const { return off_trail_values() + kCapacity * sizeof(int); }
+    size_t off_samples() const {
+        return (off_strides() + kCapacity * sizeof(int) + alignof(SampleArgs) - 1) / alignof(SampleArgs) *
+               alignof(SampleArgs);
+    }
     template <typename T>
     T* dev_at(size_t offset) const { return reinterpret_cast<T*>(tables_.as<char>() + offset); }
     template <typename T>
@@ -1231,8 +1236,13 @@ private:
     bf16_t* const* last_hidden_ptrs() const { return dev_at<bf16_t*>(off_last()); }
     int* const* position_ptrs() const { return dev_at<int*>(off_pos_ptrs()); }
     const int* value_strides() const { return dev_at<int>(off_strides()); }
+    // sampler rows of sample `slot` (0: talker, 1..15: predictor codebooks)
+    const SampleArgs* sample_rows(int slot) const {
+        return dev_at<SampleArgs>(off_samples()) + static_cast<size_t>(slot) * kCapacity;
+    }
 
-    void fill_tables(Session** s, int n, const int* trailing) {
+    void fill_tables(Session** s, int n, const int* trailing, const std::vector<SamplingParams>& tp,
+                     const std::vector<SamplingParams>& pp) {
         int* pos = host_at<int>(0);
         for (int slot = 0; slot < kCodebooks; ++slot)
             for (int i = 0; i < kCapacity; ++i) pos[slot * kCapacity + i] = slot;
@@ -1256,6 +1266,35 @@ private:
             host_at<int*>(off_pos_ptrs())[i] = s[i]->position_ptr();
             host_at<int>(off_trail_values())[i] = trailing[i];
             host_at<int>(off_strides())[i] = value_cache_stride(s[i]->max_seq_);
+            // sampler rows: the talker's sample (mask, penalty, history
+            // append) and the 15 predictor samples (frame token p)
+            SampleArgs* rows = host_at<SampleArgs>(off_samples());
+            Session* c = s[i];
+            for (int slot = 0; slot < kCodebooks; ++slot) {
+                const bool talker = slot == 0;
+                const SamplingParams& q = talker ? tp[i] : pp[i];
+                const int vocab = talker ? cfg_.talker_vocab : cfg_.predictor_vocab;
+                SampleArgs a{};
+                a.logits = logits_.as<bf16_t>() + static_cast<size_t>(i) * vocab;
+                a.vocabulary = vocab;
+                a.suppress = talker;
+                a.eos = cfg_.codec_eos;
+                a.history = c->history_.as<int>();
+                a.history_count = c->history_count_ptr();
+                a.do_sample = q.do_sample;
+                a.top_k = q.top_k;
+                a.top_p = q.top_p;
+                a.temperature = q.temperature;
+                a.penalty = q.penalty;
+                a.random_state = c->random_state_.as<uint64_t>();
+                a.selected = c->sampled_ptr();
+                a.store_tokens = c->frame_tokens();
+                a.store_index_fallback = slot;
+                a.append_history = talker ? c->history_.as<int>() : nullptr;
+                a.append_count = talker ? c->history_count_ptr() : nullptr;
+                if (!sample_args_valid(a)) throw std::invalid_argument("invalid sampler arguments");
+                rows[static_cast<size_t>(slot) * kCapacity + i] = a;
+            }
         }
     }
 
@@ -1341,15 +1380,7 @@ private:
             if (p >= 1) {
                 Gemv(m_.predictor_heads_[p - 1], p_hidden_.as<bf16_t>(), PH, PV, kEpiStore).norm(m_.predictor_norm_, cfg_.eps)
                     .rows(n, mode).to(logits_.as<bf16_t>()).run(stream_, "batch predictor head");
-                for (int i = 0; i < n; ++i) {
-                    Session* c = s[i];
-                    check_hip(launch_sample_logits_ex(logits_.as<bf16_t>() + static_cast<size_t>(i) * PV, PV, false,
-                                                      cfg_.codec_eos, c->history_.as<int>(), c->history_count_ptr(), 0,
-                                                      ps[i].do_sample, ps[i].top_k, ps[i].top_p, ps[i].temperature,
-                                                      ps[i].penalty, c->random_state_.as<uint64_t>(), c->sampled_ptr(),
-                                                      c->frame_tokens(), nullptr, p, nullptr, nullptr, stream_),
-                              "batch predictor sample");
-                }
+                check_hip(launch_sample_rows(sample_rows(p), n, stream_), "batch predictor sample");
             }
         }
         for (int i = 0; i < n; ++i) {
@@ -1379,15 +1410,7 @@ private:
         check_hip(launch_scatter_rows(normalized_.as<bf16_t>(), last_hidden_ptrs(), n, H, stream_), "scatter last hidden");
         Gemv(m_.codec_head_, normalized_.as<bf16_t>(), H, TV, kEpiStore).rows(n, mode).to(logits_.as<bf16_t>())
             .run(stream_, "batch codec head");
-        for (int i = 0; i < n; ++i) {
-            Session* c = s[i];
-            check_hip(launch_sample_logits_ex(logits_.as<bf16_t>() + static_cast<size_t>(i) * TV, TV, true, cfg_.codec_eos,
-                                              c->history_.as<int>(), c->history_count_ptr(), 0, ts[i].do_sample,
-                                              ts[i].top_k, ts[i].top_p, ts[i].temperature, ts[i].penalty,
-                                              c->random_state_.as<uint64_t>(), c->sampled_ptr(), c->frame_tokens(),
-                                              nullptr, 0, c->history_.as<int>(), c->history_count_ptr(), stream_),
-                      "batch talker sample");
-        }
+        check_hip(launch_sample_rows(sample_rows(0), n, stream_), "batch talker sample");
         check_hip(launch_increment_each(position_ptrs(), n, stream_), "advance positions");
     }
 
