@@ -295,7 +295,8 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
     and `frames` timed batched frames (talker top-k 50 / T 0.9 / rep 1.05,
     predictor top-k 50 / T 0.9).  The runs share the sessions, so contexts
     grow from ~870 to ~1010 positions over the three runs.  A session that
-    samples the end token leaves the batch (counted)."""
+    samples the end token (random weights) is reset and prefilled again
+    outside the timed region, so every batch keeps N sessions (counted)."""
     import numpy as np
 
     lib = hip.load()
@@ -307,19 +308,32 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
         rng = np.random.default_rng(7)
         ts = hip.sampling(1, 50, 1.0, 0.9, 1.05)
         ps = hip.sampling(1, 50, 1.0, 0.9, 1.0)
-        semantic = []
+        semantic = [0] * nmax
+        restarts = 0
+
+        def start(i, seed):
+            # prefill session i (again after an end token) until its first
+            # token is not the end token
+            nonlocal restarts
+            for attempt in range(8):
+                hip.call("qwen3_tts_session_reset", sessions[i], seed + 1000 * attempt)
+                text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
+                codec = rng.integers(0, 2048, prompt).astype(np.int32)
+                pre = hip.PrefillResult()
+                hip.call("qwen3_tts_session_prefill", sessions[i], text.ctypes.data_as(C.POINTER(C.c_int32)),
+                         codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(pre))
+                if pre.first_semantic_token != cfg.codec_eos_token:
+                    semantic[i] = pre.first_semantic_token
+                    return
+                restarts += 1
+            raise RuntimeError("prefill keeps sampling the end token")
+
         for i in range(nmax):
             s = C.c_void_p()
             mem = hip.SessionMemory()
             hip.call("qwen3_tts_session_create", model, max_seq, 100 + i, C.byref(s), C.byref(mem))
             sessions.append(s)
-            text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
-            codec = rng.integers(0, 2048, prompt).astype(np.int32)
-            pre = hip.PrefillResult()
-            hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
-                     codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(pre))
-            semantic.append(pre.first_semantic_token)
-        ended = [semantic[i] == cfg.codec_eos_token for i in range(nmax)]
+            start(i, 100 + i)
         results = {"prompt_tokens": prompt, "frames": frames,
                    "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9"}
         for n in ns:
@@ -327,10 +341,8 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
             timed_batches = 0
             t_total = 0.0
             for f in range(warm + frames):
-                live = [i for i in range(n) if not ended[i]]
-                if not live:
-                    break
-                k = len(live)
+                live = list(range(n))
+                k = n
                 arr = (C.c_void_p * k)(*[sessions[i].value for i in live])
                 tr = (C.c_int32 * k)(*[int(x) for x in rng.integers(0, cfg.text_vocabulary, k)])
                 tsa = (hip.SamplingConfig * k)(*[ts] * k)
@@ -346,8 +358,11 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
                     hip.call("qwen3_tts_session_next_frame_finish_v2", sessions[i], views[j].lease_id, None,
                              C.byref(nxt), C.byref(info))
                     semantic[i] = nxt.value
-                    ended[i] = ended[i] or bool(info.ended_by_eos) or nxt.value == cfg.codec_eos_token
                 dt = time.perf_counter() - t0
+                for i in live:
+                    if semantic[i] == cfg.codec_eos_token:  # outside the timed region
+                        restarts += 1
+                        start(i, 500 + 17 * restarts)
                 if f >= warm:
                     timed_frames += k
                     timed_batches += 1
@@ -357,7 +372,7 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
                                 "session_frames_per_second": round(timed_frames / max(t_total, 1e-9), 1),
                                 "aggregate_rtf": round(t_total / max(timed_frames, 1) / 0.080, 4),
                                 "session_frames": timed_frames}
-        results["sessions_ended_by_eos"] = int(sum(ended))
+        results["sessions_restarted_after_end_token"] = restarts
         return results
     finally:
         for s in sessions:

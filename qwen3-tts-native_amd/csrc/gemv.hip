@@ -440,13 +440,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     }
     constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
     constexpr int kTiles = kSilu ? 2 : 1;
-    static_assert(kIters % 2 == 0, "weight steps come in pairs of 8-row loads");
     constexpr int kIn = 64 * kWaves * kIters;
     constexpr int kStride = kIn + 8;  // bf16 elements per LDS row (16-byte pad)
     extern __shared__ __align__(16) bf16_t xs[];  // [rows][kStride]
     __shared__ float fold[kWaves][kTiles][16][16];
-    constexpr int kTileRow = 136;
-    __shared__ __align__(16) int8_t wtile[kWaves * kTiles * 16 * kTileRow];
     __shared__ float inverse_lds[8];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -493,21 +490,18 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     if constexpr (kOneGain) gain_chunk = reinterpret_cast<const uint4*>(a.norm_weight)[threadIdx.x % kChunks];
     __builtin_amdgcn_sched_barrier(0);
 
-    // 1. weights of this wave's K slice.  Loaded 8 lanes per row: one load
-    //    instruction covers 128 contiguous bytes of each of 8 rows (64 bytes
-    //    of 16 rows runs at ~60% of the bandwidth); load i = 2*step + half
-    //    holds rows 8*half .. 8*half+7, bytes 128*step .. 128*step+127.
-    const int load_row = lane >> 3;
-    const int load_part = lane & 7;
+    // 1. weights of this wave's K slice, loaded straight in the MFMA operand
+    //    layout: lane (m, g) takes 16 bytes of channel row m at k = 64 i +
+    //    16 g, which feed two MFMAs (bytes 0-7 and 8-15; the activations use
+    //    the same k order, so the sum covers every k once).
     int4 wq[kTiles][kIters];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            const int ch = c0 + 8 * (i & 1) + load_row;
+            const int ch = c0 + m;
             const int row = (t == 0 ? 0 : a.out_features) + (ch < a.out_features ? ch : 0);
-            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + wave * (kIn / kWaves) + 128 * (i >> 1) +
-                                16 * load_part;
+            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + wave * (kIn / kWaves) + 64 * i + 16 * group;
             wq[t][i] = stream_load(reinterpret_cast<const int4*>(src));
         }
     }
@@ -568,30 +562,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     floatx4_t acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-    // per-wave LDS tile [16 rows][136 bytes] per tile: written as loaded,
-    // read back in the MFMA operand layout (lane (m, g): 8 bytes of row m);
-    // the 8-byte row pad spreads the 16 rows over all banks
-    int8_t* tile = wtile + wave * (kTiles * 16 * kTileRow);
 #pragma unroll
-    for (int step = 0; step < kIters / 2; ++step) {
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                *reinterpret_cast<int4*>(tile + t * 16 * kTileRow + (8 * h + load_row) * kTileRow + 16 * load_part) =
-                    wq[t][2 * step + h];
-            }
+    for (int i = 0; i < kIters; ++i) {
+        const int k = wave * (kIn / kWaves) + 64 * i + 16 * group;
+        bf16x8_t b0 = {}, b1 = {};
+        if (real_col) {
+            b0 = load_bf16x8(xrow + k);
+            b1 = load_bf16x8(xrow + k + 8);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = wave * (kIn / kWaves) + 128 * step + 32 * j + 8 * group;
-            bf16x8_t b = {};
-            if (real_col) b = load_bf16x8(xrow + k);
-#pragma unroll
-            for (int t = 0; t < kTiles; ++t) {
-                const uint2 q = *reinterpret_cast<const uint2*>(tile + t * 16 * kTileRow + m * kTileRow + 32 * j + 8 * group);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bytes_to_bf16x8(q.x, q.y), b, acc[t], 0, 0, 0);
-            }
+        for (int t = 0; t < kTiles; ++t) {
+            const bf16x8_t a0 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t][i].x), static_cast<uint32_t>(wq[t][i].y));
+            const bf16x8_t a1 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t][i].z), static_cast<uint32_t>(wq[t][i].w));
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[t], 0, 0, 0);
         }
     }
 #pragma unroll
