@@ -445,6 +445,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     extern __shared__ __align__(16) bf16_t xs[];  // [rows][kStride]
     __shared__ float fold[kWaves][kTiles][16][16];
     __shared__ float inverse_lds[8];
+    __shared__ __align__(16) float statistic[kNorm ? 8 : 1][256];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int rows = a.rows;
@@ -457,16 +458,31 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     //    MFMA: request them ahead of the weights (memory returns in order).
     // The session rows (up to 8 of them) are requested ahead of the weights
     // (memory returns in order) and staged in LDS as the MFMA B operands.
-    constexpr int kXPer = (8 * kChunks + kBlock - 1) / kBlock;
+    // With the RMSNorm prologue on a 256-thread block, lane l of wave w holds
+    // row w + 4 (l / 32) at chunks l % 32 + 32 j (so few rows still spread
+    // over the waves): its elements are exactly those of eight
+    // of the reference's 256 statistic threads (elements i = v, v + 256, ...),
+    // so the statistic's partial sums come straight from registers.
+    constexpr bool kRowSplit = kNorm && kBlock == 256 && kChunks % 32 == 0 && kChunks / 32 <= 8;
+    constexpr int kXPer = kRowSplit ? kChunks / 32 : (8 * kChunks + kBlock - 1) / kBlock;
     static_assert(kXPer <= 12, "x staging holds at most 12 chunks per thread");
+    auto x_slot = [&](int j, int& r, int& c) {
+        if constexpr (kRowSplit) {
+            r = (threadIdx.x >> 6) + ((threadIdx.x >> 3) & 4);
+            c = (threadIdx.x & 31) + 32 * j;
+        } else {
+            const int idx = threadIdx.x + j * kBlock;
+            r = idx / kChunks;
+            c = idx % kChunks;
+        }
+    };
     // named registers, not an array (an array here is placed in scratch)
     uint4 x0{}, x1{}, x2{}, x3{}, x4{}, x5{}, x6{}, x7{}, x8{}, x9{}, x10{}, x11{};
     // Chunk j of this thread is row (tid + j*block) / kChunks; threads past
     // the last row load nothing (a masked load issues no request).
     auto x_load = [&](int j) {
-        const int idx = threadIdx.x + j * kBlock;
-        const int r = idx / kChunks;
-        const int c = idx % kChunks;
+        int r, c;
+        x_slot(j, r, c);
         uint4 v{};
         if (r < rows) v = *reinterpret_cast<const uint4*>(a.input + static_cast<size_t>(r) * kIn + 8 * c);
         return v;
@@ -485,9 +501,22 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     if constexpr (kXPer > 11) x11 = x_load(11);
     // When kChunks divides the block, all of a thread's chunks share the
     // column c = tid % kChunks: one RMSNorm gain chunk, requested early too.
-    constexpr bool kOneGain = kNorm && kBlock % kChunks == 0;
+    constexpr bool kOneGain = kNorm && !kRowSplit && kBlock % kChunks == 0;
     uint4 gain_chunk{};
     if constexpr (kOneGain) gain_chunk = reinterpret_cast<const uint4*>(a.norm_weight)[threadIdx.x % kChunks];
+    // row-split layout: the gain chunks of this thread's columns
+    uint4 g0{}, g1{}, g2{}, g3{}, g4{}, g5{}, g6{}, g7{};
+    if constexpr (kRowSplit) {
+        const uint4* gain = reinterpret_cast<const uint4*>(a.norm_weight) + (threadIdx.x & 31);
+        g0 = gain[0];
+        if constexpr (kXPer > 1) g1 = gain[32];
+        if constexpr (kXPer > 2) g2 = gain[64];
+        if constexpr (kXPer > 3) g3 = gain[96];
+        if constexpr (kXPer > 4) g4 = gain[128];
+        if constexpr (kXPer > 5) g5 = gain[160];
+        if constexpr (kXPer > 6) g6 = gain[192];
+        if constexpr (kXPer > 7) g7 = gain[224];
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. weights of this wave's K slice, loaded straight in the MFMA operand
@@ -517,13 +546,56 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. session rows into LDS
-    {
-        auto x_store = [&](int j, const uint4& v) {
-            const int idx = threadIdx.x + j * kBlock;
-            const int r = idx / kChunks;
-            const int c = idx % kChunks;
-            if (r < rows) *reinterpret_cast<uint4*>(xs + r * kStride + 8 * c) = v;
-        };
+    auto x_store = [&](int j, const uint4& v) {
+        int r, c;
+        x_slot(j, r, c);
+        if (r < rows) *reinterpret_cast<uint4*>(xs + r * kStride + 8 * c) = v;
+    };
+    if constexpr (kRowSplit) {
+        // Statistic partials of the reference's threads v = 8 (t % 32) + e,
+        // e = 0..7 (one fma chain over the thread's chunks in order), folded
+        // per row in the reference's tree order by the wave that holds the
+        // row; then each thread normalizes its chunks from registers.
+        const int r = (threadIdx.x >> 6) + ((threadIdx.x >> 3) & 4);
+        if (r < rows) {
+            float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            auto accumulate = [&](const uint4& v) {
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xffff0000u);
+                    part[2 * i] = fmaf(lo, lo, part[2 * i]);
+                    part[2 * i + 1] = fmaf(hi, hi, part[2 * i + 1]);
+                }
+            };
+            accumulate(x0);
+            if constexpr (kXPer > 1) accumulate(x1);
+            if constexpr (kXPer > 2) accumulate(x2);
+            if constexpr (kXPer > 3) accumulate(x3);
+            if constexpr (kXPer > 4) accumulate(x4);
+            if constexpr (kXPer > 5) accumulate(x5);
+            if constexpr (kXPer > 6) accumulate(x6);
+            if constexpr (kXPer > 7) accumulate(x7);
+            float4* dst = reinterpret_cast<float4*>(&statistic[r][8 * (threadIdx.x & 31)]);
+            dst[0] = make_float4(part[0], part[1], part[2], part[3]);
+            dst[1] = make_float4(part[4], part[5], part[6], part[7]);
+        }
+        __syncthreads();
+        if (wave < rows) {
+            const float inverse_lo = fold_partials256(statistic[wave], kIn, a.norm_epsilon);
+            const float inverse_hi = wave + 4 < rows ? fold_partials256(statistic[wave + 4], kIn, a.norm_epsilon) : 0.0f;
+            const float inverse = lane < 32 ? inverse_lo : inverse_hi;
+            x_store(0, normalize_chunk_hw(x0, g0, inverse));
+            if constexpr (kXPer > 1) x_store(1, normalize_chunk_hw(x1, g1, inverse));
+            if constexpr (kXPer > 2) x_store(2, normalize_chunk_hw(x2, g2, inverse));
+            if constexpr (kXPer > 3) x_store(3, normalize_chunk_hw(x3, g3, inverse));
+            if constexpr (kXPer > 4) x_store(4, normalize_chunk_hw(x4, g4, inverse));
+            if constexpr (kXPer > 5) x_store(5, normalize_chunk_hw(x5, g5, inverse));
+            if constexpr (kXPer > 6) x_store(6, normalize_chunk_hw(x6, g6, inverse));
+            if constexpr (kXPer > 7) x_store(7, normalize_chunk_hw(x7, g7, inverse));
+        }
+        __syncthreads();
+    } else {
         if constexpr (kXPer > 0) x_store(0, x0);
         if constexpr (kXPer > 1) x_store(1, x1);
         if constexpr (kXPer > 2) x_store(2, x2);
@@ -536,9 +608,9 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
         if constexpr (kXPer > 9) x_store(9, x9);
         if constexpr (kXPer > 10) x_store(10, x10);
         if constexpr (kXPer > 11) x_store(11, x11);
+        __syncthreads();
     }
-    __syncthreads();
-    if constexpr (kNorm) {
+    if constexpr (kNorm && !kRowSplit) {
         for (int r = wave; r < rows; r += kWaves) {
             const float inverse = wave_inverse_rms(xs + r * kStride, kIn, a.norm_epsilon);
             if (lane == 0) inverse_lds[r] = inverse;
@@ -556,8 +628,6 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
 
     // 3. MFMAs: columns m < rows are sessions, the rest zero
     const bool real_col = m < rows;
-    // without the norm the MFMA operands come straight from global memory
-    // (the rows are L2-resident): no staging round trip behind the weights
     const bf16_t* xrow = xs + (real_col ? m : 0) * kStride;
     floatx4_t acc[kTiles];
 #pragma unroll
