@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma(GemvArgs a) {
 // x 128-byte weight step is transposed through a per-wave LDS tile into the
 // v_mfma_f32_16x16x32_bf16 A operand layout.
 // ---------------------------------------------------------------------------
-template <int kIters, int kWaves, int kEpi, bool kNorm>
+template <int kIters, int kWaves, int kEpi, bool kNorm, int kSplit>
 __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     constexpr int kBlock = 64 * kWaves;
     if (a.input_row_index != nullptr) {
@@ -449,8 +449,18 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int rows = a.rows;
-    const int c0 = blockIdx.x * 16;
+    // kSplit = 2: the block owns 8 channels and the 16x16 tile is used
+    // block-diagonally -- A rows m and B columns m take channel / session
+    // m % 8 over the K half m / 8, so C[c][s] + C[c + 8][s + 8] is the sum
+    // over all of K with every weight byte still consumed once (twice the
+    // blocks for the same out_features).
+    static_assert(kSplit == 1 || kSplit == 2, "one or two K halves");
+    constexpr int kCh = 16 / kSplit;            // channels per block
+    constexpr int kSteps = kIters / kSplit;     // 64-wide k steps per wave
+    static_assert(kSteps * kSplit == kIters, "whole k steps per K part");
+    const int c0 = blockIdx.x * kCh;
     const int m = lane & 15;
+    const int part_k = (m / kCh) * (kIn / kSplit);  // first k of this lane's K part
     const int group = lane >> 4;
     constexpr int kChunks = kIn / 8;  // 16-byte chunks per row
 
@@ -523,14 +533,15 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     //    layout: lane (m, g) takes 16 bytes of channel row m at k = 64 i +
     //    16 g, which feed two MFMAs (bytes 0-7 and 8-15; the activations use
     //    the same k order, so the sum covers every k once).
-    int4 wq[kTiles][kIters];
+    int4 wq[kTiles][kSteps];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
 #pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            const int ch = c0 + m;
+        for (int i = 0; i < kSteps; ++i) {
+            const int ch = c0 + m % kCh;
             const int row = (t == 0 ? 0 : a.out_features) + (ch < a.out_features ? ch : 0);
-            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + wave * (kIn / kWaves) + 64 * i + 16 * group;
+            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + part_k + wave * (kIn / kSplit / kWaves) +
+                                64 * i + 16 * group;
             wq[t][i] = stream_load(reinterpret_cast<const int4*>(src));
         }
     }
@@ -538,7 +549,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     const int out_row = threadIdx.x >> 4;
     const int out_col = threadIdx.x & 15;
     const int out_ch = c0 + out_row;
-    const bool writes = threadIdx.x < 256 && out_col < rows && out_ch < a.out_features;
+    const bool writes = threadIdx.x < 16 * kCh && out_col < rows && out_ch < a.out_features;
     GemvArgs out_args = a;
     out_args.out16 = a.out16 ? a.out16 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
     out_args.out32 = a.out32 ? a.out32 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
@@ -627,14 +638,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     }
 
     // 3. MFMAs: columns m < rows are sessions, the rest zero
-    const bool real_col = m < rows;
-    const bf16_t* xrow = xs + (real_col ? m : 0) * kStride;
+    const bool real_col = m % kCh < rows;
+    const bf16_t* xrow = xs + (real_col ? m % kCh : 0) * kStride + part_k;
     floatx4_t acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kIters; ++i) {
-        const int k = wave * (kIn / kWaves) + 64 * i + 16 * group;
+    for (int i = 0; i < kSteps; ++i) {
+        const int k = wave * (kIn / kSplit / kWaves) + 64 * i + 16 * group;
         bf16x8_t b0 = {}, b1 = {};
         if (real_col) {
             b0 = load_bf16x8(xrow + k);
@@ -661,6 +672,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
             float v = fold[0][t][out_row][out_col];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) v += fold[w][t][out_row][out_col];
+            if constexpr (kSplit == 2) {
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v += fold[w][t][out_row + kCh][out_col + kCh];
+            }
             value[t] = v;
         }
         if constexpr (kSilu) {
@@ -671,19 +686,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     }
 }
 
-template <int kIters, int kWaves, int kEpi, bool kNorm>
+template <int kIters, int kWaves, int kEpi, bool kNorm, int kSplit>
 hipError_t launch_mfma_fixed(const GemvArgs& a, hipStream_t s) {
     constexpr int kIn = 64 * kWaves * kIters;
+    constexpr int kCh = 16 / kSplit;
     const size_t lds = static_cast<size_t>(a.rows) * (kIn + 8) * sizeof(bf16_t);
     static bool configured = false;
     if (!configured) {
-        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm>),
+        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit>),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                                   static_cast<int>(8 * (kIn + 8) * sizeof(bf16_t)));
         if (st != hipSuccess) return st;
         configured = true;
     }
-    gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm><<<(a.out_features + 15) / 16, 64 * kWaves, lds, s>>>(a);
+    gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit><<<(a.out_features + kCh - 1) / kCh, 64 * kWaves, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -775,12 +791,18 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
         if (a.in_features % 256 != 0 || (kNorm && a.in_features > 6144)) {
             return hipErrorInvalidValue;
         }
+        // 8-channel blocks (K halves on the tile's diagonal blocks) where
+        // 16-channel blocks would leave CUs idle; with the RMSNorm prologue
+        // every block stages and normalizes all rows, which only pays off
+        // for the wide fused gate/up (measured on MI355X, rows 2..8).
+        constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+        const bool split = kNorm ? (kSilu && a.in_features >= 2048) : a.out_features / 16 < 256;
         switch (a.in_features) {
             // kIters = K / (64 * waves); 8 waves where K is long
-            case 1024: return launch_mfma_fixed<4, 4, kEpi, kNorm>(a, s);
-            case 2048: return launch_mfma_fixed<8, 4, kEpi, kNorm>(a, s);
-            case 3072: return launch_mfma_fixed<6, 8, kEpi, kNorm>(a, s);
-            case 6144: return launch_mfma_fixed<12, 8, kEpi, kNorm>(a, s);
+            case 1024: return split ? launch_mfma_fixed<4, 4, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<4, 4, kEpi, kNorm, 1>(a, s);
+            case 2048: return split ? launch_mfma_fixed<8, 4, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<8, 4, kEpi, kNorm, 1>(a, s);
+            case 3072: return split ? launch_mfma_fixed<6, 8, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<6, 8, kEpi, kNorm, 1>(a, s);
+            case 6144: return split ? launch_mfma_fixed<12, 8, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<12, 8, kEpi, kNorm, 1>(a, s);
             default: break;
         }
         const int grid = (a.out_features + 15) / 16;

@@ -57,7 +57,7 @@ def test_exact_rows_bit_identical(hip, orc, rows, out_f, in_f):
 
 
 @pytest.mark.parametrize("rows", [2, 4, 8])
-@pytest.mark.parametrize("out_f,in_f", [(12288, 2048), (2048, 6144), (64, 256), (130, 512)])
+@pytest.mark.parametrize("out_f,in_f", [(12288, 2048), (2048, 6144), (1028, 2048), (1024, 3072), (2052, 1024), (64, 256), (130, 512)])
 def test_mfma_rows_within_tolerance(hip, orc, rows, out_f, in_f):
     rng = np.random.default_rng(rows + out_f + in_f)
     w, s, x = gen.weights(rng, out_f, in_f), gen.scales(rng, out_f), gen.activations(rng, rows, in_f)
@@ -146,9 +146,14 @@ def test_rmsnorm_prologue_bit_identical(hip, orc, in_f, out_f):
     assert np.array_equal(y16.numpy(), ref16)
 
 
-def test_rmsnorm_prologue_mfma_rows(hip, orc):
-    rng = np.random.default_rng(5)
-    in_f, out_f, rows = 2048, 1024, 4
+@pytest.mark.parametrize("rows", [2, 3, 8])
+@pytest.mark.parametrize("in_f", [1024, 2048])
+@pytest.mark.parametrize("out_f", [1024, 1004])
+def test_rmsnorm_prologue_mfma_rows(hip, orc, rows, in_f, out_f):
+    """Batched RMSNorm prologue (both block shapes: 16 channels, and 8
+    channels over two K halves for the fused gate/up at K >= 2048), ragged
+    channel counts included."""
+    rng = np.random.default_rng(5 + rows + in_f + out_f)
     w, s, x, g = gen.weights(rng, out_f, in_f), gen.scales(rng, out_f), gen.activations(rng, rows, in_f), gen.gains(rng, in_f)
     xn = orc.rms_norm_rows(x, g)
     ref32, _ = orc.int8_gemm_rows(w, s, xn)
@@ -157,6 +162,11 @@ def test_rmsnorm_prologue_mfma_rows(hip, orc):
                   norm_weight=dev(hip, g), mode=hip.MODE_MFMA)
     got = y32.numpy()
     assert np.all(np.abs(got - ref32) <= ATOL + RTOL * np.abs(ref32))
+    wgu, sgu = gen.weights(rng, 2 * out_f, in_f), gen.scales(rng, 2 * out_f)
+    y = hip.DeviceArray((rows, out_f), np.uint16)
+    hip.int8_gemv(dev(hip, wgu), dev(hip, sgu), dev(hip, x), in_f, out_f, rows, out16=y,
+                  epilogue=hip.EPI_SILU_FUSED, norm_weight=dev(hip, g), mode=hip.MODE_MFMA)
+    check("mfma", y.numpy(), orc.int8_gate_up_silu_rows(wgu, sgu, xn))
 
 
 def test_input_row_index(hip, orc):
