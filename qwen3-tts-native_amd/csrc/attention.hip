@@ -623,9 +623,10 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// The code predictor's caches (<= 16 positions), exact order, fused QKV
-// epilogue: one wave per (query head, row) does everything, with no block
-// barrier.  Lane l holds elements l and l+64 of every 128-wide vector, which
+// The code predictor's caches (<= 16 positions), fused QKV epilogue, in the
+// exact order (kExact) or the batched path's order (kExact = false; the
+// reference's causal_gqa_attention_fast): one wave per (query head, row)
+// does everything, with no block barrier.  Lane l holds elements l and l+64 of every 128-wide vector, which
 // is the layout the reference's tree needs: the exact score's
 // s[t] = q[t]k[t] + q[t+64]k[t+64] sits in lane t and its halving tree is a
 // wave shuffle-down tree (wave_sum_down).  The wave normalizes and rotates its
@@ -637,8 +638,8 @@ __global__ __launch_bounds__(kG * kDim) void attention_small_kernel(AttnArgs a) 
 // ---------------------------------------------------------------------------
 constexpr int kShortCapacity = 16;
 
-template <int kG>
-__global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
+template <bool kExact, int kG>
+__global__ __launch_bounds__(64) void attention_short_kernel(AttnArgs a) {
     const int row = blockIdx.y;
     const int head = blockIdx.x;
     const int kvh = head / kG;
@@ -756,7 +757,25 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
     const int length = position + 1;
     const bool live = lane < length;
     float score;
-    {
+    if constexpr (!kExact) {
+        // batched semantics (causal_gqa_attention_fast): lane p < 16 forms
+        // position p's dot as one fma chain over the dimensions in order
+        const uint4* qv = reinterpret_cast<const uint4*>(head_lds[0]);
+        const uint4* kv = rows_lds[1][lane & 15];
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kDim / 8; ++c) {
+            const uint4 qa = qv[c], ka = kv[c];
+            const uint32_t qw[4] = {qa.x, qa.y, qa.z, qa.w};
+            const uint32_t kw[4] = {ka.x, ka.y, ka.z, ka.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dot = fmaf(lo_bf(qw[i]), lo_bf(kw[i]), dot);
+                dot = fmaf(hi_bf(qw[i]), hi_bf(kw[i]), dot);
+            }
+        }
+        score = live ? dot * a.scale : -INFINITY;
+    } else {
         const int sp = lane & 15;
         const int j = lane >> 4;
         const uint4* qv = reinterpret_cast<const uint4*>(head_lds[0]);
@@ -799,15 +818,25 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
     //    exponentials and then the 16 probabilities reach every lane as
     //    scalar operands (lane reads); entries past the current position are
     //    0, and adding them leaves the sequential sum as it is.
+    //    Batched semantics: the normalizer is the 256-thread tree, whose
+    //    levels 128 and 64 only add zeros here (a wave shuffle-down tree),
+    //    the value chains take the unnormalized exponentials, and the
+    //    output is scaled by the inverse once.
     const float maximum = wave_max(score);
     const float e = live ? q3_expf(score - maximum) : 0.0f;
-    float denominator = 0.0f;
+    float inverse;
+    if constexpr (kExact) {
+        float denominator = 0.0f;
 #pragma unroll
-    for (int p = 0; p < kShortCapacity; ++p) {
-        denominator += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
+        for (int p = 0; p < kShortCapacity; ++p) {
+            denominator += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), p));
+        }
+        inverse = 1.0f / denominator;
+    } else {
+        const float total = wave_sum_down<64>(e);
+        inverse = 1.0f / __int_as_float(__builtin_amdgcn_readlane(__float_as_int(total), 0));
     }
-    const float inverse = 1.0f / denominator;
-    const float prob = live ? round_bf(e * inverse) : 0.0f;
+    const float prob = kExact ? (live ? round_bf(e * inverse) : 0.0f) : e;
     float pv[kShortCapacity];
 #pragma unroll
     for (int p = 0; p < kShortCapacity; ++p) pv[p] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), p));
@@ -822,6 +851,10 @@ __global__ __launch_bounds__(64) void attention_short_exact_kernel(AttnArgs a) {
         const bool in = p <= position;
         acc0 = fmaf(pv[p], in ? v0[p] : 0.0f, acc0);
         acc1 = fmaf(pv[p], in ? v1[p] : 0.0f, acc1);
+    }
+    if constexpr (!kExact) {
+        acc0 *= inverse;
+        acc1 *= inverse;
     }
     bf16_t* out = a.output + (static_cast<size_t>(row) * a.query_heads + head) * kDim;
     out[lane] = f2bf(acc0);
@@ -842,8 +875,8 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         if (st != hipSuccess) return st;
         configured = true;
     }
-    if (kExact && a.capacity <= kShortCapacity && a.q_norm != nullptr) {
-        attention_short_exact_kernel<kG><<<dim3(a.query_heads, rows), 64, 0, stream>>>(a);
+    if (a.capacity <= kShortCapacity && a.q_norm != nullptr) {
+        attention_short_kernel<kExact, kG><<<dim3(a.query_heads, rows), 64, 0, stream>>>(a);
         return hipGetLastError();
     }
     if (a.capacity <= kSmallCapacity) {
