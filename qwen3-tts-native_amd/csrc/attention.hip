@@ -867,14 +867,10 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
     // LDS: up to 160 KB per workgroup on gfx950
     constexpr size_t kLdsLimit = 160 * 1024;
     if (head_lds > kLdsLimit) return hipErrorInvalidValue;
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_head_kernel<kExact, kG>),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  static_cast<int>(kLdsLimit));
-        if (st != hipSuccess) return st;
-        configured = true;
-    }
+    static std::atomic<unsigned long long> configured{0};
+    const hipError_t st = set_dynamic_lds_once(configured, reinterpret_cast<const void*>(attention_head_kernel<kExact, kG>),
+                                               static_cast<int>(kLdsLimit));
+    if (st != hipSuccess) return st;
     if (a.capacity <= kShortCapacity && a.q_norm != nullptr) {
         attention_short_kernel<kExact, kG><<<dim3(a.query_heads, rows), 64, 0, stream>>>(a);
         return hipGetLastError();

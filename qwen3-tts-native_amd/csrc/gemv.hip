@@ -691,14 +691,11 @@ hipError_t launch_mfma_fixed(const GemvArgs& a, hipStream_t s) {
     constexpr int kIn = 64 * kWaves * kIters;
     constexpr int kCh = 16 / kSplit;
     const size_t lds = static_cast<size_t>(a.rows) * (kIn + 8) * sizeof(bf16_t);
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit>),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  static_cast<int>(8 * (kIn + 8) * sizeof(bf16_t)));
-        if (st != hipSuccess) return st;
-        configured = true;
-    }
+    static std::atomic<unsigned long long> configured{0};
+    const hipError_t st = set_dynamic_lds_once(
+        configured, reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit>),
+        static_cast<int>(8 * (kIn + 8) * sizeof(bf16_t)));
+    if (st != hipSuccess) return st;
     gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit><<<(a.out_features + kCh - 1) / kCh, 64 * kWaves, lds, s>>>(a);
     return hipGetLastError();
 }

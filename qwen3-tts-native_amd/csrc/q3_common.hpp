@@ -8,12 +8,26 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
 
 namespace q3 {
+
+// Raises a kernel's dynamic LDS limit once per device (the attribute is held
+// per device): `done` is the call site's bit set of devices already set up.
+inline hipError_t set_dynamic_lds_once(std::atomic<unsigned long long>& done, const void* kernel, int bytes) {
+    int device = 0;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) return st;
+    const unsigned long long bit = 1ull << (device & 63);
+    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+    st = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (st == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    return st;
+}
 
 using bf16_t = uint16_t;
 

@@ -447,15 +447,12 @@ size_t stream_chain_lds_bytes() { return sizeof(Lds); }
 hipError_t launch_stream_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups, hipStream_t stream,
                                unsigned long long* trace) {
     if (ops == nullptr || count <= 0 || sync == nullptr || workgroups <= 0) return hipErrorInvalidValue;
-    static bool configured = false;
-    if (!configured) {
-        hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(stream_chain_kernel),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(Lds)));
-        if (st != hipSuccess) return st;
-        configured = true;
-    }
+    static std::atomic<unsigned long long> configured{0};
+    hipError_t st = set_dynamic_lds_once(configured, reinterpret_cast<const void*>(stream_chain_kernel),
+                                         static_cast<int>(sizeof(Lds)));
+    if (st != hipSuccess) return st;
     zero_stream_sync<<<1, 256, 0, stream>>>(sync, kChainSyncWords);
-    hipError_t st = hipGetLastError();
+    st = hipGetLastError();
     if (st != hipSuccess) return st;
     StreamState state{sync, trace};
     void* args[] = {const_cast<ChainOp**>(&ops), &count, &state};
