@@ -72,11 +72,8 @@ def test_mfma_rows_within_tolerance(hip, orc, rows, out_f, in_f):
     assert np.allclose(got, ref64, rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("mode", ["exact", "mfma"])
-@pytest.mark.parametrize("rows", [1, 4])
+@pytest.mark.parametrize("mode,rows", [("exact", 1), ("exact", 4), ("mfma", 2), ("mfma", 4)])
 def test_epilogues(hip, orc, mode, rows):
-    if mode == "mfma" and rows == 1:
-        pytest.skip("MFMA path serves rows >= 2")
     rng = np.random.default_rng(7 + rows)
     in_f, out_f = 1024, 384
     m = hip.MODE_EXACT if mode == "exact" else hip.MODE_MFMA
