@@ -391,6 +391,9 @@ def main() -> int:
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel's workload (the 28 gate/up GEMVs of a step) and a "
                          "256 MiB device-to-device copy that calibrates the HBM byte counters; for rocprofv3 --pmc")
+    ap.add_argument("--only-batched-frames", action="store_true",
+                    help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
+                         "for rocprofv3 kernel statistics")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the decode path on a single MI355X "
@@ -399,6 +402,9 @@ def main() -> int:
     import qwen3_tts_hip as hip
 
     hip.load()
+    if args.only_batched_frames:
+        print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
+        return 0
     if args.only_dominant:
         import numpy as np
 
