@@ -144,7 +144,7 @@ def test_rmsnorm_prologue_bit_identical(hip, orc, in_f, out_f):
 
 
 @pytest.mark.parametrize("rows", [2, 3, 8])
-@pytest.mark.parametrize("in_f", [1024, 2048])
+@pytest.mark.parametrize("in_f", [1024, 2048, 3072])
 @pytest.mark.parametrize("out_f", [1024, 1004])
 def test_rmsnorm_prologue_mfma_rows(hip, orc, rows, in_f, out_f):
     """Batched RMSNorm prologue (both block shapes: 16 channels, and 8
