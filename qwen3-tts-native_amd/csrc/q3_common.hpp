@@ -339,6 +339,9 @@ hipError_t launch_argmax_bf16(const bf16_t* logits, int vocabulary, int* selecte
 hipError_t launch_store_token(int* tokens, int index, int value, hipStream_t stream);
 hipError_t launch_pack_frame_codes(const int* tokens, uint16_t* codes, int count,
                                    hipStream_t stream);
+// Batch form: row r packs tokens[r][0..count) into codes[r].
+hipError_t launch_pack_frame_codes_rows(const int* const* tokens, uint16_t* const* codes, int count, int rows,
+                                        hipStream_t stream);
 hipError_t launch_gather_embedding(const bf16_t* table, int vocabulary, int width,
                                    const int* token, bf16_t* output, bool add,
                                    hipStream_t stream);

@@ -456,6 +456,12 @@ __global__ void pack_codes_kernel(const int* tokens, uint16_t* codes, int count)
     if (i < count) codes[i] = static_cast<uint16_t>(tokens[i]);
 }
 
+// One block per session of a batch: the frame's tokens into its code row.
+__global__ void pack_codes_rows_kernel(const int* const* tokens, uint16_t* const* codes, int count) {
+    const int i = threadIdx.x;
+    if (i < count) codes[blockIdx.x][i] = static_cast<uint16_t>(tokens[blockIdx.x][i]);
+}
+
 // gather_embedding_kernel (sampling_kernels.cu:428-452): an out-of-range
 // token leaves the output untouched.
 __global__ void gather_embedding_kernel(const bf16_t* table, int vocabulary, int width,
@@ -641,6 +647,13 @@ hipError_t launch_pack_frame_codes(const int* tokens, uint16_t* codes, int count
                                    hipStream_t stream) {
     if (count <= 0 || count > 64) return hipErrorInvalidValue;
     pack_codes_kernel<<<1, 64, 0, stream>>>(tokens, codes, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_frame_codes_rows(const int* const* tokens, uint16_t* const* codes, int count, int rows,
+                                        hipStream_t stream) {
+    if (count <= 0 || count > 64 || rows <= 0) return hipErrorInvalidValue;
+    pack_codes_rows_kernel<<<rows, 64, 0, stream>>>(tokens, codes, count);
     return hipGetLastError();
 }
 

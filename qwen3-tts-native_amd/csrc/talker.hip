@@ -1115,7 +1115,7 @@ public:
         act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
         logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
         layers_ = T.layers + P.layers;
-        table_bytes_ = off_samples() + static_cast<size_t>(kCodebooks) * R * sizeof(SampleArgs);
+        table_bytes_ = off_codes() + kCapacity * sizeof(void*);
         tables_ = DeviceBuffer(table_bytes_);
         check_hip(hipHostMalloc(&pinned_, table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
         std::memset(pinned_, 0, table_bytes_);
@@ -1210,7 +1210,7 @@ private:
     // positions int[kSlots][8] | K/V bases ptr[2*layers][8] | token bases ptr[8] |
     // trailing-token ptrs ptr[8] | last_hidden ptrs ptr[8] | position ptrs ptr[8] |
     // trailing tokens int[8] | talker value-cache strides int[8] |
-    // sampler arguments SampleArgs[16 samples per frame][8]
+    // sampler arguments SampleArgs[16 samples per frame][8] | code rows uint16_t*[8]
     size_t off_kv() const { return kSlots * kCapacity * sizeof(int); }
     size_t off_tokens() const { return off_kv() + 2 * layers_ * kCapacity * sizeof(void*); }
     size_t off_trail_ptrs() const { return off_tokens() + kCapacity * sizeof(void*); }
@@ -1221,6 +1221,10 @@ private:
     size_t off_samples() const {
         return (off_strides() + kCapacity * sizeof(int) + alignof(SampleArgs) - 1) / alignof(SampleArgs) *
                alignof(SampleArgs);
+    }
+    size_t off_codes() const {
+        return (off_samples() + static_cast<size_t>(kCodebooks) * kCapacity * sizeof(SampleArgs) + alignof(void*) - 1) /
+               alignof(void*) * alignof(void*);
     }
     template <typename T>
     T* dev_at(size_t offset) const { return reinterpret_cast<T*>(tables_.as<char>() + offset); }
@@ -1261,6 +1265,7 @@ private:
                 kv[(2 * (TL + l) + 1) * kCapacity + i] = hb[2 * TL + PL + l];
             }
             host_at<const int*>(off_tokens())[i] = s[i]->frame_tokens();
+            host_at<uint16_t*>(off_codes())[i] = s[i]->codes_.as<uint16_t>();
             host_at<const int*>(off_trail_ptrs())[i] = trail_dev + i;
             host_at<bf16_t*>(off_last())[i] = s[i]->last_hidden_.as<bf16_t>();
             host_at<int*>(off_pos_ptrs())[i] = s[i]->position_ptr();
@@ -1383,10 +1388,8 @@ private:
                 check_hip(launch_sample_rows(sample_rows(p), n, stream_), "batch predictor sample");
             }
         }
-        for (int i = 0; i < n; ++i) {
-            check_hip(launch_pack_frame_codes(s[i]->frame_tokens(), s[i]->codes_.as<uint16_t>(), kCodebooks, stream_),
-                      "pack frame codes");
-        }
+        check_hip(launch_pack_frame_codes_rows(token_bases(), dev_at<uint16_t* const>(off_codes()), kCodebooks, n, stream_),
+                  "pack frame codes");
     }
 
     void enqueue_talker(Session** s, int n, const std::vector<SamplingParams>& ts) {
