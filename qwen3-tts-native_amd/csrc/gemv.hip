@@ -591,7 +591,9 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
             dst[0] = make_float4(part[0], part[1], part[2], part[3]);
             dst[1] = make_float4(part[4], part[5], part[6], part[7]);
         }
-        __syncthreads();
+        // rows w and w + 4 are held and folded by wave w alone: its LDS
+        // accesses complete in order, so no block barrier is needed here
+        __builtin_amdgcn_wave_barrier();
         if (wave < rows) {
             const float inverse_lo = fold_partials256(statistic[wave], kIn, a.norm_epsilon);
             const float inverse_hi = wave + 4 < rows ? fold_partials256(statistic[wave + 4], kIn, a.norm_epsilon) : 0.0f;
