@@ -1,0 +1,166 @@
+"""Pins the oracle's model-level sequence (oracle/oracle.c orc_prefill,
+orc_frame_step, orc_run_decoder, orc_project_text) against the independent
+float64 NumPy model in frame_f64.py.
+
+The two agree up to accumulation-order rounding: the oracle sums in the
+reference's fp32 order, the NumPy model in float64, and both round to bf16
+where the reference stores bf16.  Every comparison is made with the NumPy
+model teacher-forced on the oracle's tokens, so continuous state (KV caches,
+hidden states, logits) is compared with a tolerance while every discrete
+choice (greedy token) must agree wherever the NumPy logits' top-2 margin is
+larger than twice that tolerance.
+
+Bound: a bf16 rounding flip is 2^-8 relative; through a few layers and an LM
+head such flips stay below 1 % of the tensor's largest magnitude (measured
+maximum on these models: 0.56 %, in the batched predictor's KV cache; most
+tensors agree exactly).  A structural
+mistake -- a dropped residual, the un-normalized hidden seeding predictor
+position 0, an embedding table or LM head off by one codebook, a RoPE
+position off by one, a missing text projection -- moves these tensors by
+tens of percent; the sensitivity test below shows five such mistakes failing.
+"""
+import numpy as np
+import pytest
+
+import toy_model
+from frame_f64 import F64Model, from_bits
+from toy_model import TOY
+
+REL = 0.01  # of the tensor's max magnitude
+
+GREEDY = (0, 0, 1.0, 1.0, 1.05)
+SMALL = dict(TOY, talker_hidden=256, talker_intermediate=512, predictor_hidden=256,
+             predictor_intermediate=384, text_vocabulary=300)
+
+
+def close(got, ref, what):
+    scale = np.max(np.abs(ref))
+    err = np.max(np.abs(got - ref))
+    assert err <= REL * scale, f"{what}: max err {err:.4g} vs scale {scale:.4g}"
+    return err / scale
+
+
+def check_token(scores, token, what):
+    """The oracle's greedy token must be the NumPy argmax unless the top two
+    NumPy scores are within the comparison bound."""
+    finite = scores[np.isfinite(scores)]
+    bound = 2 * REL * np.max(np.abs(finite))
+    best = int(np.argmax(scores))
+    if best == token:
+        return True
+    top2 = np.sort(finite)[-2:]
+    assert scores[token] >= scores[best] - bound, f"{what}: oracle {token}, numpy {best}, margin {top2[1] - top2[0]}"
+    return False
+
+
+def run(orc, c, seed, frames=3, prompt=6, batch=False, model_cls=F64Model):
+    weights = toy_model.make_weights(c, seed=seed)
+    om = toy_model.OracleModel(orc, c, weights, batch_semantics=batch)
+    fm = model_cls(c, weights, batch_semantics=batch)
+    rng = np.random.default_rng(seed + 1)
+    max_seq = 32
+    text = rng.integers(0, c["text_vocabulary"], prompt).astype(np.int32)
+    codec = rng.integers(0, 2048, prompt).astype(np.int32)
+    text[1] = -1  # a codec-only position (zero text embedding)
+    codec[0] = -1  # a text-only position
+    o = toy_model.OracleSession(om, max_seq, 7)
+    om.model.batch_semantics = 0  # prefill is single-session in both
+    fm.batch = False
+    first = o.prefill(text, codec, GREEDY)
+    st = fm.new_session(max_seq)
+    for t, cd in zip(text, codec):
+        _, logits = fm.talker_step(st, fm.prompt_embedding(int(t), int(cd)))
+    b = o.bufs
+    kv = c["talker_key_value_heads"] * c["head_dimension"]
+    tk = from_bits(b["tk"]).reshape(c["talker_layers"], max_seq, kv)
+    close(tk[:, :prompt], st["talker"]["k"][:, :prompt].reshape(c["talker_layers"], prompt, kv), "prefill K cache")
+    close(from_bits(b["last"]), st["last_hidden"], "prefill last hidden")
+    close(from_bits(b["logits"][:c["talker_vocabulary"]]), logits, "prefill logits")
+    check_token(fm.talker_scores(logits, [], GREEDY[4]), first, "prefill first token")
+    st["history"].append(first)
+    om.model.batch_semantics = int(batch)
+    fm.batch = batch
+    sem, agreed = first, 0
+    for f in range(frames):
+        if sem == c["codec_eos_token"]:
+            break
+        trailing = int(rng.integers(0, c["text_vocabulary"]))
+        codes, nxt = o.frame(sem, trailing, GREEDY, GREEDY)
+        pred_logits, logits = fm.frame_logits(st, [int(x) for x in codes], trailing)
+        for r, pl in enumerate(pred_logits):
+            agreed += check_token(pl, int(codes[r + 1]), f"frame {f} codebook {r + 1}")
+        pkv = c["predictor_key_value_heads"] * c["head_dimension"]
+        pk = from_bits(b["pk"]).reshape(c["predictor_layers"], 16, pkv)
+        pv = from_bits(b["pv"]).reshape(c["predictor_layers"], 16, pkv)
+        close(pk, st["predictor"]["k"].reshape(pk.shape), f"frame {f} predictor K cache")
+        close(pv, st["predictor"]["v"].reshape(pv.shape), f"frame {f} predictor V cache")
+        pos = st["position"]
+        tv = from_bits(b["tv"]).reshape(c["talker_layers"], max_seq, kv)
+        close(tv[:, :pos], st["talker"]["v"][:, :pos].reshape(c["talker_layers"], pos, kv), f"frame {f} talker V cache")
+        close(from_bits(b["last"]), st["last_hidden"], f"frame {f} last hidden")
+        close(from_bits(b["logits"][:c["talker_vocabulary"]]), logits, f"frame {f} talker logits")
+        agreed += check_token(fm.talker_scores(logits, st["history"], GREEDY[4]), nxt, f"frame {f} next token")
+        st["history"].append(nxt)
+        sem = nxt
+    return agreed
+
+
+@pytest.mark.parametrize("batch", [False, True])
+@pytest.mark.parametrize("seed", [3, 11])
+def test_oracle_frames_match_float64_model(orc, seed, batch):
+    agreed = run(orc, SMALL, seed, batch=batch)
+    assert agreed >= 40  # the token checks were not vacuous: most tokens had a clear margin
+
+
+def test_oracle_frames_match_float64_model_wide_predictor(orc):
+    """16 query / 8 key-value predictor heads (the production GQA shape)."""
+    c = dict(SMALL, predictor_query_heads=16, predictor_key_value_heads=8, predictor_hidden=512)
+    agreed = run(orc, c, 5, frames=2)
+    assert agreed >= 25
+
+
+class _WrongHead(F64Model):
+    def predictor_position(self, state, x, position, head):
+        return super().predictor_position(state, x, position, head if head < 0 else (head + 1) % 15)
+
+
+class _RopeOffByOne(F64Model):
+    def rope(self, x, position, d):
+        return super().rope(x, position + 1, d)
+
+
+class _RawSeed(F64Model):
+    """Predictor position 0 seeded with the talker's un-normalized hidden."""
+
+    def decoder(self, part, h, cache, position):
+        out = super().decoder(part, h, cache, position)
+        if part == "talker":
+            self._raw = out
+        return out
+
+    def predictor_position(self, state, x, position, head):
+        return super().predictor_position(state, self._raw if position == 0 else x, position, head)
+
+
+class _NoTextProjection(F64Model):
+    def frame_logits(self, state, codes, trailing_text):
+        self.project_text, keep = (lambda t: np.zeros(self.talker.hidden)), self.project_text
+        try:
+            return super().frame_logits(state, codes, trailing_text)
+        finally:
+            self.project_text = keep
+
+
+class _ResidualEmbeddingOffByOne(F64Model):
+    def __init__(self, *a, **k):
+        super().__init__(*a, **k)
+        self.pred_emb = self.pred_emb[1:] + self.pred_emb[:1]
+
+
+@pytest.mark.parametrize("mutant", [_WrongHead, _RopeOffByOne, _RawSeed, _NoTextProjection,
+                                    _ResidualEmbeddingOffByOne])
+def test_float64_model_detects_structural_mistakes(orc, mutant):
+    """The comparison is sensitive: a NumPy model with one plausible
+    structural mistake fails it."""
+    with pytest.raises(AssertionError):
+        run(orc, SMALL, 3, frames=2, model_cls=mutant)
