@@ -103,26 +103,90 @@ float orc_uniform_random(uint64_t* state) {
 /* int8 GEMV family                                                          */
 /* ------------------------------------------------------------------------ */
 
-/* quantize_weight_rows_kernel, K/int8_gemv.cu:20-52: per row absmax
- * (max is order independent), scale = amax/127 or 1, value = w * (1/scale),
- * clamp to +-127, lrintf (round half to even). */
-void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
-                              float* scales, int in_features, int out_features) {
-    for (int r = 0; r < out_features; ++r) {
-        const uint16_t* row = weight + (size_t)r * in_features;
+/* Channel-range parallelism for the model-level restatement: every output
+ * channel is computed independently in the exact order, so splitting the
+ * channels over threads changes no bit.  orc_set_threads(n) sets the count
+ * (1 by default); small matrices always run on the calling thread. */
+static int g_threads = 1;
+
+void orc_set_threads(int threads) {
+    g_threads = threads < 1 ? 1 : (threads > 256 ? 256 : threads);
+}
+
+typedef void (*ChannelRangeFn)(void* ctx, int c0, int c1);
+typedef struct RangeJob {
+    ChannelRangeFn fn;
+    void* ctx;
+    int c0, c1;
+} RangeJob;
+
+static void* range_worker(void* arg) {
+    RangeJob* j = (RangeJob*)arg;
+    j->fn(j->ctx, j->c0, j->c1);
+    return NULL;
+}
+
+static void for_channels(int channels, size_t work, ChannelRangeFn fn, void* ctx) {
+    int threads = g_threads;
+    if (work < ((size_t)1 << 20) || threads <= 1) {
+        fn(ctx, 0, channels);
+        return;
+    }
+    if (threads > channels) threads = channels;
+    pthread_t tid[256];
+    RangeJob jobs[256];
+    const int per = (channels + threads - 1) / threads;
+    int started = 0;
+    for (int t = 0; t < threads; ++t) {
+        const int c0 = t * per;
+        const int c1 = c0 + per < channels ? c0 + per : channels;
+        if (c0 >= c1) break;
+        jobs[t] = (RangeJob){fn, ctx, c0, c1};
+        if (pthread_create(&tid[t], NULL, range_worker, &jobs[t]) != 0) {
+            range_worker(&jobs[t]);
+            tid[t] = 0;
+        }
+        started = t + 1;
+    }
+    for (int t = 0; t < started; ++t) {
+        if (tid[t]) pthread_join(tid[t], NULL);
+    }
+}
+
+typedef struct QuantCtx {
+    const uint16_t* weight;
+    int8_t* quantized;
+    float* scales;
+    int in_features;
+} QuantCtx;
+
+static void quantize_range(void* p, int r0, int r1) {
+    const QuantCtx* q = (const QuantCtx*)p;
+    const int in_features = q->in_features;
+    for (int r = r0; r < r1; ++r) {
+        const uint16_t* row = q->weight + (size_t)r * in_features;
         float maximum = 0.0f;
         for (int i = 0; i < in_features; ++i) {
             maximum = fmaxf(maximum, fabsf(bf(row[i])));
         }
         const float scale = maximum > 0.0f ? maximum / 127.0f : 1.0f;
         const float inverse = 1.0f / scale;
-        scales[r] = scale;
+        q->scales[r] = scale;
         for (int i = 0; i < in_features; ++i) {
             const float value = bf(row[i]) * inverse;
             const float clamped = fminf(fmaxf(value, -127.0f), 127.0f);
-            quantized[(size_t)r * in_features + i] = (int8_t)lrintf(clamped);
+            q->quantized[(size_t)r * in_features + i] = (int8_t)lrintf(clamped);
         }
     }
+}
+
+/* quantize_weight_rows_kernel, K/int8_gemv.cu:20-52: per row absmax
+ * (max is order independent), scale = amax/127 or 1, value = w * (1/scale),
+ * clamp to +-127, lrintf (round half to even). */
+void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
+                              float* scales, int in_features, int out_features) {
+    QuantCtx q = {weight, quantized, scales, in_features};
+    for_channels(out_features, (size_t)out_features * in_features, quantize_range, &q);
 }
 
 /* One output channel, one activation row, in the reference's exact order
@@ -155,21 +219,37 @@ static float* widen_rows(const uint16_t* input, int rows, int in_features) {
     return x;
 }
 
+typedef struct GemmCtx {
+    const int8_t* weight;
+    const float* scales;
+    const float* x;
+    int in_features, out_features, rows;
+    float* y32;
+    uint16_t* y16;
+    uint16_t* inout;
+} GemmCtx;
+
+static void gemm_range(void* p, int c0, int c1) {
+    const GemmCtx* g = (const GemmCtx*)p;
+    for (int r = 0; r < g->rows; ++r) {
+        for (int c = c0; c < c1; ++c) {
+            const float value = dot_channel_exact(g->weight + (size_t)c * g->in_features,
+                                                  g->x + (size_t)r * g->in_features, g->in_features);
+            const float y = value * g->scales[c];
+            if (g->y32) g->y32[(size_t)r * g->out_features + c] = y;
+            if (g->y16) g->y16[(size_t)r * g->out_features + c] = tobf(y);
+        }
+    }
+}
+
 /* int8_dequant_gemm_kernel<kRows>, K/int8_gemv.cu:58-128: output =
  * bf16(value * scale[c]).  Requires in_features % 16 == 0. */
 void orc_int8_gemm_rows(const int8_t* weight, const float* scales,
                         const uint16_t* input, int in_features,
                         int out_features, int rows, float* y32, uint16_t* y16) {
     float* x = widen_rows(input, rows, in_features);
-    for (int r = 0; r < rows; ++r) {
-        for (int c = 0; c < out_features; ++c) {
-            const float value = dot_channel_exact(weight + (size_t)c * in_features,
-                                                  x + (size_t)r * in_features, in_features);
-            const float y = value * scales[c];
-            if (y32) y32[(size_t)r * out_features + c] = y;
-            if (y16) y16[(size_t)r * out_features + c] = tobf(y);
-        }
-    }
+    GemmCtx g = {weight, scales, x, in_features, out_features, rows, y32, y16, NULL};
+    for_channels(out_features, (size_t)out_features * in_features * rows, gemm_range, &g);
     free(x);
 }
 
@@ -188,6 +268,18 @@ void orc_int8_gemm_rows_f64(const int8_t* weight, const float* scales,
     }
 }
 
+static void gemm_add_range(void* p, int c0, int c1) {
+    const GemmCtx* g = (const GemmCtx*)p;
+    for (int r = 0; r < g->rows; ++r) {
+        for (int c = c0; c < c1; ++c) {
+            const float value = dot_channel_exact(g->weight + (size_t)c * g->in_features,
+                                                  g->x + (size_t)r * g->in_features, g->in_features);
+            const size_t i = (size_t)r * g->out_features + c;
+            g->inout[i] = tobf(fmaf(value, g->scales[c], bf(g->inout[i])));
+        }
+    }
+}
+
 /* int8_dequant_gemm_add_kernel, K/int8_gemv.cu:132-199.  The epilogue
  * `float(out) + value * scale` is contracted to one fma by nvcc's default
  * -fmad=true, so it is restated as fmaf(value, scale, out). */
@@ -195,15 +287,26 @@ void orc_int8_gemm_rows_add(const int8_t* weight, const float* scales,
                             const uint16_t* input, uint16_t* inout,
                             int in_features, int out_features, int rows) {
     float* x = widen_rows(input, rows, in_features);
-    for (int r = 0; r < rows; ++r) {
-        for (int c = 0; c < out_features; ++c) {
-            const float value = dot_channel_exact(weight + (size_t)c * in_features,
-                                                  x + (size_t)r * in_features, in_features);
-            const size_t i = (size_t)r * out_features + c;
-            inout[i] = tobf(fmaf(value, scales[c], bf(inout[i])));
+    GemmCtx g = {weight, scales, x, in_features, out_features, rows, NULL, NULL, inout};
+    for_channels(out_features, (size_t)out_features * in_features * rows, gemm_add_range, &g);
+    free(x);
+}
+
+static void gate_up_range(void* p, int c0, int c1) {
+    const GemmCtx* g = (const GemmCtx*)p;
+    const int in_features = g->in_features, out_features = g->out_features;
+    for (int r = 0; r < g->rows; ++r) {
+        const float* xr = g->x + (size_t)r * in_features;
+        for (int c = c0; c < c1; ++c) {
+            const float gv = dot_channel_exact(g->weight + (size_t)c * in_features, xr, in_features);
+            const float uv = dot_channel_exact(
+                g->weight + ((size_t)out_features + c) * in_features, xr, in_features);
+            const float gate = gv * g->scales[c];
+            const float up = uv * g->scales[out_features + c];
+            const float activated = gate / (1.0f + q3_expf(-gate));
+            g->inout[(size_t)r * out_features + c] = tobf(activated * up);
         }
     }
-    free(x);
 }
 
 /* int8_dequant_gate_up_silu_kernel, K/int8_gemv.cu:206-293: weight is
@@ -212,18 +315,8 @@ void orc_int8_gate_up_silu_rows(const int8_t* weight, const float* scales,
                                 const uint16_t* input, uint16_t* output,
                                 int in_features, int out_features, int rows) {
     float* x = widen_rows(input, rows, in_features);
-    for (int r = 0; r < rows; ++r) {
-        const float* xr = x + (size_t)r * in_features;
-        for (int c = 0; c < out_features; ++c) {
-            const float g = dot_channel_exact(weight + (size_t)c * in_features, xr, in_features);
-            const float u = dot_channel_exact(
-                weight + ((size_t)out_features + c) * in_features, xr, in_features);
-            const float gate = g * scales[c];
-            const float up = u * scales[out_features + c];
-            const float activated = gate / (1.0f + q3_expf(-gate));
-            output[(size_t)r * out_features + c] = tobf(activated * up);
-        }
-    }
+    GemmCtx g = {weight, scales, x, in_features, out_features, rows, NULL, NULL, output};
+    for_channels(out_features, (size_t)2 * out_features * in_features * rows, gate_up_range, &g);
     free(x);
 }
 

@@ -40,6 +40,10 @@ void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
 
 /* y32 (optional) receives value*scale before the bf16 store; y16 (optional)
  * receives the bf16 store.  Both are [rows][out]. */
+/* Threads used by the GEMV restatements for large matrices (default 1);
+ * results do not depend on it. */
+void orc_set_threads(int threads);
+
 void orc_int8_gemm_rows(const int8_t* weight, const float* scales,
                         const uint16_t* input, int in_features,
                         int out_features, int rows, float* y32, uint16_t* y16);

@@ -199,3 +199,9 @@ def expf_array(x):
     out = np.empty_like(x)
     lib().orc_expf_array(_p(x), _p(out), C.c_size_t(x.size))
     return out
+
+
+def set_threads(threads: int) -> None:
+    """Threads for the model-level GEMVs of large matrices (bit-identical
+    results for any count)."""
+    lib().orc_set_threads(int(threads))
