@@ -305,6 +305,15 @@ typedef struct Qwen3TtsModelConfigV1 {
     float rms_epsilon, rope_theta;
 } Qwen3TtsModelConfigV1;
 
+/* Diagnostics (what the reference traces as "final_norm", talker.cu:3484 and
+ * :3230): copies the session's final-normalized talker
+ * hidden state (talker_hidden bf16 values, `bytes` must equal 2 *
+ * talker_hidden) after the last completed prefill or frame to host memory.
+ * Fails with QWEN3_TTS_TALKER_STATUS_STATE while a frame lease is in flight. */
+QWEN3_TTS_API int32_t qwen3_tts_session_read_last_hidden_v1(
+    Qwen3TtsSessionHandle handle, void* destination, uint64_t bytes, char* error,
+    size_t error_capacity);
+
 /* Fills `output` with the VoiceDesign geometry of the reference. */
 QWEN3_TTS_API void qwen3_tts_model_config_default(Qwen3TtsModelConfigV1* output);
 

@@ -808,6 +808,13 @@ static void predictor_position(const OrcModel* m, OrcSession* s, const uint16_t*
     free(hidden);
 }
 
+static void trace(const OrcModel* m, const OrcSession* s, int row) {
+    if (s->trace_logits == NULL) return;
+    const int width = m->talker_vocab > m->predictor_vocab ? m->talker_vocab : m->predictor_vocab;
+    const int vocab = row == 0 ? m->talker_vocab : m->predictor_vocab;
+    memcpy(s->trace_logits + (size_t)row * width, s->logits, (size_t)vocab * 2);
+}
+
 /* begin_frame, K/talker.cu:1095-1244 (single session); with
  * m->batch_semantics one session's row of batch_begin_frames,
  * K/talker.cu:1495-1881 (each row of the lockstep batch is independent). */
@@ -822,6 +829,7 @@ int orc_frame_step(const OrcModel* m, OrcSession* s, int semantic_token,
     predictor_position(m, s, s->last_hidden, 0, -1);
     memcpy(input, m->codec_embedding + (size_t)semantic_token * H, (size_t)H * 2);
     predictor_position(m, s, input, 1, 0);
+    trace(m, s, 1);
     tokens[1] = orc_sample_logits(s->logits, m->predictor_vocab, 0, m->codec_eos, s->history,
                                   s->history_count, ps->do_sample, ps->top_k, ps->top_p,
                                   ps->temperature, ps->repetition_penalty, &s->random_state);
@@ -831,6 +839,7 @@ int orc_frame_step(const OrcModel* m, OrcSession* s, int semantic_token,
             memcpy(input, m->predictor_embeddings[residual - 1] + (size_t)tok * H, (size_t)H * 2);
         }
         predictor_position(m, s, input, residual + 1, residual);
+        trace(m, s, residual + 1);
         tokens[residual + 1] = orc_sample_logits(
             s->logits, m->predictor_vocab, 0, m->codec_eos, s->history, s->history_count,
             ps->do_sample, ps->top_k, ps->top_p, ps->temperature, ps->repetition_penalty,
@@ -848,6 +857,7 @@ int orc_frame_step(const OrcModel* m, OrcSession* s, int semantic_token,
     orc_project_text(m, trailing_text_token, text);
     orc_add_in_place(input, text, H);
     orc_talker_step(m, s, input);
+    trace(m, s, 0);
     s->position += 1;
     const int next = sample_talker(m, s, ts);
     free(input);

@@ -38,12 +38,12 @@ float orc_uniform_random(uint64_t* state);
 void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
                               float* scales, int in_features, int out_features);
 
-/* y32 (optional) receives value*scale before the bf16 store; y16 (optional)
- * receives the bf16 store.  Both are [rows][out]. */
 /* Threads used by the GEMV restatements for large matrices (default 1);
  * results do not depend on it. */
 void orc_set_threads(int threads);
 
+/* y32 (optional) receives value*scale before the bf16 store; y16 (optional)
+ * receives the bf16 store.  Both are [rows][out]. */
 void orc_int8_gemm_rows(const int8_t* weight, const float* scales,
                         const uint16_t* input, int in_features,
                         int out_features, int rows, float* y32, uint16_t* y16);
@@ -140,6 +140,10 @@ typedef struct OrcSession {
     uint16_t* pred_v;
     uint16_t* last_hidden; /* [talker.hidden] (final-normed) */
     uint16_t* logits;      /* [max(talker_vocab, predictor_vocab)] */
+    /* Optional (NULL: off): the logits each sample of orc_frame_step reads,
+     * [16][max(talker_vocab, predictor_vocab)]: row 0 the talker's (raw,
+     * before mask and penalty), rows 1..15 the predictor codebooks'. */
+    uint16_t* trace_logits;
 } OrcSession;
 
 typedef struct OrcSampling {

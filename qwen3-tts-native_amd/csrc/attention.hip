@@ -1,19 +1,20 @@
-// Decode attention over a bf16 KV cache, head dimension 128, as three
-// kernels so that every phase runs on many compute units:
+// Decode attention over a bf16 KV cache, head dimension 128.  Four kernels:
 //
-//   scores   one lane per (row, kv head, position): the key row is read once
-//            and dotted with every query head of the GQA group.
-//   softmax  one block per (row, query head): maximum, exponentials and the
-//            normalizer; writes the probabilities (exact) or the unnormalized
-//            weights plus 1/sum (fast) back over the scores.
-//   values   one wave per (row, kv head, slice of the head dimension): lanes
-//            are (query head of the group, dimension) pairs, each running the
-//            reference's sequential fma chain over positions.  Value rows are
-//            streamed through a 16-deep register ring (16-byte loads, 16 KB
-//            in flight per wave) and transposed through LDS.
-//
-// Caches of at most 64 positions (the code predictor's) run all three phases
-// in one kernel.
+//   scores  (caches > 64 positions) one wave per (64 positions, query head,
+//           row), lane = position: the query head and the new key are
+//           RMSNormed and rotated in-lane, the group's first head appends the
+//           new key and value to the caches, then each lane runs the
+//           reference's dot tree over the 128 dimensions for its position.
+//   head    (caches > 64 positions) one wave per (row, query head, half of
+//           the head dimension), lane = dimension: the softmax of the head's
+//           scores (maximum, exponentials, normalizer) runs under a 16-deep
+//           register ring of 16-byte value loads from the blocked
+//           dimension-major value cache, then each lane runs the reference's
+//           sequential chain over positions.
+//   short   (the code predictor's <= 16 positions) one wave per query head:
+//           append, scores, softmax and values fused, with the QKV epilogue.
+//   small   (other caches <= 64 positions) one block of G*128 threads per
+//           (kv head, row), the phases in one kernel.
 //
 // Two arithmetic variants, each the reference's own operation order:
 //   exact  causal_gqa_attention_kernel (talker_kernels.cu:287-357):

@@ -476,9 +476,13 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     constexpr bool kRowSplit = kNorm && kBlock == 256 && kChunks % 32 == 0 && kChunks / 32 <= 8;
     constexpr int kXPer = kRowSplit ? kChunks / 32 : (8 * kChunks + kBlock - 1) / kBlock;
     static_assert(kXPer <= 12, "x staging holds at most 12 chunks per thread");
+    // Row-split layout: wave w holds rows w and w + 4 (lanes 0-31 and 32-63),
+    // which the statistic fold below relies on (it has no block barrier).
+    static_assert(!kRowSplit || kWaves == 4, "the row-split layout maps rows w and w + 4 to wave w of four");
+    auto split_row = [] { return static_cast<int>(threadIdx.x >> 6) + static_cast<int>((threadIdx.x >> 3) & 4); };
     auto x_slot = [&](int j, int& r, int& c) {
         if constexpr (kRowSplit) {
-            r = (threadIdx.x >> 6) + ((threadIdx.x >> 3) & 4);
+            r = split_row();
             c = (threadIdx.x & 31) + 32 * j;
         } else {
             const int idx = threadIdx.x + j * kBlock;
@@ -567,7 +571,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
         // e = 0..7 (one fma chain over the thread's chunks in order), folded
         // per row in the reference's tree order by the wave that holds the
         // row; then each thread normalizes its chunks from registers.
-        const int r = (threadIdx.x >> 6) + ((threadIdx.x >> 3) & 4);
+        const int r = split_row();
         if (r < rows) {
             float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             auto accumulate = [&](const uint4& v) {

@@ -757,6 +757,18 @@ public:
 
     uint16_t current_semantic() const { return semantic_; }
 
+    // Diagnostics: the talker's final-normalized hidden state (the predictor's
+    // position-0 input and the codec head's input) after the last completed
+    // frame or prefill, copied to host memory.
+    void read_last_hidden(void* destination, uint64_t bytes) {
+        const uint64_t need = static_cast<uint64_t>(cfg_.talker.hidden) * sizeof(bf16_t);
+        if (destination == nullptr || bytes != need) throw std::invalid_argument("last hidden needs talker_hidden bf16 values");
+        if (frame_in_flight_) throw std::runtime_error("a device frame lease is in flight");
+        check_hip(hipSetDevice(device_), "hipSetDevice(read last hidden)");
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize(read last hidden)");
+        check_hip(hipMemcpy(destination, last_hidden_.as<void>(), need, hipMemcpyDeviceToHost), "read last hidden");
+    }
+
     Qwen3TtsTalkerStateInfo state_info() const {
         Qwen3TtsTalkerStateInfo r{};
         r.abi_version = QWEN3_TTS_TALKER_ABI_VERSION;
@@ -1117,14 +1129,20 @@ public:
         layers_ = T.layers + P.layers;
         table_bytes_ = off_codes() + kCapacity * sizeof(void*);
         tables_ = DeviceBuffer(table_bytes_);
-        check_hip(hipHostMalloc(&pinned_, table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
-        std::memset(pinned_, 0, table_bytes_);
+        for (int k = 0; k < kStaging; ++k) {
+            check_hip(hipHostMalloc(&staging_[k], table_bytes_, hipHostMallocDefault), "hipHostMalloc(batch tables)");
+            std::memset(staging_[k], 0, table_bytes_);
+            check_hip(hipEventCreateWithFlags(&staged_[k], hipEventDisableTiming), "hipEventCreate(batch tables)");
+        }
     }
     ~BatchRunner() {
         (void)hipSetDevice(device_);
         if (stream_) (void)hipStreamSynchronize(stream_);
         destroy_graphs();
-        if (pinned_) (void)hipHostFree(pinned_);
+        for (int k = 0; k < kStaging; ++k) {
+            if (staging_[k]) (void)hipHostFree(staging_[k]);
+            if (staged_[k]) (void)hipEventDestroy(staged_[k]);
+        }
         for (hipEvent_t e : join_) if (e) (void)hipEventDestroy(e);
         if (stream_) (void)hipStreamDestroy(stream_);
     }
@@ -1151,40 +1169,39 @@ public:
             c->pending_lease_ = lease;
             c->pending_position_ = static_cast<uint32_t>(c->position_);
         }
+        // The host tables are staged in a ring of pinned buffers: the upload
+        // of an earlier batch may still wait behind its sessions' work, so a
+        // buffer is refilled only after its own upload has completed.
+        current_ = next_staging_;
+        next_staging_ = (next_staging_ + 1) % kStaging;
+        if (staged_used_[current_]) check_hip(hipEventSynchronize(staged_[current_]), "hipEventSynchronize(batch tables)");
         fill_tables(s, n, trailing, tp, pp);
-        std::vector<uint64_t> key;
-        key.push_back(static_cast<uint64_t>(n));
-        for (int i = 0; i < n; ++i) {
-            key.push_back(reinterpret_cast<uint64_t>(s[i]));
-            for (const SamplingParams* q : {&tp[i], &pp[i]}) {
-                uint32_t bits[3];
-                std::memcpy(&bits[0], &q->top_p, 4);
-                std::memcpy(&bits[1], &q->temperature, 4);
-                std::memcpy(&bits[2], &q->penalty, 4);
-                key.push_back((static_cast<uint64_t>(q->do_sample) << 32) | static_cast<uint32_t>(q->top_k));
-                key.push_back((static_cast<uint64_t>(bits[0]) << 32) | bits[1]);
-                key.push_back(bits[2]);
-            }
-        }
+        // A captured frame bakes only the row count, the GEMV mode and the
+        // largest session capacity (attention grid and bound); everything
+        // session-specific reaches the kernels through the tables.  Graph
+        // sets for a few such keys are kept, so batches of different
+        // compositions alternate without re-capture.
+        int max_capacity = kCodebooks;
+        for (int i = 0; i < n; ++i) max_capacity = std::max(max_capacity, s[i]->max_seq_);
+        const GraphKey key{n, batch_gemv_mode(), max_capacity};
         try {
             for (int i = 0; i < n; ++i) {
                 check_hip(hipEventRecord(join_[i], s[i]->stream_), "hipEventRecord(join)");
                 check_hip(hipStreamWaitEvent(stream_, join_[i], 0), "hipStreamWaitEvent(join)");
             }
-            if (key != key_) {
-                destroy_graphs();
-                key_ = key;
-            }
-            check_hip(hipMemcpyAsync(tables_.as<void>(), pinned_, table_bytes_, hipMemcpyHostToDevice, stream_),
+            GraphSet& graphs = graph_set(key);
+            check_hip(hipMemcpyAsync(tables_.as<void>(), staging_[current_], table_bytes_, hipMemcpyHostToDevice, stream_),
                       "upload batch tables");
+            check_hip(hipEventRecord(staged_[current_], stream_), "hipEventRecord(batch tables)");
+            staged_used_[current_] = true;
             for (int i = 0; i < n; ++i) check_hip(hipEventRecord(s[i]->predictor_start_, stream_), "hipEventRecord");
-            run_graph(predictor_graph_, [&] { enqueue_predictor(s, n, pp); });
+            run_graph(graphs, graphs.predictor, [&] { enqueue_predictor(n, key.mode); });
             for (int i = 0; i < n; ++i) {
                 check_hip(hipEventRecord(s[i]->predictor_stop_, stream_), "hipEventRecord");
                 check_hip(hipEventRecord(s[i]->codes_ready_, stream_), "hipEventRecord");
                 check_hip(hipEventRecord(s[i]->start_, stream_), "hipEventRecord");
             }
-            run_graph(talker_graph_, [&] { enqueue_talker(s, n, tp); });
+            run_graph(graphs, graphs.talker, [&] { enqueue_talker(n, key.mode, key.capacity); });
             for (int i = 0; i < n; ++i) {
                 Session* c = s[i];
                 check_hip(hipEventRecord(c->stop_, stream_), "hipEventRecord");
@@ -1198,8 +1215,8 @@ public:
             }
         } catch (...) {
             for (int i = 0; i < n; ++i) s[i]->poison();
-            destroy_graphs();
             (void)hipStreamSynchronize(stream_);
+            destroy_graphs();
             throw;
         }
         for (int i = 0; i < n; ++i) views[i] = s[i]->view(s[i]->pending_lease_);
@@ -1229,7 +1246,7 @@ private:
     template <typename T>
     T* dev_at(size_t offset) const { return reinterpret_cast<T*>(tables_.as<char>() + offset); }
     template <typename T>
-    T* host_at(size_t offset) const { return reinterpret_cast<T*>(static_cast<char*>(pinned_) + offset); }
+    T* host_at(size_t offset) const { return reinterpret_cast<T*>(static_cast<char*>(staging_[current_]) + offset); }
 
     int* positions(int slot) const { return dev_at<int>(0) + slot * kCapacity; }
     bf16_t* const* kv_table(int layer_slot, bool value) const {
@@ -1303,15 +1320,56 @@ private:
         }
     }
 
+    struct GraphKey {
+        int rows, mode, capacity;
+        bool operator==(const GraphKey& o) const { return rows == o.rows && mode == o.mode && capacity == o.capacity; }
+    };
+    struct GraphSet {
+        GraphKey key;
+        hipGraphExec_t predictor = nullptr, talker = nullptr;
+        int uncaptured = 0;  // eager enqueues so far (the first frame runs eagerly)
+        uint64_t last_use = 0;
+    };
+    static constexpr size_t kGraphSets = 4;
+
+    // The graph set of `key`, created on first use; the least recently used
+    // set is evicted when kGraphSets are held (after the stream has drained:
+    // its graphs may still be queued).
+    GraphSet& graph_set(const GraphKey& key) {
+        for (GraphSet& g : graphs_) {
+            if (g.key == key) {
+                g.last_use = ++use_clock_;
+                return g;
+            }
+        }
+        if (graphs_.size() >= kGraphSets) {
+            auto victim = std::min_element(graphs_.begin(), graphs_.end(),
+                                           [](const GraphSet& a, const GraphSet& b) { return a.last_use < b.last_use; });
+            check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize(evict batch graphs)");
+            destroy(*victim);
+            graphs_.erase(victim);
+        }
+        graphs_.push_back(GraphSet{key});
+        graphs_.back().last_use = ++use_clock_;
+        return graphs_.back();
+    }
+
+    static void destroy(GraphSet& g) {
+        for (hipGraphExec_t* e : {&g.predictor, &g.talker}) {
+            if (*e) (void)hipGraphExecDestroy(*e);
+            *e = nullptr;
+        }
+    }
+
     template <typename Enqueue>
-    void run_graph(hipGraphExec_t& exec, Enqueue&& enqueue) {
+    void run_graph(GraphSet& set, hipGraphExec_t& exec, Enqueue&& enqueue) {
         if (exec != nullptr) {
             check_hip(hipGraphLaunch(exec, stream_), "hipGraphLaunch(batch)");
             return;
         }
-        if (uncaptured_ < 2 || !Session::graphs_enabled()) {
+        if (set.uncaptured < 2 || !Session::graphs_enabled()) {
             enqueue();
-            ++uncaptured_;
+            ++set.uncaptured;
             return;
         }
         check_hip(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture(batch)");
@@ -1332,19 +1390,15 @@ private:
     }
 
     void destroy_graphs() {
-        for (hipGraphExec_t* g : {&predictor_graph_, &talker_graph_}) {
-            if (*g) (void)hipGraphExecDestroy(*g);
-            *g = nullptr;
-        }
-        uncaptured_ = 0;
+        for (GraphSet& g : graphs_) destroy(g);
+        graphs_.clear();
     }
 
-    void run_decoder(bool predictor, int n, const int* pos, int capacity) {
+    void run_decoder(bool predictor, int n, int mode, const int* pos, int capacity) {
         const Dims& d = predictor ? cfg_.predictor : cfg_.talker;
         const std::vector<Layer>& layers = predictor ? m_.predictor_layers_ : m_.talker_layers_;
         bf16_t* hidden = predictor ? p_hidden_.as<bf16_t>() : hidden_.as<bf16_t>();
         const int slot0 = predictor ? cfg_.talker.layers : 0;
-        const int mode = batch_gemv_mode();
         for (int l = 0; l < d.layers; ++l) {
             const Layer& L = layers[l];
             Gemv(L.qkv, hidden, d.hidden, d.qkv_width(), kEpiStore).norm(L.input_norm, cfg_.eps).rows(n, mode)
@@ -1364,9 +1418,8 @@ private:
         }
     }
 
-    void enqueue_predictor(Session** s, int n, const std::vector<SamplingParams>& ps) {
+    void enqueue_predictor(int n, int mode) {
         const int H = cfg_.talker.hidden, PH = cfg_.predictor.hidden, PV = cfg_.predictor_vocab;
-        const int mode = batch_gemv_mode();
         bf16_t* input = text_input_.as<bf16_t>();
         for (int p = 0; p < kCodebooks; ++p) {
             if (p == 0) {
@@ -1381,7 +1434,7 @@ private:
             }
             Gemv(m_.small_to_mtp_, input, H, PH, kEpiBias).bias(m_.small_to_mtp_bias_).rows(n, mode)
                 .to(p_hidden_.as<bf16_t>()).run(stream_, "batch small_to_mtp");
-            run_decoder(true, n, positions(p), kCodebooks);
+            run_decoder(true, n, mode, positions(p), kCodebooks);
             if (p >= 1) {
                 Gemv(m_.predictor_heads_[p - 1], p_hidden_.as<bf16_t>(), PH, PV, kEpiStore).norm(m_.predictor_norm_, cfg_.eps)
                     .rows(n, mode).to(logits_.as<bf16_t>()).run(stream_, "batch predictor head");
@@ -1392,11 +1445,8 @@ private:
                   "pack frame codes");
     }
 
-    void enqueue_talker(Session** s, int n, const std::vector<SamplingParams>& ts) {
+    void enqueue_talker(int n, int mode, int max_capacity) {
         const int H = cfg_.talker.hidden, TV = cfg_.talker_vocab;
-        const int mode = batch_gemv_mode();
-        int max_capacity = kCodebooks;
-        for (int i = 0; i < n; ++i) max_capacity = std::max(max_capacity, s[i]->max_seq_);
         check_hip(launch_sum_embeddings_rows(m_.embedding_tables_.as<const bf16_t*>(), kCodebooks, TV, cfg_.predictor_vocab, H,
                                              token_bases(), hidden_.as<bf16_t>(), n, stream_),
                   "batch codec embeddings");
@@ -1407,7 +1457,7 @@ private:
             .to(proj_.as<bf16_t>()).run(stream_, "batch text fc1");
         Gemv(m_.text_fc2_, proj_.as<bf16_t>(), H, H, kEpiBiasAdd).bias(m_.text_fc2_bias_).rows(n, mode)
             .to(hidden_.as<bf16_t>()).run(stream_, "batch text fc2");
-        run_decoder(false, n, positions(kCodebooks), max_capacity);
+        run_decoder(false, n, mode, positions(kCodebooks), max_capacity);
         check_hip(launch_rms_norm_rows(hidden_.as<bf16_t>(), m_.talker_norm_, normalized_.as<bf16_t>(), n, H, cfg_.eps, stream_),
                   "batch talker final norm");
         check_hip(launch_scatter_rows(normalized_.as<bf16_t>(), last_hidden_ptrs(), n, H, stream_), "scatter last hidden");
@@ -1425,10 +1475,13 @@ private:
     std::array<hipEvent_t, kCapacity> join_{};
     DeviceBuffer hidden_, normalized_, p_hidden_, text_input_, proj_, qkv_, attn_, attn_scratch_, act_, logits_, tables_;
     size_t table_bytes_ = 0;
-    void* pinned_ = nullptr;
-    hipGraphExec_t predictor_graph_ = nullptr, talker_graph_ = nullptr;
-    int uncaptured_ = 0;
-    std::vector<uint64_t> key_;
+    static constexpr int kStaging = 2;
+    void* staging_[kStaging] = {};
+    hipEvent_t staged_[kStaging] = {};
+    bool staged_used_[kStaging] = {};
+    int current_ = 0, next_staging_ = 0;
+    std::vector<GraphSet> graphs_;
+    uint64_t use_clock_ = 0;
 };
 
 void delete_batch_runner(BatchRunner* r) { delete r; }
@@ -1614,6 +1667,12 @@ QWEN3_TTS_API int32_t qwen3_tts_session_state_info(Qwen3TtsSessionHandle handle,
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
     }
     return protect([&] { *output = session_of(handle)->state_info(); }, QWEN3_TTS_TALKER_STATUS_STATE, error, cap);
+}
+
+QWEN3_TTS_API int32_t qwen3_tts_session_read_last_hidden_v1(Qwen3TtsSessionHandle handle, void* destination,
+                                                            uint64_t bytes, char* error, size_t cap) {
+    return protect([&] { session_of(handle)->read_last_hidden(destination, bytes); }, QWEN3_TTS_TALKER_STATUS_STATE,
+                   error, cap);
 }
 
 }  // extern "C"

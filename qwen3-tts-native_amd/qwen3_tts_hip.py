@@ -188,6 +188,7 @@ SIGNATURES = {
                                                         C.POINTER(SamplingConfig), C.POINTER(SamplingConfig),
                                                         C.POINTER(DeviceFrameViewV2)] + ERR),
     "qwen3_tts_session_state_info": (I32, [P, C.POINTER(TalkerStateInfo)] + ERR),
+    "qwen3_tts_session_read_last_hidden_v1": (I32, [P, P, U64] + ERR),
     # additive exports
     "qwen3_tts_model_config_default": (None, [C.POINTER(ModelConfigV1)]),
     "qwen3_tts_model_create_with_config": (I32, [I32, C.POINTER(ModelConfigV1), C.POINTER(P)] + ERR),

@@ -9,6 +9,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+import gen
 import toy_model
 from toy_model import TOY
 
@@ -156,35 +157,221 @@ def test_batched_then_single_frame(hip, orc, toy, monkeypatch):
             lib.qwen3_tts_session_destroy(s)
 
 
-def test_batched_frames_mfma_mode(hip, orc, toy, monkeypatch):
+# The MFMA batch GEMV sums in another order than the reference's kernel, so a
+# fp32 dot product may differ in its last bits (within rel 1e-3 / abs 1e-2,
+# test_gemv_gpu.py) and an occasional bf16 store rounds the other way.  Such
+# one-ulp flips propagate through the frame; measured on this toy model (N =
+# 2, 4, 8, four frames) the final hidden state differs by at most 0.0044 of
+# its largest value (about one bf16 ulp there) and every greedy token agreed.
+# The bar: the last hidden within
+# HIDDEN_TOL of the oracle's (batch semantics), and every greedy token
+# identical wherever the oracle's top-2 margin exceeds LOGIT_TOL; a session
+# whose token legitimately differs (margin below LOGIT_TOL) leaves lockstep
+# with the oracle and is not compared further.
+HIDDEN_TOL = 2 ** -6  # of max |hidden|: four bf16 ulps at the largest value
+LOGIT_TOL = 2 ** -5  # of max |logit|: eight bf16 ulps at the largest value
+
+
+def read_last_hidden(hip, session, width):
+    out = np.zeros(width, np.uint16)
+    hip.call("qwen3_tts_session_read_last_hidden_v1", session, out.ctypes.data, out.nbytes)
+    return out
+
+
+def token_agrees(gpu, ref, scores, what):
+    """True if identical; False (diverged) if they differ within the margin
+    bound; raises if they differ by more."""
+    if gpu == ref:
+        return True
+    finite = scores[np.isfinite(scores)]
+    tol = LOGIT_TOL * np.max(np.abs(finite))
+    assert scores[ref] - scores[gpu] <= tol, f"{what}: gpu {gpu}, oracle {ref}, margin {scores[ref] - scores[gpu]:.4g} > {tol:.4g}"
+    return False
+
+
+def talker_scores(logits, history, penalty):
+    s = logits.astype(np.float64)
+    mask = np.arange(len(s)) >= 2048
+    mask[TOY["codec_eos_token"]] = False
+    s[mask] = -np.inf
+    if penalty != 1.0 and len(history):
+        idx = np.unique(history)
+        s[idx] = np.where(s[idx] < 0, s[idx] * penalty, s[idx] / penalty)
+    return s
+
+
+@pytest.mark.parametrize("n", [2, 4, 8])
+def test_batched_frames_mfma_mode(hip, orc, toy, monkeypatch, n):
     monkeypatch.delenv("QWEN3_TTS_BATCH_GEMV", raising=False)
     model, om = toy
-    n = 4
     sessions, oracles, sems, lib = make_sessions(hip, model, om, n, GREEDY)
-    agree = total = 0
+    tracked = set(range(n))
+    compared = worst_h = 0
+    pv = TOY["predictor_vocabulary"]
     try:
         for f in range(4):
             live = [i for i in range(n) if sems[i] != TOY["codec_eos_token"]]
             if not live:
                 break
-            res = batch_frame(hip, model, [sessions[i] for i in live], [3] * len(live), GREEDY, GREEDY)
+            res = batch_frame(hip, model, [sessions[i] for i in live], [3 + i for i in live], GREEDY, GREEDY)
             om.model.batch_semantics = 1
             for k, i in enumerate(live):
                 codes, nxt, info = res[k]
-                assert np.all(codes[1:] < 2048) and (nxt < 2048 or nxt == TOY["codec_eos_token"])
                 assert info.predictor_gpu_milliseconds > 0
-                if f == 0:
-                    ocodes, onxt = oracles[i].frame(sems[i], 3, GREEDY, GREEDY)
-                    agree += int(np.sum(codes == ocodes))
-                    total += 16
+                if i in tracked:
+                    o = oracles[i]
+                    ocodes, onxt = o.frame(sems[i], 3 + i, GREEDY, GREEDY)
+                    trace = gen.f32(o.bufs["trace"])
+                    same = codes[0] == ocodes[0]
+                    for r in range(1, 16):
+                        if not same:
+                            break
+                        same = token_agrees(int(codes[r]), int(ocodes[r]), trace[r, :pv], f"frame {f} session {i} codebook {r}")
+                    if same:
+                        hist = o.bufs["history"][:o.s.history_count - 1]
+                        same = token_agrees(nxt, onxt, talker_scores(trace[0, :TOY["talker_vocabulary"]], hist, GREEDY[4]),
+                                            f"frame {f} session {i} next token")
+                    if same:
+                        h = gen.f32(read_last_hidden(hip, sessions[i], TOY["talker_hidden"]))
+                        ref = gen.f32(o.bufs["last"])
+                        err = np.max(np.abs(h - ref)) / np.max(np.abs(ref))
+                        worst_h = max(worst_h, err)
+                        assert err <= HIDDEN_TOL, f"frame {f} session {i}: last hidden off by {err:.4g} of max"
+                        compared += 1
+                    else:
+                        tracked.discard(i)
                 sems[i] = nxt
-        # MFMA sums in a different order than the reference: greedy tokens
-        # agree except where two logits are within an fp32 rounding of a tie
-        assert agree >= 0.75 * total, (agree, total)
+        print(f"n={n}: {compared} session-frames compared, worst last-hidden error {worst_h:.3g} of max")
+        # not vacuous: most session-frames stayed in lockstep with the oracle
+        assert compared >= 0.75 * 4 * n
     finally:
         om.model.batch_semantics = 0
         for s in sessions:
             lib.qwen3_tts_session_destroy(s)
+
+
+def begin_batch(hip, model, sessions, trailing, ts, ps):
+    n = len(sessions)
+    arr = (C.c_void_p * n)(*[s.value for s in sessions])
+    tr = (C.c_int32 * n)(*trailing)
+    tsa = (hip.SamplingConfig * n)(*[hip.SamplingConfig(*ts)] * n)
+    psa = (hip.SamplingConfig * n)(*[hip.SamplingConfig(*ps)] * n)
+    views = (hip.DeviceFrameViewV2 * n)()
+    for v in views:
+        v.struct_size = C.sizeof(hip.DeviceFrameViewV2)
+    hip.call("qwen3_tts_model_batch_next_frame_begin_v2", model, arr, n, tr, tsa, psa, views)
+    return views
+
+
+def finish_batch(hip, sessions, views):
+    out = []
+    for s, v in zip(sessions, views):
+        nxt = C.c_uint16()
+        info = hip.CodecFrameInfo()
+        hip.call("qwen3_tts_session_next_frame_finish_v2", s, v.lease_id, None, C.byref(nxt), C.byref(info))
+        codes = np.zeros(16, np.uint16)
+        hip.call("qwen3_tts_device_memcpy", codes.ctypes.data, v.device_codes, 32)
+        out.append((codes, nxt.value))
+    return out
+
+
+def test_two_batches_in_flight(hip, orc, toy, monkeypatch):
+    """Two disjoint batches begun back to back, then both finished: each runs
+    with its own tables (the second begin must not overwrite the first
+    batch's staged tables while their upload is still queued)."""
+    monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
+    model, om = toy
+    sessions, oracles, sems, lib = make_sessions(hip, model, om, 5, GREEDY)
+    try:
+        for f in range(3):
+            if any(t == TOY["codec_eos_token"] for t in sems):
+                break
+            first, second = [0, 1, 2], [3, 4]
+            v1 = begin_batch(hip, model, [sessions[i] for i in first], [f + i for i in first], GREEDY, GREEDY)
+            v2 = begin_batch(hip, model, [sessions[i] for i in second], [f + i for i in second], GREEDY, GREEDY)
+            r2 = finish_batch(hip, [sessions[i] for i in second], v2)
+            r1 = finish_batch(hip, [sessions[i] for i in first], v1)
+            om.model.batch_semantics = 1
+            for group, res in ((first, r1), (second, r2)):
+                for k, i in enumerate(group):
+                    ocodes, onxt = oracles[i].frame(sems[i], f + i, GREEDY, GREEDY)
+                    assert np.array_equal(res[k][0], ocodes), (f, i)
+                    assert res[k][1] == onxt
+                    sems[i] = onxt
+    finally:
+        om.model.batch_semantics = 0
+        for s in sessions:
+            lib.qwen3_tts_session_destroy(s)
+
+
+def test_alternating_batch_sizes(hip, orc, toy, monkeypatch):
+    """Batches of 8 and of 1 alternate (graph sets for both stay cached; the
+    code-row pointers past the batch's size are stale and must not be used),
+    each session's device codes checked against the oracle."""
+    monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
+    model, om = toy
+    sessions, oracles, sems, lib = make_sessions(hip, model, om, 8, GREEDY)
+    try:
+        for f, members in enumerate([range(8), [5], range(8), [2], range(8), [0]]):
+            members = [i for i in members if sems[i] != TOY["codec_eos_token"]]
+            if not members:
+                continue
+            views = begin_batch(hip, model, [sessions[i] for i in members], [f] * len(members), GREEDY, GREEDY)
+            res = finish_batch(hip, [sessions[i] for i in members], views)
+            om.model.batch_semantics = 1
+            for k, i in enumerate(members):
+                ocodes, onxt = oracles[i].frame(sems[i], f, GREEDY, GREEDY)
+                assert np.array_equal(res[k][0], ocodes), (f, i)
+                assert res[k][1] == onxt
+                sems[i] = onxt
+    finally:
+        om.model.batch_semantics = 0
+        for s in sessions:
+            lib.qwen3_tts_session_destroy(s)
+
+
+def test_new_session_with_larger_capacity_after_graph_capture(hip, orc, toy, monkeypatch):
+    """A batch graph captured for sessions of capacity 64 must not be replayed
+    for a later session of capacity 200 (created, possibly at the same
+    address, after the first is destroyed) whose positions pass 64."""
+    monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
+    model, om = toy
+    lib = hip.load()
+    sessions, oracles, sems, _ = make_sessions(hip, model, om, 1, GREEDY, max_seq=64)
+    for f in range(4):  # frames 3+ replay the captured graph
+        if sems[0] == TOY["codec_eos_token"]:
+            break
+        views = begin_batch(hip, model, sessions, [f], GREEDY, GREEDY)
+        sems[0] = finish_batch(hip, sessions, views)[0][1]
+    lib.qwen3_tts_session_destroy(sessions[0])
+    s = C.c_void_p()
+    mem = hip.SessionMemory()
+    hip.call("qwen3_tts_session_create", model, 200, 9, C.byref(s), C.byref(mem))
+    try:
+        rng = np.random.default_rng(90)
+        count = 70
+        text = rng.integers(0, TOY["text_vocabulary"], count).astype(np.int32)
+        codec = rng.integers(0, 2048, count).astype(np.int32)
+        pre = hip.PrefillResult()
+        hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                 codec.ctypes.data_as(C.POINTER(C.c_int32)), count, hip.SamplingConfig(*GREEDY), C.byref(pre))
+        o = toy_model.OracleSession(om, 200, 9)
+        om.model.batch_semantics = 0
+        sem = o.prefill(text, codec, GREEDY)
+        assert sem == pre.first_semantic_token
+        om.model.batch_semantics = 1
+        for f in range(4):
+            if sem == TOY["codec_eos_token"]:
+                break
+            views = begin_batch(hip, model, [s], [f], GREEDY, GREEDY)
+            codes, nxt = finish_batch(hip, [s], views)[0]
+            ocodes, onxt = o.frame(sem, f, GREEDY, GREEDY)
+            assert np.array_equal(codes, ocodes), f
+            assert nxt == onxt
+            sem = onxt
+    finally:
+        om.model.batch_semantics = 0
+        lib.qwen3_tts_session_destroy(s)
 
 
 def test_batch_argument_errors(hip, toy):

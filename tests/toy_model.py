@@ -129,7 +129,7 @@ class OrcSession(C.Structure):
     _fields_ = [("max_seq", C.c_int), ("position", C.c_int), ("history_count", C.c_int),
                 ("history", C.c_void_p), ("random_state", C.c_uint64), ("talker_k", C.c_void_p),
                 ("talker_v", C.c_void_p), ("pred_k", C.c_void_p), ("pred_v", C.c_void_p),
-                ("last_hidden", C.c_void_p), ("logits", C.c_void_p)]
+                ("last_hidden", C.c_void_p), ("logits", C.c_void_p), ("trace_logits", C.c_void_p)]
 
 
 class OrcSampling(C.Structure):
@@ -227,13 +227,15 @@ class OracleSession:
             pk=np.zeros(c["predictor_layers"] * 16 * pkv, np.uint16),
             pv=np.zeros(c["predictor_layers"] * 16 * pkv, np.uint16),
             last=np.zeros(c["talker_hidden"], np.uint16),
-            logits=np.zeros(max(c["talker_vocabulary"], c["predictor_vocabulary"]), np.uint16))
+            logits=np.zeros(max(c["talker_vocabulary"], c["predictor_vocabulary"]), np.uint16),
+            trace=np.zeros((16, max(c["talker_vocabulary"], c["predictor_vocabulary"])), np.uint16))
         s = OrcSession()
         s.max_seq, s.position, s.history_count = max_seq, 0, 0
         s.random_state = seed if seed != 0 else 0x9E3779B97F4A7C15
         b = self.bufs
         s.history, s.talker_k, s.talker_v = _ptr(b["history"]), _ptr(b["tk"]), _ptr(b["tv"])
         s.pred_k, s.pred_v, s.last_hidden, s.logits = _ptr(b["pk"]), _ptr(b["pv"]), _ptr(b["last"]), _ptr(b["logits"])
+        s.trace_logits = _ptr(b["trace"])
         self.s = s
 
     def prefill(self, text, codec, sampling):
