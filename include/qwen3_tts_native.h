@@ -409,6 +409,22 @@ QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention(
     uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
     int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
     int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
+/* The same fused decode step without any device allocation (no counterpart
+ * in the reference: for callers that cannot call hipMalloc -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).  The
+ * score workspace and the value temporary live in a static per-device
+ * scratch of 32 MiB held until the process ends; calls needing more (roughly
+ * rows * (4 * query_heads + 2 * key_value_heads * 128) * max_sequence_length
+ * bytes) fail with QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT.  Every call on a
+ * device shares that device's scratch: calls that overlap on one device
+ * (different streams, or different threads) race and must be serialized by
+ * the caller.  Results are identical to qwen3_tts_op_decode_attention. */
+QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention_noalloc_v1(
+    int32_t exact, const uint16_t* qkv, int32_t qkv_stride, const uint16_t* q_norm,
+    const uint16_t* k_norm, const uint16_t* rope_table, float epsilon, uint16_t* const* key_bases,
+    uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
+    int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
+    int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
 QWEN3_TTS_API int32_t qwen3_tts_op_kv_scatter_rows(
     const uint16_t* rows_data, uint16_t* const* cache_bases, const int32_t* positions,
     int32_t rows, int32_t width, int32_t row_stride, void* stream, char* error,

@@ -6,6 +6,8 @@
 // this build's own (wave64 reductions, one wave per head, device-resident
 // positions so a frame can be replayed as a hipGraph).
 #include <algorithm>
+#include <mutex>
+
 #include "q3_common.hpp"
 #include "q3_math.h"
 #include "head_device.hpp"
@@ -359,21 +361,34 @@ struct ValueTemporary {
     int stride = 0;
 };
 
-hipError_t make_value_temporary(ValueTemporary& t, bf16_t* const* value_bases, const bf16_t* value_cache,
-                                const int* positions, int fixed_length, int rows, int kv_width, int capacity,
-                                hipStream_t stream) {
+size_t value_temporary_bytes(int rows, int kv_width, int capacity) {
+    const size_t table_bytes = (static_cast<size_t>(rows) * sizeof(bf16_t*) + 255) / 256 * 256;
+    return table_bytes + static_cast<size_t>(rows) * kv_width * value_cache_stride(capacity) * sizeof(bf16_t);
+}
+
+// Lays the temporary out in `memory` (value_temporary_bytes of it) and fills
+// it: a table of per-row pointers, then each row's values dimension-major.
+hipError_t fill_value_temporary(ValueTemporary& t, void* memory, bf16_t* const* value_bases,
+                                const bf16_t* value_cache, const int* positions, int fixed_length, int rows,
+                                int kv_width, int capacity, hipStream_t stream) {
     t.stride = value_cache_stride(capacity);
     const size_t table_bytes = (static_cast<size_t>(rows) * sizeof(bf16_t*) + 255) / 256 * 256;
-    const size_t value_bytes = static_cast<size_t>(rows) * kv_width * t.stride * sizeof(bf16_t);
-    hipError_t st = hipMallocAsync(&t.memory, table_bytes + value_bytes, stream);
-    if (st != hipSuccess) return st;
-    t.table = static_cast<bf16_t**>(t.memory);
-    t.values = reinterpret_cast<bf16_t*>(static_cast<char*>(t.memory) + table_bytes);
+    t.table = static_cast<bf16_t**>(memory);
+    t.values = reinterpret_cast<bf16_t*>(static_cast<char*>(memory) + table_bytes);
     const size_t per_row = static_cast<size_t>(kv_width) * t.stride;
     const int blocks = static_cast<int>(std::min<size_t>((per_row + 255) / 256, 1024));
     values_to_dimension_major_kernel<<<dim3(blocks, rows), 256, 0, stream>>>(
         value_bases, value_cache, positions, fixed_length, kv_width, t.stride, t.values, t.table);
     return hipGetLastError();
+}
+
+hipError_t make_value_temporary(ValueTemporary& t, bf16_t* const* value_bases, const bf16_t* value_cache,
+                                const int* positions, int fixed_length, int rows, int kv_width, int capacity,
+                                hipStream_t stream) {
+    hipError_t st = hipMallocAsync(&t.memory, value_temporary_bytes(rows, kv_width, capacity), stream);
+    if (st != hipSuccess) return st;
+    return fill_value_temporary(t, t.memory, value_bases, value_cache, positions, fixed_length, rows, kv_width,
+                                capacity, stream);
 }
 
 hipError_t free_value_temporary(ValueTemporary& t, hipStream_t stream, hipError_t st) {
@@ -439,37 +454,123 @@ hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride
                                     max_sequence_length, stream);
 }
 
-hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
-                                      const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
-                                      bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
-                                      bf16_t* output, int rows, int query_heads, int key_value_heads,
-                                      int head_dimension, int max_sequence_length, hipStream_t stream) {
-    if (rows <= 0 || query_heads <= 0 || max_sequence_length <= 0 || key_bases == nullptr ||
-        value_bases == nullptr) {
-        return hipErrorInvalidValue;
-    }
-    if (key_value_heads <= 0 || head_dimension != 128 || positions == nullptr) return hipErrorInvalidValue;
-    void* workspace = nullptr;
-    hipError_t st =
-        hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, max_sequence_length), stream);
-    if (st != hipSuccess) return st;
+// File-scope scratch of the allocation-free decode attention entry point:
+// each device holds its own copy for the life of the process.  In host code
+// the name is only a stand-in; the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+constexpr size_t kNoAllocScratchBytes = size_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+bool decode_attention_args_ok(int rows, int query_heads, int key_value_heads, int head_dimension,
+                              int max_sequence_length, bf16_t* const* key_bases, bf16_t* const* value_bases,
+                              const int* positions) {
+    return rows > 0 && query_heads > 0 && max_sequence_length > 0 && key_bases != nullptr && value_bases != nullptr &&
+           key_value_heads > 0 && head_dimension == 128 && positions != nullptr;
+}
+
+size_t aligned256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// The fused decode step on caller-provided scratch memory: the score
+// workspace, then the dimension-major value temporary.  Nothing in it needs
+// to start at zero (every element is written before it is read).
+hipError_t decode_attention_in(void* scratch, bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                               const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                               bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
+                               bf16_t* output, int rows, int query_heads, int key_value_heads, int head_dimension,
+                               int max_sequence_length, hipStream_t stream) {
     const int kv_width = key_value_heads * head_dimension;
+    float* workspace = static_cast<float*>(scratch);
+    void* temporary =
+        static_cast<char*>(scratch) + aligned256(attention_workspace_bytes(rows, query_heads, max_sequence_length));
     ValueTemporary values;
-    st = make_value_temporary(values, value_bases, nullptr, positions, 0, rows, kv_width, max_sequence_length, stream);
+    hipError_t st = fill_value_temporary(values, temporary, value_bases, nullptr, positions, 0, rows, kv_width,
+                                         max_sequence_length, stream);
     if (st == hipSuccess) {
         st = launch_decode_attention(exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
                                      values.table, nullptr, nullptr, positions, output, rows, query_heads,
-                                     key_value_heads, head_dimension, max_sequence_length,
-                                     static_cast<float*>(workspace), nullptr, stream);
+                                     key_value_heads, head_dimension, max_sequence_length, workspace, nullptr, stream);
     }
     if (st == hipSuccess) {
         appended_value_back_kernel<<<dim3((kv_width + 255) / 256, rows), 256, 0, stream>>>(
             value_bases, positions, kv_width, values.stride, values.values);
         st = hipGetLastError();
     }
-    st = free_value_temporary(values, stream, st);
-    const hipError_t freed = hipFreeAsync(workspace, stream);
+    return st;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_address[kMaxDevices] = {};
+
+hipError_t scratch_for_current_device(void** out) {
+    int device = 0;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) return st;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_address[device] == nullptr) {
+        void* ptr = nullptr;
+        st = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (st != hipSuccess) return st;
+        scratch_address[device] = ptr;
+    }
+    *out = scratch_address[device];
+    return hipSuccess;
+}
+
+}  // namespace
+
+size_t decode_attention_scratch_bytes(int rows, int query_heads, int key_value_heads, int head_dimension,
+                                      int max_sequence_length) {
+    return aligned256(attention_workspace_bytes(rows, query_heads, max_sequence_length)) +
+           value_temporary_bytes(rows, key_value_heads * head_dimension, max_sequence_length);
+}
+
+size_t decode_attention_scratch_limit() { return kNoAllocScratchBytes; }
+
+hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                      const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                      bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
+                                      bf16_t* output, int rows, int query_heads, int key_value_heads,
+                                      int head_dimension, int max_sequence_length, hipStream_t stream) {
+    if (!decode_attention_args_ok(rows, query_heads, key_value_heads, head_dimension, max_sequence_length, key_bases,
+                                  value_bases, positions)) {
+        return hipErrorInvalidValue;
+    }
+    void* memory = nullptr;
+    hipError_t st = hipMallocAsync(
+        &memory, decode_attention_scratch_bytes(rows, query_heads, key_value_heads, head_dimension, max_sequence_length),
+        stream);
+    if (st != hipSuccess) return st;
+    st = decode_attention_in(memory, exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
+                             value_bases, positions, output, rows, query_heads, key_value_heads, head_dimension,
+                             max_sequence_length, stream);
+    const hipError_t freed = hipFreeAsync(memory, stream);
     return st != hipSuccess ? st : freed;
+}
+
+hipError_t launch_decode_attention_op_noalloc(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                              const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                              bf16_t* const* key_bases, bf16_t* const* value_bases,
+                                              const int* positions, bf16_t* output, int rows, int query_heads,
+                                              int key_value_heads, int head_dimension, int max_sequence_length,
+                                              hipStream_t stream) {
+    if (!decode_attention_args_ok(rows, query_heads, key_value_heads, head_dimension, max_sequence_length, key_bases,
+                                  value_bases, positions)) {
+        return hipErrorInvalidValue;
+    }
+    if (decode_attention_scratch_bytes(rows, query_heads, key_value_heads, head_dimension, max_sequence_length) >
+        kNoAllocScratchBytes) {
+        return hipErrorInvalidValue;
+    }
+    void* memory = nullptr;
+    const hipError_t st = scratch_for_current_device(&memory);
+    if (st != hipSuccess) return st;
+    return decode_attention_in(memory, exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
+                               value_bases, positions, output, rows, query_heads, key_value_heads, head_dimension,
+                               max_sequence_length, stream);
 }
 
 hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,

@@ -261,6 +261,18 @@ hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_str
                                       bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,
                                       bf16_t* output, int rows, int query_heads, int key_value_heads,
                                       int head_dimension, int max_sequence_length, hipStream_t stream);
+// The same on the library's per-device static scratch (no allocation); fails
+// with hipErrorInvalidValue when decode_attention_scratch_bytes exceeds
+// decode_attention_scratch_limit().
+hipError_t launch_decode_attention_op_noalloc(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
+                                              const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
+                                              bf16_t* const* key_bases, bf16_t* const* value_bases,
+                                              const int* positions, bf16_t* output, int rows, int query_heads,
+                                              int key_value_heads, int head_dimension, int max_sequence_length,
+                                              hipStream_t stream);
+size_t decode_attention_scratch_bytes(int rows, int query_heads, int key_value_heads, int head_dimension,
+                                      int max_sequence_length);
+size_t decode_attention_scratch_limit();
 hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride, bf16_t* const* key_bases,
                                bf16_t* const* value_bases, const int* positions, bf16_t* output, int rows,
                                int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,

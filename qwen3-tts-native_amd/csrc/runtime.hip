@@ -688,6 +688,28 @@ QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention(int32_t exact, const uint16_
                          "decode attention", error, cap);
 }
 
+QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention_noalloc_v1(
+    int32_t exact, const uint16_t* qkv, int32_t qkv_stride, const uint16_t* q_norm, const uint16_t* k_norm,
+    const uint16_t* rope_table, float epsilon, uint16_t* const* key_bases, uint16_t* const* value_bases,
+    const int32_t* positions, uint16_t* output, int32_t rows, int32_t qh, int32_t kvh, int32_t hd, int32_t max_seq,
+    void* stream, char* error, size_t cap) {
+    if (rows > 0 && qh > 0 && kvh > 0 && hd > 0 && max_seq > 0) {
+        const size_t need = decode_attention_scratch_bytes(rows, qh, kvh, hd, max_seq);
+        if (need > decode_attention_scratch_limit()) {
+            char message[160];
+            std::snprintf(message, sizeof(message),
+                          "decode attention needs %zu bytes of scratch; the allocation-free entry point holds %zu",
+                          need, decode_attention_scratch_limit());
+            write_error(error, cap, message);
+            return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
+        }
+    }
+    return launch_status(launch_decode_attention_op_noalloc(exact != 0, qkv, qkv_stride, q_norm, k_norm, rope_table,
+                                                            epsilon, key_bases, value_bases, positions, output, rows,
+                                                            qh, kvh, hd, max_seq, as_stream(stream)),
+                         "decode attention (no allocation)", error, cap);
+}
+
 QWEN3_TTS_API int32_t qwen3_tts_op_kv_scatter_rows(const uint16_t* rows_data, uint16_t* const* cache_bases,
                                                    const int32_t* positions, int32_t rows, int32_t width,
                                                    int32_t row_stride, void* stream, char* error, size_t cap) {

@@ -203,6 +203,8 @@ SIGNATURES = {
     "qwen3_tts_op_attention": (I32, [I32, P, I32, P, P, P, P, I32, I32, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_decode_attention": (I32, [I32, P, I32, P, P, P, C.c_float, P, P, P, P, I32, I32, I32, I32, I32, P]
                                       + ERR),
+    "qwen3_tts_op_decode_attention_noalloc_v1": (I32, [I32, P, I32, P, P, P, C.c_float, P, P, P, P, I32, I32, I32,
+                                                        I32, I32, P] + ERR),
     "qwen3_tts_op_kv_scatter_rows": (I32, [P, P, P, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_elementwise": (I32, [I32, P, P, I32, I32, P] + ERR),
     "qwen3_tts_op_sample_logits": (I32, [P, I32, I32, I32, P, P, SamplingConfig, P, P, P] + ERR),
