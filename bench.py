@@ -86,14 +86,16 @@ def batched(hip, steps: int, warmup: int):
     return result
 
 
-def cpu_baseline(seconds: float = 10.0):
-    """Oracle exact-order int8 GEMV chain on the host cores (bounded sample)."""
+def cpu_baseline(seconds: float = 8.0):
+    """Oracle exact-order int8 GEMV chain on the host cores (bounded sample):
+    once on every core this process may run on (its CPU affinity set, the
+    box's share of the host), once on one thread."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     rng = np.random.default_rng(0)
     sample_layers = 2
     mats = []
@@ -104,22 +106,31 @@ def cpu_baseline(seconds: float = 10.0):
             x = oracle.f32_to_bf16(rng.standard_normal(in_f).astype(np.float32))
             mats.append((w, s, x))
     per_layer = sum(w.nbytes + 4 * w.shape[0] + 2 * w.shape[1] + 2 * w.shape[0] for w, _, _ in mats) / sample_layers
-    t0 = time.perf_counter()
-    layers_done = 0
-    while True:
-        for w, s, x in mats:
-            oracle.int8_gemm_rows_mt(w, s, x, threads)
-        layers_done += sample_layers
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
+
+    def timed(n_threads, budget):
+        t0 = time.perf_counter()
+        layers_done = 0
+        while True:
+            for w, s, x in mats:
+                oracle.int8_gemm_rows_mt(w, s, x, n_threads)
+            layers_done += sample_layers
+            if time.perf_counter() - t0 >= budget:
+                break
+        dt = time.perf_counter() - t0
+        return per_layer * layers_done / dt / 1e9, layers_done, dt
+
+    gbs, layers_done, dt = timed(threads, seconds)
+    gbs1, layers1, dt1 = timed(1, seconds)
     return {
-        "value": round(per_layer * layers_done / dt / 1e9, 3),
+        "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": f"{layers_done} talker-layer GEMV chains (QKV, O, gate+up, down; {sample_layers} distinct "
-                  f"layers cycled) in {dt:.1f} s with the oracle's exact-order int8 GEMV on {threads} threads",
+                  f"layers cycled) in {dt:.1f} s with the oracle's exact-order int8 GEMV on {threads} threads "
+                  f"(every core of this process's CPU affinity set; the host reports {os.cpu_count()})",
+        "one_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                       "sample": f"{layers1} talker-layer GEMV chains in {dt1:.1f} s on one thread"},
     }
 
 
@@ -391,6 +402,9 @@ def main() -> int:
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel's workload (the 28 gate/up GEMVs of a step) and a "
                          "256 MiB device-to-device copy that calibrates the HBM byte counters; for rocprofv3 --pmc")
+    ap.add_argument("--only-batched-gemv", action="store_true",
+                    help="run only config 4's MFMA GEMVs (N = 2, 4, 8; gate+up and down, 28 distinct layers); "
+                         "for rocprofv3 --pmc")
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
@@ -402,6 +416,9 @@ def main() -> int:
     import qwen3_tts_hip as hip
 
     hip.load()
+    if args.only_batched_gemv:
+        print(json.dumps({"batched_config4": batched(hip, args.steps, args.warmup)}), flush=True)
+        return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
         return 0
@@ -445,12 +462,14 @@ def main() -> int:
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+                     "traffic_source": "recorded rocprofv3 PMC passes of this kernel "
+                                       "(profiles/gemv_gate_up_hbm_traffic_pmc.md), not measured in this run",
                      "kernel": "gemv_exact_fixed<4, SiluRounded, norm> (gate+up 12288x2048)",
                      "bytes_per_launch": int(launch_bytes), "us_per_launch": round(launch_us, 3)},
     }
     # The launch-shape ceiling: the same 112 launches (same weight bytes,
     # same graph) as plain 16-byte reads with no GEMV arithmetic.
-    ceiling = step_benchmark(hip, args.steps, args.warmup, use_graph=6)
+    ceiling = step_benchmark(hip, args.steps, args.warmup, use_graph=2)
     ceiling_gbs = main_run.weight_bytes / (ceiling.milliseconds_per_step * 1e-3) / 1e9
     gemv_weight_gbs = main_run.weight_bytes / (ms * 1e-3) / 1e9
     line["launch_ceiling"] = {"what": "the step's 112 launches as plain reads of the same weights (one hipGraph)",

@@ -477,10 +477,9 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     int32_t mode;
     int32_t warmup;
     int32_t steps;
-    int32_t use_graph;     /* 0 eager launches, 1 hipGraph per step, 2 persistent chain kernel, 3 warp-specialized streaming chain kernel,
-                              4 linked launches on two streams (one graph each), 5 linked launches, eager,
-                              6 the same launches as plain 16-byte reads of the weights in one hipGraph
-                              (the launch-shape ceiling; no GEMV arithmetic, rows must be 1) */
+    int32_t use_graph;     /* 0 eager launches, 1 hipGraph per step, 2 the same launches as plain
+                              16-byte reads of the weights in one hipGraph (the launch-shape
+                              ceiling; no GEMV arithmetic, rows must be 1) */
     int32_t kernel_filter; /* 0 whole chain; 1 QKV, 2 O, 3 gate/up, 4 down GEMVs only */
     uint64_t weight_bytes;
     uint64_t algorithmic_bytes_per_step;
@@ -489,13 +488,6 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     double gemv_kernel_milliseconds_per_step;
     uint64_t output_checksum; /* FNV-1a of the final hidden, qkv and activation rows */
 } Qwen3TtsStepBenchmarkV1;
-/* Diagnostic: device time per grid barrier of the persistent chain kernel's
- * barrier variants (0: agent fences + relaxed atomics; 1: no fences;
- * 2: release/acquire atomics; 3: no sleep in the poll; 4: variant 0 + a 4 KB
- * re-read after each barrier).  workgroups <= 0 uses one per CU. */
-QWEN3_TTS_API int32_t qwen3_tts_benchmark_grid_barrier(
-    int32_t device_index, int32_t variant, int32_t barriers, int32_t workgroups,
-    double* microseconds_per_barrier, char* error, size_t error_capacity);
 QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(
     int32_t device_index, Qwen3TtsStepBenchmarkV1* inout, char* error, size_t error_capacity);
 

@@ -164,7 +164,7 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
     if (b == nullptr || b->struct_size != sizeof(Qwen3TtsStepBenchmarkV1) || b->layers <= 0 || b->hidden <= 0 ||
         b->intermediate <= 0 || b->query_width <= 0 || b->key_value_width <= 0 || b->rows < 1 || b->rows > 8 ||
         b->steps <= 0 || b->warmup < 0 || b->kernel_filter < 0 || b->kernel_filter > 4 || b->use_graph < 0 ||
-        b->use_graph > 6 || (b->use_graph == 6 && b->rows != 1)) {
+        b->use_graph > 2 || (b->use_graph == 2 && b->rows != 1)) {
         write_error(error, cap, "invalid step benchmark arguments");
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
     }
@@ -194,78 +194,20 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         check_hip(launch_fill_bf16_normal(act, static_cast<uint64_t>(R) * I, 0x5EED0016ULL, 0.0f, 1.0f, stream), "fill act");
         const int mode = b->mode;
         const int filter = b->kernel_filter;
-        // Linked launches (use_graph 4: captured in a graph, 5: eager): the
-        // GEMVs alternate between two streams and order themselves through
-        // their link counters, so each kernel streams its weights while its
-        // predecessor still runs.
-        const bool linked = b->use_graph == 4 || b->use_graph == 5;
-        if (linked && (R != 1 || mode == kModeMfma)) throw std::invalid_argument("linked launches serve exact batch 1");
-        const int per_step = L * (filter == 0 ? 4 : 1);
-        unsigned* link_words = nullptr;
-        int* link_status = nullptr;
-        hipStream_t side = nullptr;
-        hipEvent_t fork = nullptr, join = nullptr;
-        if (linked) {
-            link_words = mem.get<unsigned>(static_cast<size_t>(kLinkWords) * per_step);
-            link_status = mem.get<int>(1);
-            check_hip(hipMemset(link_words, 0, sizeof(unsigned) * kLinkWords * per_step), "zero links");
-            check_hip(hipMemset(link_status, 0, sizeof(int)), "zero link status");
-            check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate(side)");
-            check_hip(hipEventCreateWithFlags(&fork, hipEventDisableTiming), "hipEventCreate(fork)");
-            check_hip(hipEventCreateWithFlags(&join, hipEventDisableTiming), "hipEventCreate(join)");
-        }
-        // QWEN3_TTS_LINK_TRACE=<file>: per launch of the last step, the first
-        // and last workgroup start, the last wait end and the last arrival
-        // (100 MHz clock), written as text (diagnostics).
-        const char* link_trace_path = std::getenv("QWEN3_TTS_LINK_TRACE");
-        unsigned long long* link_trace = nullptr;
-        if (linked && link_trace_path) link_trace = mem.get<unsigned long long>(4ull * per_step);
-        auto reset_trace = [&] {
-            if (!link_trace) return;
-            std::vector<unsigned long long> init(4ull * per_step, 0ull);
-            for (int k = 0; k < per_step; ++k) init[4 * k] = ~0ull;
-            check_hip(hipMemcpy(link_trace, init.data(), init.size() * 8, hipMemcpyHostToDevice), "reset trace");
-        };
-        reset_trace();
-        int launch_index = 0;
-        int only_parity = -1;  // >= 0: launch only the kernels of this stream (graph capture)
-        bool dry = false;                              // record footprints only
-        std::vector<std::pair<int, int>> footprints;  // workgroups, per CU
         int* read_sink = mem.get<int>(1);
-        auto launch = [&](GemvArgs g, const char* what) {
-            if (b->use_graph == 6) {  // the same weight bytes, plain reads
+        auto launch = [&](const GemvArgs& g, const char* what) {
+            if (b->use_graph == 2) {  // the same weight bytes, plain reads
                 const bool pair = g.epilogue == kEpiSiluRounded || g.epilogue == kEpiSiluFused;
                 const uint64_t bytes = static_cast<uint64_t>(g.in_features) * g.out_features * (pair ? 2 : 1);
                 read_weights_kernel<<<1536, 256, 0, stream>>>(g.weight, bytes, read_sink);
                 check_hip(hipGetLastError(), what);
                 return;
             }
-            if (!linked) {
-                check_hip(launch_int8_gemv(g, stream), what);
-                return;
-            }
-            const int k = launch_index++ % per_step;
-            g.link_counters = link_words + static_cast<size_t>(kLinkWords) * k;
-            g.link_wait = link_words + static_cast<size_t>(kLinkWords) * ((k + per_step - 1) % per_step);
-            g.link_bias = k == 0 ? 0u : 1u;
-            g.link_status = link_status;
-            g.link_trace = link_trace ? link_trace + 4 * k : nullptr;
-            if (only_parity >= 0 && k % 2 != only_parity) return;
-            if (dry) {
-                int wg = 0, per_cu = 0;
-                check_hip(gemv_launch_footprint(g, &wg, &per_cu), "GEMV footprint");
-                footprints.emplace_back(wg, per_cu);
-                return;
-            }
-            check_hip(launch_int8_gemv(g, k % 2 == 0 ? stream : side), what);
+            check_hip(launch_int8_gemv(g, stream), what);
         };
         // QKV output has the full fused row; O reads the q part with row
         // stride qkv_rows when R == 1 (the attention output stand-in).
         auto enqueue_step = [&] {
-            if (linked && !dry && only_parity < 0) {
-                check_hip(hipEventRecord(fork, stream), "hipEventRecord(fork)");
-                check_hip(hipStreamWaitEvent(side, fork, 0), "hipStreamWaitEvent(fork)");
-            }
             for (int l = 0; l < L; ++l) {
                 int8_t* base = w + per_layer * l;
                 float* sb = s + scales_per_layer * l;
@@ -277,11 +219,9 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                 const float* so = sqkv + qkv_rows;
                 const float* sgu = so + H;
                 const float* sd = sgu + 2 * I;
-                GemvArgs a;
-                a.rows = R;
-                a.mode = mode;
-                a.norm_epsilon = 1.0e-6f;
                 if (filter == 0 || filter == 1) {
+                    GemvArgs a;
+                    a.rows = R; a.mode = mode; a.norm_epsilon = 1.0e-6f;
                     a.weight = wqkv; a.scales = sqkv; a.input = hidden; a.norm_weight = gains;
                     a.in_features = H; a.out_features = static_cast<int>(qkv_rows); a.out16 = qkv;
                     a.epilogue = kEpiStore;
@@ -311,92 +251,8 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                     launch(d, "down GEMV");
                 }
             }
-            if (linked && !dry && only_parity < 0) {
-                check_hip(hipEventRecord(join, side), "hipEventRecord(join)");
-                check_hip(hipStreamWaitEvent(stream, join, 0), "hipStreamWaitEvent(join)");
-            }
         };
-        // Persistent chain: the same GEMVs as one op list.
-        const int workgroups = chain_workgroups();
-        ChainOp* d_ops = nullptr;
-        unsigned* d_sync = nullptr;
-        int op_count = 0;
-        if (b->use_graph == 2 || b->use_graph == 3) {
-            if (R != 1) throw std::invalid_argument("the persistent chain serves batch 1");
-            std::vector<ChainOp> ops;
-            for (int l = 0; l < L; ++l) {
-                int8_t* base = w + per_layer * l;
-                float* sb = s + scales_per_layer * l;
-                const int8_t* wqkv = base;
-                const int8_t* wo = wqkv + qkv_rows * H;
-                const int8_t* wgu = wo + static_cast<size_t>(H) * QW;
-                const int8_t* wd = wgu + 2ull * I * H;
-                auto add = [&](const int8_t* wt, const float* sc, const bf16_t* in, const bf16_t* norm, bf16_t* out,
-                               int in_f, int out_f, int epi) {
-                    ChainOp op{};
-                    op.kind = b->use_graph == 3 ? (stream_chain_supports(in_f, out_f, epi) ? 0 : -1)
-                                                : chain_kind_for(in_f, out_f, epi, workgroups);
-                    if (op.kind < 0) throw std::invalid_argument("GEMV shape not supported by the persistent chain");
-                    op.epilogue = epi;
-                    op.in_features = in_f;
-                    op.out_features = out_f;
-                    op.weight = wt;
-                    op.scales = sc;
-                    op.input = in;
-                    op.norm_weight = norm;
-                    op.out16 = out;
-                    op.norm_epsilon = 1.0e-6f;
-                    ops.push_back(op);
-                };
-                if (filter == 0 || filter == 1) add(wqkv, sb, hidden, gains, qkv, H, static_cast<int>(qkv_rows), kEpiStore);
-                if (filter == 0 || filter == 2) add(wo, sb + qkv_rows, qkv, nullptr, hidden, QW, H, kEpiAddRounded);
-                if (filter == 0 || filter == 3) add(wgu, sb + qkv_rows + H, hidden, gains + H, act, H, I, kEpiSiluRounded);
-                if (filter == 0 || filter == 4) add(wd, sb + qkv_rows + H + 2 * I, act, nullptr, hidden, I, H, kEpiAddRounded);
-            }
-            op_count = static_cast<int>(ops.size());
-            d_ops = mem.get<ChainOp>(ops.size());
-            d_sync = mem.get<unsigned>(kChainSyncWords);
-            check_hip(hipMemcpy(d_ops, ops.data(), ops.size() * sizeof(ChainOp), hipMemcpyHostToDevice), "upload ops");
-        }
-        if (linked) {
-            dry = true;
-            enqueue_step();
-            dry = false;
-            // Two linked launches are resident together: their workgroups must
-            // fit the device at once (with a margin), or a waiting kernel could
-            // hold the slots its predecessor needs.
-            hipDeviceProp_t props{};
-            check_hip(hipGetDeviceProperties(&props, device_index), "hipGetDeviceProperties");
-            for (size_t i = 0; i < footprints.size(); ++i) {
-                const auto& p = footprints[i];
-                const auto& q = footprints[(i + 1) % footprints.size()];
-                const double used = static_cast<double>(p.first) / p.second + static_cast<double>(q.first) / q.second;
-                if (p.second <= 0 || q.second <= 0 || used > 1.0 * props.multiProcessorCount) {
-                    throw std::invalid_argument("linked GEMV launches do not fit the device together (launch " +
-                                                std::to_string(i) + ": " + std::to_string(p.first) + " workgroups, " +
-                                                std::to_string(p.second) + " per CU; next: " + std::to_string(q.first) +
-                                                ", " + std::to_string(q.second) + ")");
-                }
-            }
-        }
-        hipGraphExec_t side_exec = nullptr;  // linked: the odd launches' graph
-        if (b->use_graph == 4) {
-            // one graph per stream (even launches, odd launches), each a plain
-            // chain; the link counters order the two graphs' kernels
-            for (int parity = 0; parity < 2; ++parity) {
-                hipStream_t s = parity == 0 ? stream : side;
-                only_parity = parity;
-                check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-                enqueue_step();
-                hipGraph_t graph = nullptr;
-                check_hip(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
-                const hipError_t st = hipGraphInstantiate(parity == 0 ? &exec : &side_exec, graph, nullptr, nullptr, 0);
-                (void)hipGraphDestroy(graph);
-                check_hip(st, "hipGraphInstantiate");
-            }
-            only_parity = -1;
-        }
-        if (b->use_graph == 1 || b->use_graph == 6) {
+        if (b->use_graph >= 1) {
             check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             enqueue_step();
             hipGraph_t graph = nullptr;
@@ -405,25 +261,8 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             (void)hipGraphDestroy(graph);
             check_hip(st, "hipGraphInstantiate");
         }
-        // QWEN3_TTS_CHAIN_TRACE=<file>: phase timestamps of workgroup 0 of the
-        // last persistent launch, written as text (diagnostics).
-        const char* trace_path = std::getenv("QWEN3_TTS_CHAIN_TRACE");
-        unsigned long long* d_trace = (d_ops && trace_path) ? mem.get<unsigned long long>(256 * 8) : nullptr;
         auto run = [&] {
-            if (d_ops) {
-                if (b->use_graph == 3) {
-                    check_hip(launch_stream_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "stream chain");
-                } else {
-                    check_hip(launch_persistent_chain(d_ops, op_count, d_sync, workgroups, stream, d_trace), "persistent chain");
-                }
-            } else if (side_exec) {
-                check_hip(hipEventRecord(fork, stream), "hipEventRecord(fork)");
-                check_hip(hipStreamWaitEvent(side, fork, 0), "hipStreamWaitEvent(fork)");
-                check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
-                check_hip(hipGraphLaunch(side_exec, side), "hipGraphLaunch(side)");
-                check_hip(hipEventRecord(join, side), "hipEventRecord(join)");
-                check_hip(hipStreamWaitEvent(stream, join, 0), "hipStreamWaitEvent(join)");
-            } else if (exec) {
+            if (exec) {
                 check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
             } else {
                 enqueue_step();
@@ -462,42 +301,6 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         b->total_milliseconds = ms;
         b->milliseconds_per_step = ms / b->steps;
         b->gemv_kernel_milliseconds_per_step = ms / b->steps;
-        if (d_trace) {
-            std::vector<unsigned long long> t(256 * 8);
-            check_hip(hipMemcpy(t.data(), d_trace, t.size() * 8, hipMemcpyDeviceToHost), "read trace");
-            if (FILE* f = std::fopen(trace_path, "w")) {
-                for (int i = 0; i < std::min(op_count, 256); ++i) {
-                    std::fprintf(f, "%d", i);
-                    for (int p = 0; p < 6; ++p) std::fprintf(f, " %llu", t[i * 8 + p]);
-                    std::fprintf(f, "\n");
-                }
-                std::fclose(f);
-            }
-        }
-        if (link_trace) {
-            // one more step with a clean trace
-            reset_trace();
-            run();
-            check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize(trace)");
-            std::vector<unsigned long long> t(4ull * per_step);
-            check_hip(hipMemcpy(t.data(), link_trace, t.size() * 8, hipMemcpyDeviceToHost), "read trace");
-            if (FILE* f = std::fopen(link_trace_path, "w")) {
-                for (int k = 0; k < per_step; ++k) {
-                    std::fprintf(f, "%d %llu %llu %llu %llu\n", k, t[4 * k], t[4 * k + 1], t[4 * k + 2], t[4 * k + 3]);
-                }
-                std::fclose(f);
-            }
-        }
-        if (link_status) {
-            int status = 0;
-            check_hip(hipMemcpy(&status, link_status, sizeof(int), hipMemcpyDeviceToHost), "read link status");
-            if (status != 0) throw DeviceFailure("linked GEMV launches: a wait timed out");
-        }
-        if (d_sync) {
-            int status = 0;
-            check_hip(hipMemcpy(&status, d_sync + 1, sizeof(int), hipMemcpyDeviceToHost), "read chain status");
-            if (status != 0) throw DeviceFailure("persistent chain: a grid barrier wait timed out");
-        }
         {
             uint64_t h = 1469598103934665603ULL;
             for (auto [ptr, count] : {std::make_pair(hidden, static_cast<size_t>(R) * H),
@@ -513,13 +316,6 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             b->output_checksum = h;
         }
         if (exec) (void)hipGraphExecDestroy(exec);
-        if (side_exec) (void)hipGraphExecDestroy(side_exec);
-        if (side) {
-            (void)hipStreamSynchronize(side);
-            (void)hipStreamDestroy(side);
-        }
-        if (fork) (void)hipEventDestroy(fork);
-        if (join) (void)hipEventDestroy(join);
         (void)hipEventDestroy(start);
         (void)hipEventDestroy(stop);
         (void)hipStreamDestroy(stream);

@@ -43,15 +43,7 @@ using namespace gemv_detail;
 // are still in flight; no memory round trip follows the dot product except the
 // output store.
 // ---------------------------------------------------------------------------
-//
-// Linked variant (kLinked): the weights and the constant epilogue operands
-// are requested first, then thread 0 waits for the previous launch's
-// completion flag, then x (device-coherent loads) and the residual follow;
-// the outputs are stored device-coherently and the workgroup arrives on its
-// launch's counters.  While the previous launch runs, this one's weight
-// stream is already in flight.
-// ---------------------------------------------------------------------------
-template <int kVpl, int kEpi, bool kNorm, bool kLinked = false>
+template <int kVpl, int kEpi, bool kNorm>
 __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
     if (a.input_row_index != nullptr) {
         a.input += static_cast<size_t>(*a.input_row_index) * a.in_features;
@@ -80,25 +72,15 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
     const uint4* xin = reinterpret_cast<const uint4*>(a.input);
     const uint4* gin = reinterpret_cast<const uint4*>(a.norm_weight);
     uint4 x0{}, x1{}, x2{}, g0{}, g1{}, g2{};
-    const int group = blockIdx.x & 7;
-    unsigned group_count = 0;
-    if constexpr (kLinked) {
-        if (threadIdx.x == 0) {
-            group_count = link_read_group(a.link_counters, group);
-            if (a.link_trace != nullptr && blockIdx.x == 0) a.link_trace[0] = wall_clock64();
-            if (a.link_trace != nullptr && blockIdx.x == gridDim.x - 1) a.link_trace[1] = wall_clock64();
-        }
-    } else {
-        x0 = xin[chunk(0)];
-        if constexpr (kNorm) g0 = gin[chunk(0)];
-        if constexpr (kPer > 1) {
-            x1 = xin[chunk(1)];
-            if constexpr (kNorm) g1 = gin[chunk(1)];
-        }
-        if constexpr (kPer > 2) {
-            x2 = xin[chunk(2)];
-            if constexpr (kNorm) g2 = gin[chunk(2)];
-        }
+    x0 = xin[chunk(0)];
+    if constexpr (kNorm) g0 = gin[chunk(0)];
+    if constexpr (kPer > 1) {
+        x1 = xin[chunk(1)];
+        if constexpr (kNorm) g1 = gin[chunk(1)];
+    }
+    if constexpr (kPer > 2) {
+        x2 = xin[chunk(2)];
+        if constexpr (kNorm) g2 = gin[chunk(2)];
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight loads
 
@@ -117,27 +99,7 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
     // unit and discard it.
     const int first = unit < units ? unit : units - 1;
     issue(first);
-    EpiInputs epi;
-    if constexpr (kLinked) {
-        epi = prefetch_constants<kEpi>(a, first);
-        if constexpr (kNorm) {
-            g0 = gin[chunk(0)];
-            if constexpr (kPer > 1) g1 = gin[chunk(1)];
-            if constexpr (kPer > 2) g2 = gin[chunk(2)];
-        }
-        if (threadIdx.x == 0 && a.link_wait != nullptr) {
-            const unsigned step = group_count / link_members(group);
-            link_wait_flag(a.link_wait + (9 + group) * kLinkLineWords, step + a.link_bias, a.link_status);
-            if (a.link_trace != nullptr && blockIdx.x == 0) a.link_trace[2] = wall_clock64();
-        }
-        __syncthreads();
-        x0 = coherent_load16(xin + chunk(0));
-        if constexpr (kPer > 1) x1 = coherent_load16(xin + chunk(1));
-        if constexpr (kPer > 2) x2 = coherent_load16(xin + chunk(2));
-        load_residual<kEpi>(a, first, epi);
-    } else {
-        epi = prefetch_epi<kEpi>(a, first);
-    }
+    const EpiInputs epi = prefetch_epi<kEpi>(a, first);
     __builtin_amdgcn_sched_barrier(0);  // and the LDS stores of x behind them
 
     auto stage = [&](int j, const uint4& xv) {
@@ -198,16 +160,9 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
     for (int r = 0; r < kRows; ++r) acc[r] = fold32(acc[r]);
     if (lane == 0 && unit < units) {
         if constexpr (kSilu) {
-            finish_gate_up<kEpi, kLinked>(a, unit, acc[0], acc[kRows - 1], epi);
+            finish_gate_up<kEpi>(a, unit, acc[0], acc[kRows - 1], epi);
         } else {
-            finish_channel<kEpi, kLinked>(a, unit, acc[0], epi);
-        }
-    }
-    if constexpr (kLinked) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores have completed
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            if (link_arrive(a.link_counters, group) && a.link_trace != nullptr) a.link_trace[3] = wall_clock64();
+            finish_channel<kEpi>(a, unit, acc[0], epi);
         }
     }
 }
@@ -751,24 +706,16 @@ int device_cu_count() {
     return count;
 }
 
-template <int kEpi, bool kNorm, bool kLinked>
-const void* fixed_kernel(int vpl) {
-    switch (vpl) {
-        case 2: return reinterpret_cast<const void*>(gemv_exact_fixed<2, kEpi, kNorm, kLinked>);
-        case 4: return reinterpret_cast<const void*>(gemv_exact_fixed<4, kEpi, kNorm, kLinked>);
-        case 6: return reinterpret_cast<const void*>(gemv_exact_fixed<6, kEpi, kNorm, kLinked>);
-        case 12: return reinterpret_cast<const void*>(gemv_exact_fixed<12, kEpi, kNorm, kLinked>);
-        default: return nullptr;
-    }
-}
-
 template <int kEpi, bool kNorm>
 hipError_t dispatch_fixed(const GemvArgs& a, int vpl, int grid, hipStream_t s) {
-    const void* fn = a.link_counters != nullptr ? fixed_kernel<kEpi, kNorm, true>(vpl) : fixed_kernel<kEpi, kNorm, false>(vpl);
-    if (fn == nullptr) return hipErrorInvalidValue;
-    GemvArgs copy = a;
-    void* params[] = {&copy};
-    return hipLaunchKernel(fn, dim3(grid), dim3(kThreads), params, 0, s);
+    switch (vpl) {
+        case 2: gemv_exact_fixed<2, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 4: gemv_exact_fixed<4, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 6: gemv_exact_fixed<6, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        case 12: gemv_exact_fixed<12, kEpi, kNorm><<<grid, kThreads, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 template <int kEpi, bool kNorm>
@@ -819,7 +766,6 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
             return dispatch_fixed<kEpi, kNorm>(a, vpl, grid, s);
         }
     }
-    if (a.link_counters != nullptr) return hipErrorInvalidValue;  // links exist on the fixed-K path only
     const int generic_units = a.out_features;
     int grid = (generic_units + kHalfWaves - 1) / kHalfWaves;
     const int cap = device_cu_count() * 16;
@@ -841,11 +787,6 @@ hipError_t launch_int8_gemv(const GemvArgs& a, hipStream_t stream) {
     if (a.epilogue == kEpiStore && a.out16 == nullptr && a.out32 == nullptr) return hipErrorInvalidValue;
     if (a.epilogue >= kEpiBias && a.bias == nullptr) return hipErrorInvalidValue;
     if (a.input_row_index != nullptr && a.rows != 1) return hipErrorInvalidValue;
-    if (a.link_counters != nullptr &&
-        (a.rows != 1 || a.mode == kModeMfma || a.out32 != nullptr || a.link_status == nullptr ||
-         a.input_row_index != nullptr)) {
-        return hipErrorInvalidValue;
-    }
     const bool norm = a.norm_weight != nullptr;
     switch (a.epilogue) {
         case kEpiStore: return norm ? dispatch<kEpiStore, true>(a, stream) : dispatch<kEpiStore, false>(a, stream);
@@ -858,35 +799,6 @@ hipError_t launch_int8_gemv(const GemvArgs& a, hipStream_t stream) {
         case kEpiBiasAdd: return norm ? dispatch<kEpiBiasAdd, true>(a, stream) : dispatch<kEpiBiasAdd, false>(a, stream);
         default: return hipErrorInvalidValue;
     }
-}
-
-namespace {
-template <int kEpi>
-const void* linked_kernel(bool norm, int vpl) {
-    return norm ? fixed_kernel<kEpi, true, true>(vpl) : fixed_kernel<kEpi, false, true>(vpl);
-}
-}  // namespace
-
-hipError_t gemv_launch_footprint(const GemvArgs& a, int* workgroups, int* per_cu) {
-    if (workgroups == nullptr || per_cu == nullptr) return hipErrorInvalidValue;
-    if (a.rows != 1 || a.in_features % 512 != 0 || a.out_features <= 0) return hipErrorInvalidValue;
-    const int vpl = a.in_features / 512;
-    const bool norm = a.norm_weight != nullptr;
-    const void* fn = nullptr;
-    switch (a.epilogue) {
-        case kEpiStore: fn = linked_kernel<kEpiStore>(norm, vpl); break;
-        case kEpiAddFma: fn = linked_kernel<kEpiAddFma>(norm, vpl); break;
-        case kEpiAddRounded: fn = linked_kernel<kEpiAddRounded>(norm, vpl); break;
-        case kEpiSiluFused: fn = linked_kernel<kEpiSiluFused>(norm, vpl); break;
-        case kEpiSiluRounded: fn = linked_kernel<kEpiSiluRounded>(norm, vpl); break;
-        case kEpiBias: fn = linked_kernel<kEpiBias>(norm, vpl); break;
-        case kEpiBiasSilu: fn = linked_kernel<kEpiBiasSilu>(norm, vpl); break;
-        case kEpiBiasAdd: fn = linked_kernel<kEpiBiasAdd>(norm, vpl); break;
-        default: break;
-    }
-    if (fn == nullptr) return hipErrorInvalidValue;
-    *workgroups = (a.out_features + kHalfWaves - 1) / kHalfWaves;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, fn, kThreads, 0);
 }
 
 hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,

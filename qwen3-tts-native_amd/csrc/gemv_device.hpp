@@ -1,5 +1,4 @@
-// Device helpers of the int8 GEMV family shared by the per-GEMV kernels
-// (gemv.hip) and the persistent chain kernel (persistent.hip).
+// Device helpers of the int8 GEMV family (gemv.hip).
 //
 // The exact order reproduces native/qwen3-tts-native/native/src/int8_gemv.cu:
 // 67-125: lane l of a 32-lane group owns the 16-byte weight vectors
@@ -187,27 +186,6 @@ __device__ __forceinline__ float chain16_packed(const int4 w, const uint32_t* xp
     return sum;
 }
 
-// bf16 output access.  kCoherent: agent-scope relaxed atomics (device-
-// coherent loads/stores that bypass the non-coherent caches), used when other
-// workgroups of a persistent grid read the value after a grid barrier.
-template <bool kCoherent>
-__device__ __forceinline__ float load_out(const bf16_t* p) {
-    if constexpr (kCoherent) {
-        return bf2f(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    } else {
-        return bf2f(*p);
-    }
-}
-
-template <bool kCoherent>
-__device__ __forceinline__ void store_out(bf16_t* p, bf16_t v) {
-    if constexpr (kCoherent) {
-        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        *p = v;
-    }
-}
-
 // Epilogue operands of one output channel (or gate/up pair): the scale(s),
 // the residual or bias.  Loaded before the dot products so their memory
 // latency overlaps the weight stream instead of following it.
@@ -218,163 +196,74 @@ struct EpiInputs {
     float prior = 0.0f;  // residual of bias-add
 };
 
-template <int kEpi, bool kCoherent = false>
+template <int kEpi>
 __device__ __forceinline__ EpiInputs prefetch_epi(const GemvArgs& a, int channel) {
     EpiInputs e;
     e.scale0 = a.scales[channel];
     if constexpr (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded) {
         e.scale1 = a.scales[a.out_features + channel];
     } else if constexpr (kEpi == kEpiAddFma || kEpi == kEpiAddRounded) {
-        e.extra = load_out<kCoherent>(a.out16 + channel);
+        e.extra = bf2f(a.out16[channel]);
     } else if constexpr (kEpi == kEpiBias || kEpi == kEpiBiasSilu) {
         e.extra = bf2f(a.bias[channel]);
     } else if constexpr (kEpi == kEpiBiasAdd) {
         e.extra = bf2f(a.bias[channel]);
-        e.prior = load_out<kCoherent>(a.out16 + channel);
+        e.prior = bf2f(a.out16[channel]);
     }
     return e;
 }
 
 // Half-wave lane 0 epilogue for the plain / residual / bias epilogues.
-template <int kEpi, bool kCoherent = false>
+template <int kEpi>
 __device__ __forceinline__ void finish_channel(const GemvArgs& a, int channel, float value, const EpiInputs& e) {
     const float scale = e.scale0;
     bf16_t* out = a.out16 + channel;
     if constexpr (kEpi == kEpiStore) {
         const float y = value * scale;
         if (a.out32 != nullptr) a.out32[channel] = y;
-        if (a.out16 != nullptr) store_out<kCoherent>(out, f2bf(y));
+        if (a.out16 != nullptr) *out = f2bf(y);
     } else if constexpr (kEpi == kEpiAddFma) {
-        store_out<kCoherent>(out, f2bf(fmaf(value, scale, e.extra)));
+        *out = f2bf(fmaf(value, scale, e.extra));
     } else if constexpr (kEpi == kEpiAddRounded) {
         const float projected = round_bf(value * scale);
-        store_out<kCoherent>(out, f2bf(e.extra + projected));
+        *out = f2bf(e.extra + projected);
     } else if constexpr (kEpi == kEpiBias) {
-        store_out<kCoherent>(out, f2bf(round_bf(value * scale) + e.extra));
+        *out = f2bf(round_bf(value * scale) + e.extra);
     } else if constexpr (kEpi == kEpiBiasSilu) {
         float v = round_bf(value * scale) + e.extra;
         v *= 1.0f / (1.0f + q3_expf(-v));
-        store_out<kCoherent>(out, f2bf(v));
+        *out = f2bf(v);
     } else if constexpr (kEpi == kEpiBiasAdd) {
         const float projected = round_bf(round_bf(value * scale) + e.extra);
-        store_out<kCoherent>(out, f2bf(e.prior + projected));
+        *out = f2bf(e.prior + projected);
     }
 }
 
 // Gate/up pair epilogue (int8_gemv.cu:284-288 fused; separate SiLU-gate
 // rounding for the single-session path).
-template <int kEpi, bool kCoherent = false>
+template <int kEpi>
 __device__ __forceinline__ void finish_gate_up(const GemvArgs& a, int channel, float g, float u, const EpiInputs& e) {
     const float gate = g * e.scale0;
     const float up = u * e.scale1;
     if constexpr (kEpi == kEpiSiluFused) {
         const float activated = gate / (1.0f + q3_expf(-gate));
-        store_out<kCoherent>(a.out16 + channel, f2bf(activated * up));
+        a.out16[channel] = f2bf(activated * up);
     } else {
         const float gate16 = round_bf(gate);
         const float up16 = round_bf(up);
         const float activated = round_bf(gate16 / (1.0f + q3_expf(-gate16)));
-        store_out<kCoherent>(a.out16 + channel, f2bf(activated * up16));
+        a.out16[channel] = f2bf(activated * up16);
     }
 }
 
-template <int kEpi, bool kCoherent = false>
+template <int kEpi>
 __device__ __forceinline__ void store_channel(const GemvArgs& a, int channel, float value) {
-    finish_channel<kEpi, kCoherent>(a, channel, value, prefetch_epi<kEpi, kCoherent>(a, channel));
+    finish_channel<kEpi>(a, channel, value, prefetch_epi<kEpi>(a, channel));
 }
 
-template <int kEpi, bool kCoherent = false>
+template <int kEpi>
 __device__ __forceinline__ void store_gate_up(const GemvArgs& a, int channel, float g, float u) {
-    finish_gate_up<kEpi, kCoherent>(a, channel, g, u, prefetch_epi<kEpi, kCoherent>(a, channel));
-}
-
-// Epilogue operands that never change during a chain (scales, bias): a linked
-// launch requests them with its weights, before it waits; the residual is
-// read after the wait (it is the previous launches' output).
-template <int kEpi>
-__device__ __forceinline__ EpiInputs prefetch_constants(const GemvArgs& a, int channel) {
-    EpiInputs e;
-    e.scale0 = a.scales[channel];
-    if constexpr (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded) {
-        e.scale1 = a.scales[a.out_features + channel];
-    } else if constexpr (kEpi == kEpiBias || kEpi == kEpiBiasSilu || kEpi == kEpiBiasAdd) {
-        e.extra = bf2f(a.bias[channel]);
-    }
-    return e;
-}
-
-template <int kEpi>
-__device__ __forceinline__ void load_residual(const GemvArgs& a, int channel, EpiInputs& e) {
-    if constexpr (kEpi == kEpiAddFma || kEpi == kEpiAddRounded) {
-        e.extra = load_out<true>(a.out16 + channel);
-    } else if constexpr (kEpi == kEpiBiasAdd) {
-        e.prior = load_out<true>(a.out16 + channel);
-    }
-}
-
-// 16 bytes written by other workgroups of earlier launches that may still be
-// resident: two device-coherent 8-byte loads.
-__device__ __forceinline__ uint4 coherent_load16(const uint4* p) {
-    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_uint4(static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32), static_cast<uint32_t>(hi),
-                      static_cast<uint32_t>(hi >> 32));
-}
-
-// ---------------------------------------------------------------------------
-// Launch links.  Workgroup b belongs to group b % 8 (members: the workgroups
-// of that residue).  A workgroup arrives on its group counter after its
-// stores have completed; the last member of a group arrives on the total
-// counter; the last group writes the completion flag (= completed steps) into
-// 8 lines, which the next launch's workgroups poll (group g its copy g).
-// All counters only grow, so a workgroup's step is its group counter, read
-// before it arrives, divided by the group's members.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ unsigned link_members(int group) {
-    return (gridDim.x - static_cast<unsigned>(group) + 7u) / 8u;
-}
-
-__device__ __forceinline__ unsigned link_read_group(const unsigned* counters, int group) {
-    return __hip_atomic_load(counters + group * kLinkLineWords, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Bounded wait of one thread for flag >= target (wrap-safe compare).  Gives
-// up after ~0.2 s, or when another wait gave up, and records it in `status`,
-// so every workgroup always finishes.
-__device__ inline void link_wait_flag(const unsigned* flag, unsigned target, int* status) {
-    const uint64_t start = wall_clock64();
-    unsigned spins = 0;
-    while (static_cast<int>(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-        __builtin_amdgcn_s_sleep(1);
-        if ((++spins & 63u) == 0u) {
-            if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
-            if (wall_clock64() - start > 20000000ull) {  // 100 MHz clock
-                __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                return;
-            }
-        }
-    }
-}
-
-// Called by one thread after every thread's stores of this workgroup have
-// completed (s_waitcnt + barrier).  Returns true for the arrival that
-// completed the launch.
-__device__ inline bool link_arrive(unsigned* counters, int group) {
-    const unsigned members = link_members(group);
-    const unsigned groups = gridDim.x < 8u ? gridDim.x : 8u;
-    const unsigned before =
-        __hip_atomic_fetch_add(counters + group * kLinkLineWords, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((before + 1u) % members != 0u) return false;
-    const unsigned total =
-        __hip_atomic_fetch_add(counters + 8 * kLinkLineWords, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    if (total % groups != 0u) return false;
-    const unsigned completed = total / groups;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        __hip_atomic_store(counters + (9 + c) * kLinkLineWords, completed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return true;
+    finish_gate_up<kEpi>(a, channel, g, u, prefetch_epi<kEpi>(a, channel));
 }
 
 }  // namespace gemv_detail

@@ -171,29 +171,9 @@ struct GemvArgs {
     int rows = 1;
     int epilogue = kEpiStore;
     int mode = kModeAuto;
-    // Linked launch (rows == 1, exact order, K a multiple of 1024 up to 6144):
-    // the kernel may start while the previous launch of a chain is still
-    // running.  It requests its weights, waits until the previous launch's
-    // completion flag reaches (its step + link_bias), reads activations with
-    // device-coherent loads, stores with device-coherent stores and signals
-    // its own completion.  Counters are monotone (zeroed once at creation,
-    // never reset), so the same links serve every replay of a chain.
-    unsigned* link_counters = nullptr;    // this launch's kLinkWords words
-    const unsigned* link_wait = nullptr;  // the previous launch's counters (nullptr: no wait)
-    unsigned link_bias = 1;               // 1 within a step; 0 for a step's first launch
-    int* link_status = nullptr;           // set to 1 when a wait gave up (results invalid)
-    unsigned long long* link_trace = nullptr;  // optional diagnostics: 4 clock values per launch
 };
 
-// Words of one launch's link counters: 8 group counters, a total counter and 8
-// copies of the completion flag, each on its own 128-byte line.
-constexpr int kLinkLineWords = 32;
-constexpr int kLinkWords = 17 * kLinkLineWords;
-
 hipError_t launch_int8_gemv(const GemvArgs& args, hipStream_t stream);
-// Workgroups and resident workgroups per CU of the kernel launch_int8_gemv
-// would use for `args` (used to check that two linked launches fit at once).
-hipError_t gemv_launch_footprint(const GemvArgs& args, int* workgroups, int* per_cu);
 
 hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,
                                        int in_features, int out_features, hipStream_t stream);
@@ -362,33 +342,6 @@ hipError_t launch_gather_embedding(const bf16_t* table, int vocabulary, int widt
 hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int vocabulary0,
                                  int vocabulary, int width, const int* tokens, bf16_t* output,
                                  hipStream_t stream);
-
-// Persistent GEMV chain (persistent.hip): one op per dependent GEMV.
-struct ChainOp {
-    int kind;  // chosen by chain_kind_for
-    int epilogue;
-    int in_features;
-    int out_features;
-    const int8_t* weight;
-    const float* scales;
-    const bf16_t* input;
-    const bf16_t* norm_weight;
-    const bf16_t* bias;
-    bf16_t* out16;
-    float norm_epsilon;
-    int reserved;
-};
-constexpr int kChainSyncWords = 32 * 16;
-int chain_kind_for(int in_features, int out_features, int epilogue, int workgroups);
-int chain_workgroups();
-// Warp-specialized persistent chain (loader waves stream weights into an LDS
-// ring; compute waves consume): same op list, ChainOp::kind ignored.
-bool stream_chain_supports(int in_features, int out_features, int epilogue);
-size_t stream_chain_lds_bytes();
-hipError_t launch_stream_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups, hipStream_t stream,
-                               unsigned long long* trace = nullptr);
-hipError_t launch_persistent_chain(const ChainOp* ops, int count, unsigned* sync, int workgroups,
-                                   hipStream_t stream, unsigned long long* trace = nullptr);
 
 // Lockstep-batch glue: rows of a batch from / to per-session buffers.
 hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,

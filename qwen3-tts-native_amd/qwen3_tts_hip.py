@@ -218,7 +218,6 @@ SIGNATURES = {
     "qwen3_tts_stream_destroy": (None, [P]),
     "qwen3_tts_stream_synchronize": (I32, [P] + ERR),
     "qwen3_tts_benchmark_talker_step_gemvs": (I32, [I32, C.POINTER(StepBenchmarkV1)] + ERR),
-    "qwen3_tts_benchmark_grid_barrier": (I32, [I32, I32, I32, I32, C.POINTER(C.c_double)] + ERR),
 }
 
 _LIB = None
