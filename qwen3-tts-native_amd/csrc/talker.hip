@@ -846,6 +846,8 @@ private:
     template <typename Enqueue>
     void launch_graph(Graph& g, const SamplingParams& key, Enqueue&& enqueue) {
         if (g.have_key && !(g.key == key)) {
+            // the old graph may still be queued on the stream
+            if (g.exec) check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize(replace graph)");
             if (g.exec) (void)hipGraphExecDestroy(g.exec);
             g.exec = nullptr;
             g.eager_runs = 0;
