@@ -314,6 +314,14 @@ QWEN3_TTS_API int32_t qwen3_tts_session_read_last_hidden_v1(
     Qwen3TtsSessionHandle handle, void* destination, uint64_t bytes, char* error,
     size_t error_capacity);
 
+/* Diagnostics: positions 0..count-1 of talker layer `layer`'s key cache
+ * (which = 0) or value cache (which = 1) as [position][kv_width] bf16 in host
+ * memory; `bytes` must equal 2 * count * kv_width.  Fails with
+ * QWEN3_TTS_TALKER_STATUS_STATE while a frame lease is in flight. */
+QWEN3_TTS_API int32_t qwen3_tts_session_read_talker_cache_v1(
+    Qwen3TtsSessionHandle handle, int32_t layer, int32_t which, int32_t count, void* destination,
+    uint64_t bytes, char* error, size_t error_capacity);
+
 /* Fills `output` with the VoiceDesign geometry of the reference. */
 QWEN3_TTS_API void qwen3_tts_model_config_default(Qwen3TtsModelConfigV1* output);
 
@@ -425,6 +433,22 @@ QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention_noalloc_v1(
     uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
     int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
     int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
+/* The prefill's bf16 GEMM (the reference's cublasGemmEx / StridedBatchedEx
+ * calls with CUBLAS_COMPUTE_32F, talker.cu:2637-2674,2772-2842):
+ * C[m][n] = bf16(sum_k A[m][k] * B[n][k]) with fp32 accumulation, all
+ * row-major; batch z uses A + z*a_batch, B + (z / b_group)*b_batch and
+ * C + z*c_batch (elements).  k, lda, ldb, a_batch, b_batch multiples of 8;
+ * A and B 16-byte aligned. */
+QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_v1(
+    const uint16_t* a, const uint16_t* b, uint16_t* c, int32_t m, int32_t n, int32_t k, int32_t lda,
+    int32_t ldb, int32_t ldc, int32_t batch, int32_t b_group, int64_t a_batch, int64_t b_batch,
+    int64_t c_batch, void* stream, char* error, size_t error_capacity);
+/* causal_softmax_kernel (talker_kernels.cu:232-260) on bf16 scores
+ * [heads][rows][stride], in place; keys past the query (up to stride) are set
+ * to 0.  rows <= 512. */
+QWEN3_TTS_API int32_t qwen3_tts_op_causal_softmax_v1(
+    uint16_t* scores, int32_t heads, int32_t rows, int32_t stride, int32_t head_dimension, void* stream,
+    char* error, size_t error_capacity);
 QWEN3_TTS_API int32_t qwen3_tts_op_kv_scatter_rows(
     const uint16_t* rows_data, uint16_t* const* cache_bases, const int32_t* positions,
     int32_t rows, int32_t width, int32_t row_stride, void* stream, char* error,

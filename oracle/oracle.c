@@ -888,3 +888,174 @@ int orc_prefill(const OrcModel* m, OrcSession* s, const int* text_ids,
     free(input);
     return sample_talker(m, s, sampling);
 }
+
+/* ------------------------------------------------------------------------ */
+/* bf16 prefill                                                              */
+/* ------------------------------------------------------------------------ */
+
+typedef struct Bf16GemmCtx {
+    const float *a, *b;
+    uint16_t* c;
+    int m, n, k, ldc;
+} Bf16GemmCtx;
+
+/* 0: fp32 fmaf chain in k order; 1: the sum accumulated in double (the
+ * product of two bf16 is exact in double) and rounded once to fp32. */
+static int g_gemm_order = 0;
+
+void orc_set_gemm_order(int order) { g_gemm_order = order; }
+
+static void bf16_gemm_range(void* p, int j0, int j1) {
+    const Bf16GemmCtx* g = (const Bf16GemmCtx*)p;
+    for (int i = 0; i < g->m; ++i) {
+        const float* ai = g->a + (size_t)i * g->k;
+        for (int j = j0; j < j1; ++j) {
+            const float* bj = g->b + (size_t)j * g->k;
+            float acc = 0.0f;
+            if (g_gemm_order == 1) {
+                double sum = 0.0;
+                for (int t = 0; t < g->k; ++t) sum += (double)ai[t] * (double)bj[t];
+                acc = (float)sum;
+            } else {
+                for (int t = 0; t < g->k; ++t) acc = fmaf(ai[t], bj[t], acc);
+            }
+            g->c[(size_t)i * g->ldc + j] = tobf(acc);
+        }
+    }
+}
+
+void orc_bf16_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int n, int k,
+                   int lda, int ldb, int ldc) {
+    float* af = (float*)malloc((size_t)m * k * sizeof(float));
+    float* bf_ = (float*)malloc((size_t)n * k * sizeof(float));
+    for (int i = 0; i < m; ++i) orc_bf16_to_f32_array(a + (size_t)i * lda, af + (size_t)i * k, (size_t)k);
+    for (int j = 0; j < n; ++j) orc_bf16_to_f32_array(b + (size_t)j * ldb, bf_ + (size_t)j * k, (size_t)k);
+    Bf16GemmCtx g = {af, bf_, c, m, n, k, ldc};
+    for_channels(n, (size_t)m * n * k, bf16_gemm_range, &g);
+    free(af);
+    free(bf_);
+}
+
+void orc_causal_softmax(uint16_t* scores, int heads, int rows, int stride, int head_dimension) {
+    const float scale = 1.0f / sqrtf((float)head_dimension);
+    float* e = (float*)malloc((size_t)rows * sizeof(float));
+    for (int h = 0; h < heads; ++h) {
+        for (int q = 0; q < rows; ++q) {
+            uint16_t* row = scores + ((size_t)h * rows + q) * stride;
+            float maximum = -INFINITY;
+            for (int key = 0; key <= q; ++key) {
+                e[key] = rbf(bf(row[key]) * scale);
+                maximum = fmaxf(maximum, e[key]);
+            }
+            float denominator = 0.0f;
+            for (int key = 0; key <= q; ++key) denominator += q3_expf(e[key] - maximum);
+            const float inverse = 1.0f / denominator;
+            for (int key = 0; key < stride; ++key) {
+                row[key] = key <= q ? tobf(q3_expf(e[key] - maximum) * inverse) : tobf(0.0f);
+            }
+        }
+    }
+    free(e);
+}
+
+/* run_decoder_prefill, K/talker.cu:2854-3202: per layer RMSNorm rows, q/k/v
+ * GEMMs, head norms, RoPE from position 0, cache writes, attention (GEMM path
+ * or exact kernel), O GEMM + residual, RMSNorm, gate and up GEMMs, SiLU gate,
+ * down GEMM + residual. */
+static void prefill_decoder(const OrcModel* m, OrcSession* s, uint16_t* hidden, int rows, int gemm_capacity) {
+    const OrcDims* d = &m->talker;
+    const int H = d->hidden, I = d->intermediate, hd = d->head_dimension;
+    const int qw = d->query_heads * hd, kvw = d->key_value_heads * hd;
+    const int group = d->query_heads / d->key_value_heads;
+    uint16_t* normalized = (uint16_t*)malloc((size_t)rows * H * 2);
+    uint16_t* q = (uint16_t*)malloc((size_t)rows * qw * 2);
+    uint16_t* k = (uint16_t*)malloc((size_t)rows * kvw * 2);
+    uint16_t* v = (uint16_t*)malloc((size_t)rows * kvw * 2);
+    uint16_t* attn = (uint16_t*)malloc((size_t)rows * qw * 2);
+    uint16_t* proj = (uint16_t*)malloc((size_t)rows * H * 2);
+    uint16_t* gate = (uint16_t*)malloc((size_t)rows * I * 2);
+    uint16_t* up = (uint16_t*)malloc((size_t)rows * I * 2);
+    int* positions = (int*)malloc((size_t)rows * sizeof(int));
+    for (int r = 0; r < rows; ++r) positions[r] = r;
+    const int gemm_path = rows <= gemm_capacity;
+    uint16_t* scores = gemm_path ? (uint16_t*)malloc((size_t)rows * rows * 2) : NULL;
+    uint16_t* qh = gemm_path ? (uint16_t*)malloc((size_t)rows * hd * 2) : NULL;
+    uint16_t* kh = gemm_path ? (uint16_t*)malloc((size_t)rows * hd * 2) : NULL;
+    uint16_t* vt = gemm_path ? (uint16_t*)malloc((size_t)rows * hd * 2) : NULL;
+    uint16_t* oh = gemm_path ? (uint16_t*)malloc((size_t)rows * hd * 2) : NULL;
+    for (int li = 0; li < d->layers; ++li) {
+        const OrcLayer* L = &m->talker_layers[li];
+        uint16_t* kc = s->talker_k + (size_t)li * s->max_seq * kvw;
+        uint16_t* vc = s->talker_v + (size_t)li * s->max_seq * kvw;
+        orc_rms_norm_rows(hidden, L->input_norm, normalized, rows, H, m->rms_eps);
+        orc_bf16_gemm(normalized, L->q16, q, rows, qw, H, H, H, qw);
+        orc_bf16_gemm(normalized, L->k16, k, rows, kvw, H, H, H, kvw);
+        orc_bf16_gemm(normalized, L->v16, v, rows, kvw, H, H, H, kvw);
+        orc_head_rms_norm_rows(q, L->q_norm, rows, d->query_heads, hd, m->rms_eps);
+        orc_head_rms_norm_rows(k, L->k_norm, rows, d->key_value_heads, hd, m->rms_eps);
+        orc_rope_rows(q, rows, d->query_heads, hd, positions, m->rope_theta);
+        orc_rope_rows(k, rows, d->key_value_heads, hd, positions, m->rope_theta);
+        memcpy(kc, k, (size_t)rows * kvw * 2);
+        memcpy(vc, v, (size_t)rows * kvw * 2);
+        if (gemm_path) {
+            /* run_prefill_gqa_gemm, K/talker.cu:2750-2852: per query head,
+             * scores = bf16(q k^T), causal softmax, out = bf16(p v). */
+            for (int h = 0; h < d->query_heads; ++h) {
+                const int kvh = h / group;
+                for (int r = 0; r < rows; ++r) {
+                    memcpy(qh + (size_t)r * hd, q + (size_t)r * qw + (size_t)h * hd, (size_t)hd * 2);
+                    memcpy(kh + (size_t)r * hd, k + (size_t)r * kvw + (size_t)kvh * hd, (size_t)hd * 2);
+                    for (int t = 0; t < hd; ++t) vt[(size_t)t * rows + r] = v[(size_t)r * kvw + (size_t)kvh * hd + t];
+                }
+                orc_bf16_gemm(qh, kh, scores, rows, rows, hd, hd, hd, rows);
+                orc_causal_softmax(scores, 1, rows, rows, hd);
+                orc_bf16_gemm(scores, vt, oh, rows, hd, rows, rows, rows, hd);
+                for (int r = 0; r < rows; ++r) {
+                    memcpy(attn + (size_t)r * qw + (size_t)h * hd, oh + (size_t)r * hd, (size_t)hd * 2);
+                }
+            }
+        } else {
+            /* prefill_causal_gqa_attention_kernel, K/talker_kernels.cu:115-191:
+             * row r attends positions 0..r with the exact kernel's order. */
+            for (int r = 0; r < rows; ++r) {
+                orc_causal_gqa_attention(q + (size_t)r * qw, kc, vc, attn + (size_t)r * qw, d->query_heads,
+                                         d->key_value_heads, hd, r + 1);
+            }
+        }
+        orc_bf16_gemm(attn, L->o16, proj, rows, H, qw, qw, qw, H);
+        orc_add_in_place(hidden, proj, rows * H);
+        orc_rms_norm_rows(hidden, L->post_norm, normalized, rows, H, m->rms_eps);
+        orc_bf16_gemm(normalized, L->gate16, gate, rows, I, H, H, H, I);
+        orc_bf16_gemm(normalized, L->up16, up, rows, I, H, H, H, I);
+        orc_silu_gate(gate, up, rows * I);
+        orc_bf16_gemm(gate, L->down16, proj, rows, H, I, I, I, H);
+        orc_add_in_place(hidden, proj, rows * H);
+    }
+    free(normalized); free(q); free(k); free(v); free(attn); free(proj); free(gate); free(up); free(positions);
+    free(scores); free(qh); free(kh); free(vt); free(oh);
+}
+
+int orc_prefill_bf16(const OrcModel* m, OrcSession* s, const int* text_ids, const int* codec_ids,
+                     int count, const OrcSampling* sampling, int gemm_capacity) {
+    const int H = m->talker.hidden;
+    uint16_t* hidden = (uint16_t*)malloc((size_t)count * H * 2);
+    for (int i = 0; i < count; ++i) {
+        /* prepare_prompt_embedding, K/talker.cu:2721-2748 (int8 text projection) */
+        uint16_t* row = hidden + (size_t)i * H;
+        if (text_ids[i] >= 0) {
+            orc_project_text(m, text_ids[i], row);
+        } else {
+            memset(row, 0, (size_t)H * 2);
+        }
+        if (codec_ids[i] >= 0) orc_add_in_place(row, m->codec_embedding + (size_t)codec_ids[i] * H, H);
+    }
+    prefill_decoder(m, s, hidden, count, gemm_capacity);
+    /* run_talker_prefill, K/talker.cu:3204-3249: final norm of the last row,
+     * bf16 codec head GEMM (rows = 1). */
+    orc_rms_norm_rows(hidden + (size_t)(count - 1) * H, m->talker_norm, s->last_hidden, 1, H, m->rms_eps);
+    orc_bf16_gemm(s->last_hidden, m->codec_head16, s->logits, 1, m->talker_vocab, H, H, H, m->talker_vocab);
+    free(hidden);
+    s->position = count;
+    s->history_count = 0;
+    return sample_talker(m, s, sampling);
+}

@@ -103,6 +103,8 @@ typedef struct OrcLayer {
     const uint16_t *input_norm, *q_norm, *k_norm, *post_norm;
     const int8_t *q, *k, *v, *o, *gate_up, *down; /* gate_up: gate rows first */
     const float *q_s, *k_s, *v_s, *o_s, *gate_up_s, *down_s;
+    /* bf16 weights (the prefill's, K/talker.cu:2750-3202) */
+    const uint16_t *q16, *k16, *v16, *o16, *gate16, *up16, *down16;
 } OrcLayer;
 
 typedef struct OrcModel {
@@ -126,6 +128,7 @@ typedef struct OrcModel {
      * batched int8 decoder (K/talker.cu:2038-2334): fast attention, fma
      * residual epilogue, fused gate/up SiLU. */
     int batch_semantics;
+    const uint16_t* codec_head16; /* bf16 codec head (prefill logits) */
 } OrcModel;
 
 typedef struct OrcSession {
@@ -172,6 +175,25 @@ int orc_frame_step(const OrcModel* m, OrcSession* s, int semantic_token,
  * Returns the first semantic token. */
 int orc_prefill(const OrcModel* m, OrcSession* s, const int* text_ids,
                 const int* codec_ids, int count, const OrcSampling* sampling);
+
+/* ---- bf16 prefill (K/talker.cu:2750-3249) ------------------------------ */
+/* c[i][j] = bf16(sum_k a[i][k] * b[j][k]): fp32 fmaf chain in k order (the
+ * reference's cuBLAS order is unspecified; this is the oracle's own). */
+void orc_bf16_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int n, int k,
+                   int lda, int ldb, int ldc);
+/* Accumulation of orc_bf16_gemm: 0 (default) the fp32 chain above; 1 the sum
+ * in double rounded once -- a second valid order, used to measure how far
+ * two fp32 GEMM orders drift apart through a deep prefill. */
+void orc_set_gemm_order(int order);
+/* causal_softmax_kernel (K/talker_kernels.cu:232-260) on [heads][rows][stride]. */
+void orc_causal_softmax(uint16_t* scores, int heads, int rows, int stride, int head_dimension);
+/* run_talker_prefill with the prompt embeddings of prepare_prompt_embedding:
+ * fills the session's talker caches 0..count-1, last_hidden and logits, then
+ * samples the first semantic token.  Attention uses the GEMM path when count
+ * <= gemm_capacity (min(max_seq, 512) in the reference), else the exact
+ * per-row kernel. */
+int orc_prefill_bf16(const OrcModel* m, OrcSession* s, const int* text_ids, const int* codec_ids,
+                     int count, const OrcSampling* sampling, int gemm_capacity);
 
 #ifdef __cplusplus
 }

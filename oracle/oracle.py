@@ -205,3 +205,28 @@ def set_threads(threads: int) -> None:
     """Threads for the model-level GEMVs of large matrices (bit-identical
     results for any count)."""
     lib().orc_set_threads(int(threads))
+
+
+def bf16_gemm(a_bits, b_bits):
+    """c = bf16(a @ b^T) with the oracle's fp32 accumulation (k order)."""
+    a = _c(np.atleast_2d(a_bits), np.uint16)
+    b = _c(np.atleast_2d(b_bits), np.uint16)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.empty((m, n), np.uint16)
+    lib().orc_bf16_gemm(_p(a), _p(b), _p(c), m, n, k, k, k, n)
+    return c
+
+
+def causal_softmax(scores_bits, head_dimension):
+    """causal_softmax_kernel on [heads][rows][stride] bf16 scores (copy)."""
+    s = _c(scores_bits, np.uint16).copy()
+    heads, rows, stride = s.shape
+    lib().orc_causal_softmax(_p(s), heads, rows, stride, head_dimension)
+    return s
+
+
+def set_gemm_order(order: int) -> None:
+    """0: the bf16 GEMM's fp32 chain in k order (default); 1: accumulated in
+    double and rounded once."""
+    lib().orc_set_gemm_order(int(order))

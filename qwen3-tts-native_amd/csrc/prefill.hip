@@ -1,0 +1,309 @@
+// bf16 prompt prefill for gfx950: the reference's prefill runs the talker's
+// bf16 weights through cuBLAS GEMMs with fp32 accumulation and bf16 outputs
+// (native/qwen3-tts-native/native/src/talker.cu:2637-2674, 2750-3249).  Here
+// every such product is one MFMA kernel, gemm_bf16_kernel:
+//
+//   C[m][n] = bf16( sum_k A[m][k] * B[n][k] )      (fp32 accumulation)
+//
+// with A and B row-major and K contiguous in both (activations x weights^T,
+// queries x keys^T, probabilities x values^T), batched over heads through
+// gridDim.z with a grouped B index for GQA.  A 128x128 block tile of 256
+// threads (4 waves, 64x64 each = 4x4 v_mfma_f32_16x16x32_bf16 tiles), K in
+// steps of 64 staged through double-buffered LDS (padded rows), the next
+// step's global loads issued before the current step's MFMAs.
+//
+// The summation order of an fp32 GEMM is not the reference's (cuBLAS leaves
+// it unspecified), so this path is compared with tolerances; everything
+// around the GEMMs (causal softmax, head norm, RoPE, residual adds, SiLU
+// gate) reproduces the reference's operation order exactly.
+#include <algorithm>
+
+#include "q3_common.hpp"
+#include "q3_math.h"
+#include "head_device.hpp"
+
+namespace q3 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
+constexpr int kGemmThreads = 256;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// One 16-byte chunk (8 consecutive k) of row `row` at column `col`, zero past
+// the matrix (rows >= limit or k >= k_limit; K is a multiple of 8).
+__device__ __forceinline__ uint4 load_chunk(const bf16_t* base, int ld, int row, int limit, int col, int k_limit) {
+    uint4 v{0u, 0u, 0u, 0u};
+    if (row < limit && col < k_limit) v = *reinterpret_cast<const uint4*>(base + static_cast<size_t>(row) * ld + col);
+    return v;
+}
+
+__global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g) {
+    __shared__ __align__(16) bf16_t as[2][kBM * kLdsRow];
+    __shared__ __align__(16) bf16_t bs[2][kBN * kLdsRow];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int m0 = blockIdx.y * kBM;
+    const int n0 = blockIdx.x * kBN;
+    const int z = blockIdx.z;
+    const bf16_t* a = g.a + static_cast<size_t>(z) * g.a_batch;
+    const bf16_t* b = g.b + static_cast<size_t>(z / g.b_group) * g.b_batch;
+    bf16_t* c = g.c + static_cast<size_t>(z) * g.c_batch;
+
+    // Global -> LDS: 128 rows x 8 chunks per operand, 4 chunks per thread.
+    uint4 ra[4], rb[4];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int chunk = tid + i * kGemmThreads;
+            const int row = chunk >> 3;
+            const int col = k0 + (chunk & 7) * 8;
+            ra[i] = load_chunk(a, g.lda, m0 + row, g.m, col, g.k);
+            rb[i] = load_chunk(b, g.ldb, n0 + row, g.n, col, g.k);
+        }
+    };
+    auto stage = [&](int buffer) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int chunk = tid + i * kGemmThreads;
+            const int row = chunk >> 3;
+            const int col = (chunk & 7) * 8;
+            *reinterpret_cast<uint4*>(&as[buffer][row * kLdsRow + col]) = ra[i];
+            *reinterpret_cast<uint4*>(&bs[buffer][row * kLdsRow + col]) = rb[i];
+        }
+    };
+
+    const int wm = (wave >> 1) * 64;  // wave tile origin inside the block tile
+    const int wn = (wave & 1) * 64;
+    const int m = lane & 15;
+    const int group = lane >> 4;
+    floatx4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int steps = (g.k + kBK - 1) / kBK;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int buffer = s & 1;
+        if (s + 1 < steps) fetch((s + 1) * kBK);  // in flight under the MFMAs
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 32) {
+            bf16x8_t af[4], bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&as[buffer][(wm + 16 * i + m) * kLdsRow + kk + 8 * group]));
+                bfr[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&bs[buffer][(wn + 16 * i + m) * kLdsRow + kk + 8 * group]));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (s + 1 < steps) {
+            stage(buffer ^ 1);
+            __syncthreads();
+        }
+    }
+    // acc[i][j][r] = C[wm + 16 i + 4 group + r][wn + 16 j + m]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm + 16 * i + 4 * group + r;
+            if (row >= g.m) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + wn + 16 * j + m;
+                if (col < g.n) c[static_cast<size_t>(row) * g.ldc + col] = f2bf(acc[i][j][r]);
+            }
+        }
+    }
+}
+
+// causal_softmax_kernel (talker_kernels.cu:232-260) on bf16 scores
+// [heads][rows][stride]: scaled = bf16(s * (1/sqrt(d))); maximum over keys
+// 0..query; denominator = sequential fp32 sum of exp(scaled - max); p =
+// bf16(exp(scaled - max) * (1/denominator)); keys query+1 .. stride-1 = 0.
+// One wave per (head, query) row: the wave computes the exponentials in
+// parallel (into LDS), lane 0 sums them in key order.
+__global__ __launch_bounds__(64) void causal_softmax_kernel(bf16_t* scores, int rows, int stride, float scale) {
+    __shared__ float e[kPrefillAttentionRows];
+    __shared__ float inverse_lds;
+    const int query = blockIdx.x;
+    bf16_t* row = scores + (static_cast<size_t>(blockIdx.y) * rows + query) * stride;
+    const int lane = threadIdx.x;
+    const int count = query + 1;
+    float maximum = -__int_as_float(0x7f800000);
+    for (int key = lane; key < count; key += 64) {
+        const float scaled = round_bf(bf2f(row[key]) * scale);
+        e[key] = scaled;
+        maximum = fmaxf(maximum, scaled);
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, offset, 64));
+    for (int key = lane; key < count; key += 64) e[key] = q3_expf(e[key] - maximum);
+    __syncthreads();
+    if (lane == 0) {
+        float denominator = 0.0f;
+        for (int key = 0; key < count; ++key) denominator += e[key];
+        inverse_lds = 1.0f / denominator;
+    }
+    __syncthreads();
+    const float inverse = inverse_lds;
+    for (int key = lane; key < stride; key += 64) row[key] = key < count ? f2bf(e[key] * inverse) : f2bf(0.0f);
+}
+
+// The QKV epilogue of a prompt of `rows` positions starting at `first`: per
+// (row, head) of the fused [rows][q | k | v] projection, head RMSNorm and
+// RoPE on q and k heads in place (the decode path's exact arithmetic and
+// RoPE table); k heads also to the key cache ([position][kv_width]), v heads
+// to the blocked dimension-major value cache.  One wave per head.
+__global__ __launch_bounds__(64) void prefill_qkv_epilogue_kernel(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm,
+                                                                  const bf16_t* rope_table, bf16_t* key_cache,
+                                                                  bf16_t* value_cache, int value_stride, int first,
+                                                                  int query_heads, int key_value_heads, float epsilon) {
+    constexpr int kDim = 128;
+    const int heads = query_heads + 2 * key_value_heads;
+    const int row = blockIdx.x / heads;
+    const int head = blockIdx.x % heads;
+    const int lane = threadIdx.x;
+    const int q_width = query_heads * kDim;
+    const int kv_width = key_value_heads * kDim;
+    const int position = first + row;
+    bf16_t* base = qkv + static_cast<size_t>(row) * (q_width + 2 * kv_width) + static_cast<size_t>(head) * kDim;
+    if (head >= query_heads + key_value_heads) {
+        const int vh = head - query_heads - key_value_heads;
+        for (int d = lane; d < kDim; d += 64) {
+            const size_t index = ((static_cast<size_t>(vh) * (value_stride >> 3) + (position >> 3)) * kDim + d) * 8 +
+                                 (position & 7);
+            value_cache[index] = base[d];
+        }
+        return;
+    }
+    const bool is_query = head < query_heads;
+    bf16_t out0, out1;
+    head_detail::norm_rope_head(base, is_query ? q_norm : k_norm, rope_table + static_cast<size_t>(position) * kDim,
+                                epsilon, out0, out1);
+    base[lane] = out0;
+    base[lane + 64] = out1;
+    if (!is_query) {
+        bf16_t* dst = key_cache + static_cast<size_t>(position) * kv_width + static_cast<size_t>(head - query_heads) * kDim;
+        dst[lane] = out0;
+        dst[lane + 64] = out1;
+    }
+}
+
+// vt[h][d][j] = v(row j, head h, dim d) for j < rows, 0 for rows <= j < stride.
+__global__ __launch_bounds__(256) void transpose_values_kernel(const bf16_t* qkv, int qkv_width, int v_offset, int rows,
+                                                               int stride, int key_value_heads, bf16_t* vt) {
+    const size_t total = static_cast<size_t>(key_value_heads) * 128 * stride;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int j = static_cast<int>(t % stride);
+        const int hd = static_cast<int>(t / stride);  // h * 128 + d
+        vt[t] = j < rows ? qkv[static_cast<size_t>(j) * qkv_width + v_offset + hd] : f2bf(0.0f);
+    }
+}
+
+// Prompt rows: out[r] = (text[r] >= 0 ? projected[r] : 0), then + the codec
+// embedding of codec[r] when codec[r] >= 0 (bf16 add), as the reference's
+// prepare_prompt_embedding (talker.cu:2721-2748).
+__global__ __launch_bounds__(256) void prompt_rows_kernel(bf16_t* rows_data, const int* text, const int* codec,
+                                                          const bf16_t* codec_embedding, int codec_vocabulary,
+                                                          int width) {
+    const int r = blockIdx.y;
+    bf16_t* out = rows_data + static_cast<size_t>(r) * width;
+    const bool has_text = text[r] >= 0;
+    const int token = codec[r];
+    const bool has_codec = token >= 0 && token < codec_vocabulary;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += gridDim.x * blockDim.x) {
+        float v = has_text ? bf2f(out[i]) : 0.0f;
+        if (has_codec) v = round_bf(v + bf2f(codec_embedding[static_cast<size_t>(token) * width + i]));
+        out[i] = f2bf(v);
+    }
+}
+
+// Text-embedding rows of the prompt (row 0 for positions without text; their
+// projection is discarded by prompt_rows_kernel).
+__global__ __launch_bounds__(256) void gather_text_rows_kernel(const bf16_t* table, const int* text, int vocabulary,
+                                                               int width, bf16_t* out) {
+    const int r = blockIdx.y;
+    const int token = text[r] >= 0 && text[r] < vocabulary ? text[r] : 0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < width; i += gridDim.x * blockDim.x) {
+        out[static_cast<size_t>(r) * width + i] = table[static_cast<size_t>(token) * width + i];
+    }
+}
+
+}  // namespace
+
+hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
+    if (g.a == nullptr || g.b == nullptr || g.c == nullptr || g.m <= 0 || g.n <= 0 || g.k <= 0 || g.batch <= 0 ||
+        g.b_group <= 0 || g.k % 8 != 0 || g.lda % 8 != 0 || g.ldb % 8 != 0 || g.lda < g.k || g.ldb < g.k ||
+        g.ldc < g.n) {
+        return hipErrorInvalidValue;
+    }
+    const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);
+    if ((align & 15u) != 0 || (g.a_batch % 8) != 0 || (g.b_batch % 8) != 0) return hipErrorInvalidValue;
+    const dim3 grid((g.n + kBN - 1) / kBN, (g.m + kBM - 1) / kBM, g.batch);
+    gemm_bf16_kernel<<<grid, kGemmThreads, 0, stream>>>(g);
+    return hipGetLastError();
+}
+
+hipError_t launch_causal_softmax(bf16_t* scores, int heads, int rows, int stride, int head_dimension,
+                                 hipStream_t stream) {
+    if (scores == nullptr || heads <= 0 || rows <= 0 || rows > kPrefillAttentionRows || stride < rows ||
+        head_dimension <= 0) {
+        return hipErrorInvalidValue;
+    }
+    const float scale = 1.0f / sqrtf(static_cast<float>(head_dimension));
+    causal_softmax_kernel<<<dim3(rows, heads), 64, 0, stream>>>(scores, rows, stride, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_qkv_epilogue(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const bf16_t* rope_table,
+                                       bf16_t* key_cache, bf16_t* value_cache, int value_stride, int first, int rows,
+                                       int query_heads, int key_value_heads, float epsilon, hipStream_t stream) {
+    if (rows <= 0 || query_heads <= 0 || key_value_heads <= 0 || value_stride % 8 != 0) return hipErrorInvalidValue;
+    const int heads = query_heads + 2 * key_value_heads;
+    prefill_qkv_epilogue_kernel<<<rows * heads, 64, 0, stream>>>(qkv, q_norm, k_norm, rope_table, key_cache, value_cache,
+                                                                 value_stride, first, query_heads, key_value_heads,
+                                                                 epsilon);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_values(const bf16_t* qkv, int qkv_width, int v_offset, int rows, int stride,
+                                   int key_value_heads, bf16_t* vt, hipStream_t stream) {
+    if (rows <= 0 || stride < rows || key_value_heads <= 0) return hipErrorInvalidValue;
+    const size_t total = static_cast<size_t>(key_value_heads) * 128 * stride;
+    const int blocks = static_cast<int>(std::min<size_t>((total + 255) / 256, 4096));
+    transpose_values_kernel<<<blocks, 256, 0, stream>>>(qkv, qkv_width, v_offset, rows, stride, key_value_heads, vt);
+    return hipGetLastError();
+}
+
+hipError_t launch_prompt_rows(bf16_t* rows_data, const int* text, const int* codec, const bf16_t* codec_embedding,
+                              int codec_vocabulary, int rows, int width, hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    prompt_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(rows_data, text, codec, codec_embedding,
+                                                                            codec_vocabulary, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_text_rows(const bf16_t* table, const int* text, int vocabulary, int rows, int width,
+                                   bf16_t* out, hipStream_t stream) {
+    if (rows <= 0 || width <= 0) return hipErrorInvalidValue;
+    gather_text_rows_kernel<<<dim3((width + 255) / 256, rows), 256, 0, stream>>>(table, text, vocabulary, width, out);
+    return hipGetLastError();
+}
+
+}  // namespace q3

@@ -343,6 +343,40 @@ hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int voc
                                  int vocabulary, int width, const int* tokens, bf16_t* output,
                                  hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// bf16 prefill (prefill.hip)
+// ---------------------------------------------------------------------------
+// C[m][n] = bf16(sum_k A[m][k] * B[n][k]) with fp32 accumulation; A, B, C
+// row-major with leading dimensions lda, ldb, ldc (elements).  Batch z uses
+// A + z * a_batch, B + (z / b_group) * b_batch, C + z * c_batch.  K, lda,
+// ldb, a_batch and b_batch must be multiples of 8 and A, B 16-byte aligned.
+struct Bf16GemmArgs {
+    const bf16_t* a = nullptr;
+    const bf16_t* b = nullptr;
+    bf16_t* c = nullptr;
+    int m = 0, n = 0, k = 0;
+    int lda = 0, ldb = 0, ldc = 0;
+    int batch = 1;
+    int b_group = 1;
+    long long a_batch = 0, b_batch = 0, c_batch = 0;
+};
+hipError_t launch_bf16_gemm(const Bf16GemmArgs& args, hipStream_t stream);
+// Prompts of at most this many positions run the reference's GEMM attention
+// (scores materialized, causal softmax); longer ones the exact per-row kernel
+// (talker.cu:3035-3054 with kPrefillGemmCapacity = 512).
+constexpr int kPrefillAttentionRows = 512;
+hipError_t launch_causal_softmax(bf16_t* scores, int heads, int rows, int stride, int head_dimension,
+                                 hipStream_t stream);
+hipError_t launch_prefill_qkv_epilogue(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const bf16_t* rope_table,
+                                       bf16_t* key_cache, bf16_t* value_cache, int value_stride, int first, int rows,
+                                       int query_heads, int key_value_heads, float epsilon, hipStream_t stream);
+hipError_t launch_transpose_values(const bf16_t* qkv, int qkv_width, int v_offset, int rows, int stride,
+                                   int key_value_heads, bf16_t* vt, hipStream_t stream);
+hipError_t launch_prompt_rows(bf16_t* rows_data, const int* text, const int* codec, const bf16_t* codec_embedding,
+                              int codec_vocabulary, int rows, int width, hipStream_t stream);
+hipError_t launch_gather_text_rows(const bf16_t* table, const int* text, int vocabulary, int rows, int width,
+                                   bf16_t* out, hipStream_t stream);
+
 // Lockstep-batch glue: rows of a batch from / to per-session buffers.
 hipError_t launch_gather_rows(const bf16_t* const* sources, int rows, int width, bf16_t* output,
                               hipStream_t stream);

@@ -710,6 +710,34 @@ QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention_noalloc_v1(
                          "decode attention (no allocation)", error, cap);
 }
 
+QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_v1(const uint16_t* a, const uint16_t* b, uint16_t* c, int32_t m,
+                                                int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t ldc,
+                                                int32_t batch, int32_t b_group, int64_t a_batch, int64_t b_batch,
+                                                int64_t c_batch, void* stream, char* error, size_t cap) {
+    Bf16GemmArgs g;
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    g.batch = batch;
+    g.b_group = b_group;
+    g.a_batch = a_batch;
+    g.b_batch = b_batch;
+    g.c_batch = c_batch;
+    return launch_status(launch_bf16_gemm(g, as_stream(stream)), "bf16 GEMM", error, cap);
+}
+
+QWEN3_TTS_API int32_t qwen3_tts_op_causal_softmax_v1(uint16_t* scores, int32_t heads, int32_t rows, int32_t stride,
+                                                     int32_t head_dimension, void* stream, char* error, size_t cap) {
+    return launch_status(launch_causal_softmax(scores, heads, rows, stride, head_dimension, as_stream(stream)),
+                         "causal softmax", error, cap);
+}
+
 QWEN3_TTS_API int32_t qwen3_tts_op_kv_scatter_rows(const uint16_t* rows_data, uint16_t* const* cache_bases,
                                                    const int32_t* positions, int32_t rows, int32_t width,
                                                    int32_t row_stride, void* stream, char* error, size_t cap) {

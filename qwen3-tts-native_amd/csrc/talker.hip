@@ -146,6 +146,9 @@ struct Layer {
     const bf16_t* q_norm = nullptr;
     const bf16_t* k_norm = nullptr;
     QTensor qkv, o, gate_up, down;
+    // bf16 weights ([out][in], as uploaded): the prompt prefill's GEMMs
+    const bf16_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr, *o16 = nullptr;
+    const bf16_t *gate16 = nullptr, *up16 = nullptr, *down16 = nullptr;
 };
 
 struct DeviceTensor {
@@ -274,6 +277,7 @@ public:
         text_fc2_bias_ = require("talker.text_projection.linear_fc2.bias", {H});
         talker_norm_ = require("talker.model.norm.weight", {H});
         const bf16_t* codec_head = require("talker.codec_head.weight", {uint64_t(cfg_.talker_vocab), H});
+        codec_head16_ = codec_head;
         const bf16_t* small = require("talker.code_predictor.small_to_mtp_projection.weight",
                                       {uint64_t(P.hidden), H});
         small_to_mtp_bias_ = require("talker.code_predictor.small_to_mtp_projection.bias", {uint64_t(P.hidden)});
@@ -307,6 +311,13 @@ public:
             s.gate = require(prefix + ".mlp.gate_proj.weight", {in, h});
             s.up = require(prefix + ".mlp.up_proj.weight", {in, h});
             s.down = require(prefix + ".mlp.down_proj.weight", {h, in});
+            l.q16 = s.q;
+            l.k16 = s.k;
+            l.v16 = s.v;
+            l.o16 = s.o;
+            l.gate16 = s.gate;
+            l.up16 = s.up;
+            l.down16 = s.down;
             layers.push_back(l);
             sources.push_back(s);
         };
@@ -444,6 +455,7 @@ private:
     DeviceBuffer int8_arena_, scale_arena_, embedding_tables_, rope_table_;
     std::vector<Layer> talker_layers_, predictor_layers_;
     QTensor text_fc1_, text_fc2_, small_to_mtp_, codec_head_;
+    const bf16_t* codec_head16_ = nullptr;
     std::array<QTensor, kResidualCodebooks> predictor_heads_{};
     const bf16_t* codec_embedding_ = nullptr;
     const bf16_t* text_embedding_ = nullptr;
@@ -606,8 +618,10 @@ public:
         check_hip(hipStreamSynchronize(stream_), "synchronize reset");
     }
 
-    // Prefill, talker.cu:1036-1093.  Prompt tokens run through the int8 decode
-    // step one position at a time (the reference runs bf16 GEMMs here).
+    // Prefill, talker.cu:1036-1093.  By default the reference's bf16 prefill
+    // (talker.cu:2750-3249): the prompt's rows through the bf16 weights as
+    // MFMA GEMMs.  QWEN3_TTS_PREFILL=decode selects the int8 decode step run
+    // once per prompt position instead (the decode path's numerics).
     Qwen3TtsTalkerPrefillResult prefill(const int32_t* text, const int32_t* codec, int count,
                                         const Qwen3TtsSamplingConfig& sampling) {
         check_hip(hipSetDevice(device_), "hipSetDevice(prefill)");
@@ -637,7 +651,12 @@ public:
             history_count_ = 0;
             check_hip(hipEventRecord(start_, stream_), "hipEventRecord(prefill start)");
             const int H = cfg_.talker.hidden;
-            for (int i = 0; i < count; ++i) {
+            const bool bf16 = bf16_prefill_enabled();
+            if (bf16) {
+                prefill_bf16(count, prompt.as<int>(), prompt.as<int>() + count);
+                emit_prefill_logits(count);
+            }
+            for (int i = 0; !bf16 && i < count; ++i) {
                 const int* text_id = prompt.as<int>() + i;
                 const int* codec_id = prompt.as<int>() + count + i;
                 if (text[i] >= 0) {
@@ -652,7 +671,7 @@ public:
                 run_decoder(false, position_ptr(), 0);
                 check_hip(launch_increment(position_ptr(), stream_), "advance position");
             }
-            emit_talker_logits();
+            if (!bf16) emit_talker_logits();
             sample_talker(sp);
             check_hip(hipEventRecord(stop_, stream_), "hipEventRecord(prefill stop)");
             position_ = count;
@@ -674,6 +693,160 @@ public:
             (void)hipStreamSynchronize(stream_);
             throw;
         }
+    }
+
+    static bool bf16_prefill_enabled() {
+        const char* v = std::getenv("QWEN3_TTS_PREFILL");
+        return v == nullptr || std::strcmp(v, "decode") != 0;
+    }
+
+    // The prompt's rows through the talker with the bf16 weights
+    // (run_decoder_prefill, talker.cu:2854-3202): every projection one MFMA
+    // GEMM over all rows; attention through materialized scores and the
+    // causal softmax when the prompt fits kPrefillAttentionRows and the
+    // session capacity (talker.cu:3035), else the exact per-row kernel.
+    // Leaves the rows' final hidden states in prefill_.hidden.
+    void prefill_bf16(int rows, const int* text_ids, const int* codec_ids) {
+        const Dims& T = cfg_.talker;
+        const int H = T.hidden, I = T.intermediate, qw = T.query_width(), kvw = T.kv_width();
+        const int qkvw = T.qkv_width(), hd = T.head_dimension;
+        const int rp = (rows + 7) / 8 * 8;
+        const bool gemm_attention = rows <= std::min(max_seq_, kPrefillAttentionRows);
+        PrefillBuffers& w = prefill_;
+        w.ensure(rows, H, I, qkvw, qw, T.query_heads, T.key_value_heads, gemm_attention ? rp : 0,
+                 gemm_attention ? 0 : max_seq_);
+        bf16_t* hidden = w.hidden.as<bf16_t>();
+        // prompt embeddings: int8 text projection (exact order, 8 rows a
+        // launch), then zero text-less rows and add codec embeddings
+        check_hip(launch_gather_text_rows(m_.text_embedding_, text_ids, cfg_.text_vocab, rows, H, w.normalized.as<bf16_t>(),
+                                          stream_),
+                  "gather prompt text embeddings");
+        for (int r0 = 0; r0 < rows; r0 += 8) {
+            const int n = std::min(8, rows - r0);
+            Gemv(m_.text_fc1_, w.normalized.as<bf16_t>() + static_cast<size_t>(r0) * H, H, H, kEpiBiasSilu)
+                .bias(m_.text_fc1_bias_).rows(n, kModeExact).to(w.proj.as<bf16_t>() + static_cast<size_t>(r0) * H)
+                .run(stream_, "prompt text fc1");
+            Gemv(m_.text_fc2_, w.proj.as<bf16_t>() + static_cast<size_t>(r0) * H, H, H, kEpiBias)
+                .bias(m_.text_fc2_bias_).rows(n, kModeExact).to(hidden + static_cast<size_t>(r0) * H)
+                .run(stream_, "prompt text fc2");
+        }
+        check_hip(launch_prompt_rows(hidden, text_ids, codec_ids, m_.codec_embedding_, cfg_.talker_vocab, rows, H, stream_),
+                  "prompt rows");
+        auto gemm = [&](const bf16_t* a, int lda, const bf16_t* weight, bf16_t* c, int ldc, int n, int k,
+                        const char* what) {
+            Bf16GemmArgs g;
+            g.a = a;
+            g.b = weight;
+            g.c = c;
+            g.m = rows;
+            g.n = n;
+            g.k = k;
+            g.lda = lda;
+            g.ldb = k;
+            g.ldc = ldc;
+            check_hip(launch_bf16_gemm(g, stream_), what);
+        };
+        bf16_t* xn = w.normalized.as<bf16_t>();
+        bf16_t* qkv = w.qkv.as<bf16_t>();
+        bf16_t* attn = w.attn.as<bf16_t>();
+        bf16_t* proj = w.proj.as<bf16_t>();
+        bf16_t* gate = w.gate.as<bf16_t>();
+        bf16_t* up = w.up.as<bf16_t>();
+        const int vstride = value_cache_stride(max_seq_);
+        for (int l = 0; l < T.layers; ++l) {
+            const Layer& L = m_.talker_layers_[l];
+            bf16_t* kc = host_bases_[l];
+            bf16_t* vc = host_bases_[T.layers + l];
+            check_hip(launch_rms_norm_rows(hidden, L.input_norm, xn, rows, H, cfg_.eps, stream_), "prefill input norm");
+            gemm(xn, H, L.q16, qkv, qkvw, qw, H, "prefill q GEMM");
+            gemm(xn, H, L.k16, qkv + qw, qkvw, kvw, H, "prefill k GEMM");
+            gemm(xn, H, L.v16, qkv + qw + kvw, qkvw, kvw, H, "prefill v GEMM");
+            check_hip(launch_prefill_qkv_epilogue(qkv, L.q_norm, L.k_norm, m_.rope_table_.as<bf16_t>(), kc, vc, vstride, 0,
+                                                  rows, T.query_heads, T.key_value_heads, cfg_.eps, stream_),
+                      "prefill q/k norm + RoPE + cache");
+            if (gemm_attention) {
+                bf16_t* scores = w.scores.as<bf16_t>();
+                bf16_t* vt = w.values_t.as<bf16_t>();
+                Bf16GemmArgs s;  // scores[h] = q_h k_h^T
+                s.a = qkv;
+                s.lda = qkvw;
+                s.a_batch = hd;
+                s.b = qkv + qw;
+                s.ldb = qkvw;
+                s.b_batch = hd;
+                s.b_group = T.query_heads / T.key_value_heads;
+                s.c = scores;
+                s.ldc = rp;
+                s.c_batch = static_cast<long long>(rows) * rp;
+                s.m = rows;
+                s.n = rows;
+                s.k = hd;
+                s.batch = T.query_heads;
+                check_hip(launch_bf16_gemm(s, stream_), "prefill score GEMM");
+                check_hip(launch_causal_softmax(scores, T.query_heads, rows, rp, hd, stream_), "prefill causal softmax");
+                check_hip(launch_transpose_values(qkv, qkvw, qw + kvw, rows, rp, T.key_value_heads, vt, stream_),
+                          "prefill value transpose");
+                Bf16GemmArgs o;  // out_h = p_h v_h
+                o.a = scores;
+                o.lda = rp;
+                o.a_batch = static_cast<long long>(rows) * rp;
+                o.b = vt;
+                o.ldb = rp;
+                o.b_batch = static_cast<long long>(hd) * rp;
+                o.b_group = T.query_heads / T.key_value_heads;
+                o.c = attn;
+                o.ldc = qw;
+                o.c_batch = hd;
+                o.m = rows;
+                o.n = hd;
+                o.k = rp;
+                o.batch = T.query_heads;
+                check_hip(launch_bf16_gemm(o, stream_), "prefill value GEMM");
+            } else {
+                // the exact kernel, row r over positions 0..r, in chunks that
+                // bound the score workspace
+                for (int r0 = 0; r0 < rows; r0 += kPrefillChunk) {
+                    const int n = std::min(kPrefillChunk, rows - r0);
+                    check_hip(launch_attention(true, qkv + static_cast<size_t>(r0) * qkvw, qkvw, nullptr, nullptr, kc, vc,
+                                               w.positions.as<int>() + r0, 0, attn + static_cast<size_t>(r0) * qw, n,
+                                               T.query_heads, T.key_value_heads, hd, max_seq_, w.workspace.as<float>(),
+                                               nullptr, stream_),
+                              "prefill exact attention");
+                }
+            }
+            gemm(attn, qw, L.o16, proj, H, H, qw, "prefill O GEMM");
+            check_hip(launch_add_in_place(hidden, proj, rows * H, stream_), "prefill attention residual");
+            check_hip(launch_rms_norm_rows(hidden, L.post_norm, xn, rows, H, cfg_.eps, stream_), "prefill post norm");
+            gemm(xn, H, L.gate16, gate, I, I, H, "prefill gate GEMM");
+            gemm(xn, H, L.up16, up, I, I, H, "prefill up GEMM");
+            check_hip(launch_silu_gate(gate, up, rows * I, stream_), "prefill SiLU gate");
+            gemm(gate, I, L.down16, proj, H, H, I, "prefill down GEMM");
+            check_hip(launch_add_in_place(hidden, proj, rows * H, stream_), "prefill MLP residual");
+        }
+    }
+
+    // run_talker_prefill's tail (talker.cu:3204-3231): final norm of the last
+    // row into last_hidden, bf16 codec head GEMM into the logits; position =
+    // prompt length.
+    void emit_prefill_logits(int rows) {
+        const int H = cfg_.talker.hidden;
+        check_hip(launch_rms_norm_rows(prefill_.hidden.as<bf16_t>() + static_cast<size_t>(rows - 1) * H, m_.talker_norm_,
+                                       last_hidden_.as<bf16_t>(), 1, H, cfg_.eps, stream_),
+                  "prefill final norm");
+        Bf16GemmArgs g;
+        g.a = last_hidden_.as<bf16_t>();
+        g.b = m_.codec_head16_;
+        g.c = logits_.as<bf16_t>();
+        g.m = 1;
+        g.n = cfg_.talker_vocab;
+        g.k = H;
+        g.lda = H;
+        g.ldb = H;
+        g.ldc = cfg_.talker_vocab;
+        check_hip(launch_bf16_gemm(g, stream_), "prefill codec head GEMM");
+        pinned_[1] = rows;
+        check_hip(hipMemcpyAsync(ints_.as<int>(), &pinned_[1], sizeof(int), hipMemcpyHostToDevice, stream_),
+                  "set position");
     }
 
     // begin_frame, talker.cu:1095-1262
@@ -769,6 +942,36 @@ public:
         check_hip(hipMemcpy(destination, last_hidden_.as<void>(), need, hipMemcpyDeviceToHost), "read last hidden");
     }
 
+    // Diagnostics: positions 0..count-1 of talker layer `layer`'s key (which
+    // 0) or value (which 1) cache as [position][kv_width] bf16.
+    void read_talker_cache(int layer, int which, int count, void* destination, uint64_t bytes) {
+        const Dims& T = cfg_.talker;
+        const int kvw = T.kv_width();
+        if (layer < 0 || layer >= T.layers || (which != 0 && which != 1) || count <= 0 || count > max_seq_ ||
+            destination == nullptr || bytes != static_cast<uint64_t>(count) * kvw * sizeof(bf16_t)) {
+            throw std::invalid_argument("cache read needs a layer, which (0 key, 1 value) and count * kv_width bf16");
+        }
+        if (frame_in_flight_) throw std::runtime_error("a device frame lease is in flight");
+        check_hip(hipSetDevice(device_), "hipSetDevice(read cache)");
+        check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize(read cache)");
+        if (which == 0) {
+            check_hip(hipMemcpy(destination, host_bases_[layer], bytes, hipMemcpyDeviceToHost), "read key cache");
+            return;
+        }
+        const int stride = value_cache_stride(max_seq_);
+        std::vector<bf16_t> blocked(static_cast<size_t>(kvw) * stride);
+        check_hip(hipMemcpy(blocked.data(), host_bases_[T.layers + layer], blocked.size() * sizeof(bf16_t),
+                            hipMemcpyDeviceToHost),
+                  "read value cache");
+        bf16_t* out = static_cast<bf16_t*>(destination);
+        for (int p = 0; p < count; ++p) {
+            for (int c = 0; c < kvw; ++c) {
+                out[static_cast<size_t>(p) * kvw + c] =
+                    blocked[((static_cast<size_t>(c >> 7) * (stride >> 3) + (p >> 3)) * 128 + (c & 127)) * 8 + (p & 7)];
+            }
+        }
+    }
+
     Qwen3TtsTalkerStateInfo state_info() const {
         Qwen3TtsTalkerStateInfo r{};
         r.abi_version = QWEN3_TTS_TALKER_ABI_VERSION;
@@ -834,6 +1037,40 @@ private:
         v.device_index = device_;
         return v;
     }
+
+    // Row buffers of the bf16 prefill, grown on demand and kept.
+    static constexpr int kPrefillChunk = 128;  // rows per exact-attention launch
+    struct PrefillBuffers {
+        DeviceBuffer hidden, normalized, qkv, attn, proj, gate, up, scores, values_t, positions, workspace;
+        int rows = 0, score_stride = 0, capacity = 0;
+        void ensure(int r, int H, int I, int qkvw, int qw, int query_heads, int kv_heads, int rp, int exact_capacity) {
+            const size_t b = sizeof(bf16_t);
+            if (r > rows) {
+                hidden = DeviceBuffer(static_cast<size_t>(r) * H * b);
+                normalized = DeviceBuffer(static_cast<size_t>(r) * H * b);
+                qkv = DeviceBuffer(static_cast<size_t>(r) * qkvw * b);
+                attn = DeviceBuffer(static_cast<size_t>(r) * qw * b);
+                proj = DeviceBuffer(static_cast<size_t>(r) * H * b);
+                gate = DeviceBuffer(static_cast<size_t>(r) * I * b);
+                up = DeviceBuffer(static_cast<size_t>(r) * I * b);
+                rows = r;
+            }
+            if (rp > score_stride) {  // GEMM attention: scores, transposed values
+                scores = DeviceBuffer(static_cast<size_t>(query_heads) * rp * rp * b);
+                values_t = DeviceBuffer(static_cast<size_t>(kv_heads) * 128 * rp * b);
+                score_stride = rp;
+            }
+            if (exact_capacity > capacity) {  // exact attention: positions, score workspace
+                std::vector<int> ids(static_cast<size_t>(exact_capacity));
+                for (int i = 0; i < exact_capacity; ++i) ids[i] = i;
+                positions = DeviceBuffer(ids.size() * sizeof(int));
+                check_hip(hipMemcpy(positions.as<void>(), ids.data(), ids.size() * sizeof(int), hipMemcpyHostToDevice),
+                          "upload prefill positions");
+                workspace = DeviceBuffer(attention_workspace_bytes(kPrefillChunk, query_heads, exact_capacity));
+                capacity = exact_capacity;
+            }
+        }
+    };
 
     struct Graph {
         hipGraphExec_t exec = nullptr;
@@ -1016,6 +1253,7 @@ private:
     std::vector<bf16_t*> host_bases_;
     int* pinned_ = nullptr;  // [0] sampled token, [1] text token, [8..] codes (u16)
     Graph predictor_graph_, talker_graph_;
+    PrefillBuffers prefill_;
     int position_ = 0;
     int history_count_ = 0;
     uint64_t frames_ = 0, device_samples_ = 0, host_syncs_ = 0;
@@ -1669,6 +1907,13 @@ QWEN3_TTS_API int32_t qwen3_tts_session_state_info(Qwen3TtsSessionHandle handle,
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
     }
     return protect([&] { *output = session_of(handle)->state_info(); }, QWEN3_TTS_TALKER_STATUS_STATE, error, cap);
+}
+
+QWEN3_TTS_API int32_t qwen3_tts_session_read_talker_cache_v1(Qwen3TtsSessionHandle handle, int32_t layer, int32_t which,
+                                                             int32_t count, void* destination, uint64_t bytes,
+                                                             char* error, size_t cap) {
+    return protect([&] { session_of(handle)->read_talker_cache(layer, which, count, destination, bytes); },
+                   QWEN3_TTS_TALKER_STATUS_STATE, error, cap);
 }
 
 QWEN3_TTS_API int32_t qwen3_tts_session_read_last_hidden_v1(Qwen3TtsSessionHandle handle, void* destination,

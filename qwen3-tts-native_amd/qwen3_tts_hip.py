@@ -189,6 +189,7 @@ SIGNATURES = {
                                                         C.POINTER(DeviceFrameViewV2)] + ERR),
     "qwen3_tts_session_state_info": (I32, [P, C.POINTER(TalkerStateInfo)] + ERR),
     "qwen3_tts_session_read_last_hidden_v1": (I32, [P, P, U64] + ERR),
+    "qwen3_tts_session_read_talker_cache_v1": (I32, [P, I32, I32, I32, P, U64] + ERR),
     # additive exports
     "qwen3_tts_model_config_default": (None, [C.POINTER(ModelConfigV1)]),
     "qwen3_tts_model_create_with_config": (I32, [I32, C.POINTER(ModelConfigV1), C.POINTER(P)] + ERR),
@@ -205,6 +206,9 @@ SIGNATURES = {
                                       + ERR),
     "qwen3_tts_op_decode_attention_noalloc_v1": (I32, [I32, P, I32, P, P, P, C.c_float, P, P, P, P, I32, I32, I32,
                                                         I32, I32, P] + ERR),
+    "qwen3_tts_op_bf16_gemm_v1": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, I32, I32, C.c_int64, C.c_int64,
+                                        C.c_int64, P] + ERR),
+    "qwen3_tts_op_causal_softmax_v1": (I32, [P, I32, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_kv_scatter_rows": (I32, [P, P, P, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_elementwise": (I32, [I32, P, P, I32, I32, P] + ERR),
     "qwen3_tts_op_sample_logits": (I32, [P, I32, I32, I32, P, P, SamplingConfig, P, P, P] + ERR),

@@ -29,6 +29,8 @@ Sources restated (K = native/qwen3-tts-native/native/src):
   frame sequence                    K/talker.cu:1095-1244
   sampler mask and penalty          K/sampling_kernels.cu:30-51
   quantizer (absmax / 127)          K/int8_gemv.cu:20-52
+  bf16 prefill (bf16 weights, GEMM  K/talker.cu:2750-3249,
+  attention, causal softmax)        K/talker_kernels.cu:115-191,232-260
 """
 from __future__ import annotations
 
@@ -96,7 +98,10 @@ class F64Model:
                     o=dequantize(weights[p + "self_attn.o_proj.weight"]),
                     gate=dequantize(weights[p + "mlp.gate_proj.weight"]),
                     up=dequantize(weights[p + "mlp.up_proj.weight"]),
-                    down=dequantize(weights[p + "mlp.down_proj.weight"])))
+                    down=dequantize(weights[p + "mlp.down_proj.weight"]),
+                    w16={n: from_bits(weights[p + n + ".weight"]) for n in (
+                        "self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                        "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")}))
             self.layers[part] = out
         self.codec_embedding = g("talker.model.codec_embedding.weight")
         self.text_embedding = g("talker.model.text_embedding.weight")
@@ -106,6 +111,7 @@ class F64Model:
         self.fc2_b = g("talker.text_projection.linear_fc2.bias")
         self.talker_norm = g("talker.model.norm.weight")
         self.codec_head = dequantize(weights["talker.codec_head.weight"])
+        self.codec_head16 = from_bits(weights["talker.codec_head.weight"])
         self.s2m = dequantize(weights["talker.code_predictor.small_to_mtp_projection.weight"])
         self.s2m_b = g("talker.code_predictor.small_to_mtp_projection.bias")
         self.predictor_norm = g("talker.code_predictor.model.norm.weight")
@@ -234,3 +240,50 @@ class F64Model:
         x = bf(x + self.project_text(trailing_text))
         _, logits = self.talker_step(state, x)
         return pred_logits, logits
+
+    # -- bf16 prefill -----------------------------------------------------
+    def score_scale(self, d):
+        return 1.0 / np.sqrt(d)
+
+    def prefill_bf16(self, state, text, codec, gemm_capacity):
+        """The reference's prompt prefill: bf16 weights, every product a
+        GEMM rounded to bf16; attention by materialized scores and the causal
+        softmax when the prompt fits gemm_capacity, else the exact per-row
+        kernel.  Returns the logits; fills the talker caches and last hidden."""
+        dims = self.talker
+        rows = len(text)
+        h = np.stack([self.prompt_embedding(int(t), int(c)) for t, c in zip(text, codec)])
+        scale = self.score_scale(dims.d)
+        group = dims.qh // dims.kvh
+        for l, L in enumerate(self.layers["talker"]):
+            w = L["w16"]
+            x = self.rms_norm(h, L["in_norm"])
+            q = bf(x @ w["self_attn.q_proj"].T).reshape(rows, dims.qh, dims.d)
+            k = bf(x @ w["self_attn.k_proj"].T).reshape(rows, dims.kvh, dims.d)
+            v = bf(x @ w["self_attn.v_proj"].T).reshape(rows, dims.kvh, dims.d)
+            q = self.rms_norm(q, L["q_norm"])
+            k = self.rms_norm(k, L["k_norm"])
+            q = np.stack([self.rope(q[r], r, dims.d) for r in range(rows)])
+            k = np.stack([self.rope(k[r], r, dims.d) for r in range(rows)])
+            state["talker"]["k"][l][:rows] = k
+            state["talker"]["v"][l][:rows] = v
+            attn = np.empty((rows, dims.qh, dims.d))
+            if rows <= gemm_capacity:
+                causal = np.tril(np.ones((rows, rows), bool))
+                for hh in range(dims.qh):
+                    s = bf(bf(q[:, hh] @ k[:, hh // group].T) * scale)
+                    s = np.where(causal, s, -np.inf)
+                    e = np.exp(s - s.max(axis=1, keepdims=True))
+                    p = bf(e / e.sum(axis=1, keepdims=True))
+                    attn[:, hh] = bf(p @ v[:, hh // group])
+            else:
+                for r in range(rows):
+                    attn[r] = self.attention(q[r], k[:r + 1], v[:r + 1], dims)
+            h = bf(h + bf(attn.reshape(rows, -1) @ w["self_attn.o_proj"].T))
+            x = self.rms_norm(h, L["post_norm"])
+            act = bf(bf(silu(bf(x @ w["mlp.gate_proj"].T))) * bf(x @ w["mlp.up_proj"].T))
+            h = bf(h + bf(act @ w["mlp.down_proj"].T))
+        last = self.rms_norm(h[-1], self.talker_norm)
+        state["last_hidden"] = last
+        state["position"] = rows
+        return bf(self.codec_head16 @ last)

@@ -19,6 +19,8 @@ position 0, an embedding table or LM head off by one codebook, a RoPE
 position off by one, a missing text projection -- moves these tensors by
 tens of percent; the sensitivity test below shows five such mistakes failing.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -164,3 +166,49 @@ def test_float64_model_detects_structural_mistakes(orc, mutant):
     structural mistake fails it."""
     with pytest.raises(AssertionError):
         run(orc, SMALL, 3, frames=2, model_cls=mutant)
+
+
+@pytest.mark.parametrize("rows,capacity", [(9, 512), (40, 512), (40, 16)])
+def test_oracle_bf16_prefill_matches_float64_model(orc, rows, capacity):
+    """The oracle's bf16 prefill (orc_prefill_bf16) against the float64
+    model: GEMM attention (rows <= capacity) and the exact per-row kernel."""
+    c = SMALL
+    weights = toy_model.make_weights(c, seed=21)
+    om = toy_model.OracleModel(orc, c, weights)
+    fm = F64Model(c, weights)
+    rng = np.random.default_rng(rows)
+    text = rng.integers(0, c["text_vocabulary"], rows).astype(np.int32)
+    codec = rng.integers(0, 2048, rows).astype(np.int32)
+    text[2] = -1
+    codec[0] = -1
+    max_seq = 64
+    o = toy_model.OracleSession(om, max_seq, 7)
+    t = np.ascontiguousarray(text)
+    cd = np.ascontiguousarray(codec)
+    first = o.lib.orc_prefill_bf16(C.byref(om.model), C.byref(o.s), t.ctypes.data_as(C.c_void_p),
+                                   cd.ctypes.data_as(C.c_void_p), rows, C.byref(toy_model.OrcSampling(*GREEDY)),
+                                   capacity)
+    st = fm.new_session(max_seq)
+    logits = fm.prefill_bf16(st, text, codec, capacity)
+    kv = c["talker_key_value_heads"] * c["head_dimension"]
+    for name, cache in (("tk", "k"), ("tv", "v")):
+        got = from_bits(o.bufs[name]).reshape(c["talker_layers"], max_seq, kv)[:, :rows]
+        close(got, st["talker"][cache][:, :rows].reshape(c["talker_layers"], rows, kv), f"prefill {cache} cache")
+    close(from_bits(o.bufs["last"]), st["last_hidden"], "prefill last hidden")
+    close(from_bits(o.bufs["logits"][:c["talker_vocabulary"]]), logits, "prefill logits")
+    check_token(fm.talker_scores(logits, [], GREEDY[4]), first, "prefill first token")
+    assert o.s.position == rows and o.s.history_count == 1
+
+
+class _PrefillWithoutScale(F64Model):
+    """Causal softmax without the 1/sqrt(d) score scale."""
+
+    def score_scale(self, d):
+        return 1.0
+
+
+@pytest.mark.parametrize("mutant", [_RopeOffByOne, _PrefillWithoutScale])
+def test_bf16_prefill_check_detects_mistakes(orc, mutant, monkeypatch):
+    monkeypatch.setattr(__import__("test_frame_f64"), "F64Model", mutant)
+    with pytest.raises(AssertionError):
+        test_oracle_bf16_prefill_matches_float64_model(orc, 40, 512)

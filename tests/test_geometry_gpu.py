@@ -66,6 +66,13 @@ def make_weights(c, seed):
     return out
 
 
+@pytest.fixture(autouse=True)
+def decode_step_prefill(monkeypatch):
+    """These tests compare with the oracle's decode-step prefill (the bf16
+    prefill has its own tests in test_prefill_gpu.py)."""
+    monkeypatch.setenv("QWEN3_TTS_PREFILL", "decode")
+
+
 @pytest.fixture(scope="module")
 def full(hip, orc):
     print("\n[geometry] generating VoiceDesign-geometry weights", flush=True)
@@ -171,3 +178,66 @@ def test_voicedesign_geometry_batched_exact(hip, orc, full, monkeypatch):
         om.model.batch_semantics = 0
         for s in sessions:
             hip.load().qwen3_tts_session_destroy(s)
+
+
+def test_voicedesign_geometry_bf16_prefill(hip, orc, full, monkeypatch):
+    """The bf16 prefill at full geometry (66 rows, GEMM attention) against
+    the oracle's orc_prefill_bf16.  Two valid fp32 summation orders of the
+    GEMMs drift apart through 28 layers (bf16 rounding flips propagate), so
+    the bar is relative to that drift: for every layer's key and value cache
+    and the final hidden state, the GPU's RMS distance from the oracle (fp32
+    chains in k order) is at most twice the oracle's own distance to a second
+    valid order (sums accumulated in double, rounded once), plus 2^-10.  At
+    layer 0 both are within 2^-6 of the largest value.  First token identical
+    unless the oracle's top-2 margin is below 2^-5 of the largest logit."""
+    monkeypatch.delenv("QWEN3_TTS_PREFILL", raising=False)
+    model, om = full
+    s = session(hip, model, 77)
+    try:
+        text, codec = prompt(77)
+        pre = hip.PrefillResult()
+        hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                 codec.ctypes.data_as(C.POINTER(C.c_int32)), PROMPT, hip.SamplingConfig(*GREEDY), C.byref(pre))
+        om.model.batch_semantics = 0
+        o = toy_model.OracleSession(om, 128, 77)
+        first = o.prefill_bf16(text, codec, GREEDY)
+        alt = toy_model.OracleSession(om, 128, 77)
+        orc.set_gemm_order(1)
+        try:
+            alt.prefill_bf16(text, codec, GREEDY)
+        finally:
+            orc.set_gemm_order(0)
+        kvw = VOICEDESIGN["talker_key_value_heads"] * 128
+        layers = VOICEDESIGN["talker_layers"]
+
+        def rms_rel(x, ref):
+            x, ref = gen.f32(x).astype(np.float64), gen.f32(ref).astype(np.float64)
+            return np.sqrt(np.mean((x - ref) ** 2)) / np.sqrt(np.mean(ref ** 2))
+
+        def max_rel(x, ref):
+            x, ref = gen.f32(x).astype(np.float64), gen.f32(ref).astype(np.float64)
+            return np.max(np.abs(x - ref)) / np.max(np.abs(ref))
+
+        report = []
+        for layer in range(layers):
+            for which, name in ((0, "tk"), (1, "tv")):
+                got = np.zeros((PROMPT, kvw), np.uint16)
+                hip.call("qwen3_tts_session_read_talker_cache_v1", s, layer, which, PROMPT, got.ctypes.data, got.nbytes)
+                ref = o.bufs[name].reshape(layers, 128, kvw)[layer, :PROMPT]
+                other = alt.bufs[name].reshape(layers, 128, kvw)[layer, :PROMPT]
+                e_gpu, e_alt = rms_rel(got, ref), rms_rel(other, ref)
+                report.append((layer, which, e_gpu, e_alt))
+                assert e_gpu <= 2 * e_alt + 2 ** -10, (layer, which, e_gpu, e_alt)
+                if layer == 0:
+                    assert max_rel(got, ref) <= 2 ** -6 and max_rel(other, ref) <= 2 ** -6
+        h = np.zeros(VOICEDESIGN["talker_hidden"], np.uint16)
+        hip.call("qwen3_tts_session_read_last_hidden_v1", s, h.ctypes.data, h.nbytes)
+        e_gpu, e_alt = rms_rel(h, o.bufs["last"]), rms_rel(alt.bufs["last"], o.bufs["last"])
+        assert e_gpu <= 2 * e_alt + 2 ** -10, (e_gpu, e_alt)
+        print(f"[geometry] bf16 prefill RMS distance from the oracle, GPU / second order: layer 27 "
+              f"{report[-1][2]:.4f} / {report[-1][3]:.4f}; last hidden {e_gpu:.4f} / {e_alt:.4f}", flush=True)
+        if pre.first_semantic_token != first:
+            logits = gen.f32(o.bufs["logits"][:VOICEDESIGN["talker_vocabulary"]]).astype(np.float64)
+            assert logits[first] - logits[pre.first_semantic_token] <= 2 ** -5 * np.max(np.abs(logits))
+    finally:
+        hip.load().qwen3_tts_session_destroy(s)

@@ -22,6 +22,13 @@ TALKER_TOPK = (1, 50, 1.0, 0.9, 1.05)
 PREDICTOR_TOPK = (1, 50, 1.0, 0.9, 1.0)
 
 
+@pytest.fixture(autouse=True)
+def decode_step_prefill(monkeypatch):
+    """These tests compare with the oracle's decode-step prefill (the bf16
+    prefill has its own tests in test_prefill_gpu.py)."""
+    monkeypatch.setenv("QWEN3_TTS_PREFILL", "decode")
+
+
 @pytest.fixture(scope="module")
 def toy(hip, orc):
     weights = toy_model.make_weights(TOY, seed=3)

@@ -107,7 +107,8 @@ class OrcDims(C.Structure):
 
 class OrcLayer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("input_norm", "q_norm", "k_norm", "post_norm", "q", "k", "v", "o",
-                                           "gate_up", "down", "q_s", "k_s", "v_s", "o_s", "gate_up_s", "down_s")]
+                                           "gate_up", "down", "q_s", "k_s", "v_s", "o_s", "gate_up_s", "down_s",
+                                           "q16", "k16", "v16", "o16", "gate16", "up16", "down16")]
 
 
 class OrcModel(C.Structure):
@@ -122,7 +123,7 @@ class OrcModel(C.Structure):
                 ("small_to_mtp", C.c_void_p), ("small_to_mtp_s", C.c_void_p),
                 ("small_to_mtp_bias", C.c_void_p), ("predictor_norm", C.c_void_p),
                 ("predictor_embeddings", C.c_void_p), ("predictor_heads", C.c_void_p),
-                ("predictor_heads_s", C.c_void_p), ("batch_semantics", C.c_int)]
+                ("predictor_heads_s", C.c_void_p), ("batch_semantics", C.c_int), ("codec_head16", C.c_void_p)]
 
 
 class OrcSession(C.Structure):
@@ -169,6 +170,10 @@ class OracleModel:
                     qq, ss = quant(*[f"{p}.{n}.weight" for n in names])
                     setattr(L, fld, _ptr(qq))
                     setattr(L, fld + "_s", _ptr(ss))
+                for fld, name in (("q16", "self_attn.q_proj"), ("k16", "self_attn.k_proj"), ("v16", "self_attn.v_proj"),
+                                  ("o16", "self_attn.o_proj"), ("gate16", "mlp.gate_proj"), ("up16", "mlp.up_proj"),
+                                  ("down16", "mlp.down_proj")):
+                    setattr(L, fld, _ptr(weights[f"{p}.{name}.weight"]))
             self.keep.append(arr)
             return arr
 
@@ -208,6 +213,7 @@ class OracleModel:
         m.predictor_embeddings, m.predictor_heads, m.predictor_heads_s = (
             C.addressof(embs), C.addressof(heads), C.addressof(heads_s))
         m.batch_semantics = int(batch_semantics)
+        m.codec_head16 = _ptr(weights["talker.codec_head.weight"])
         self.model = m
         lib = orc.lib()
         lib.orc_frame_step.restype = C.c_int
@@ -239,10 +245,21 @@ class OracleSession:
         self.s = s
 
     def prefill(self, text, codec, sampling):
+        """Prefill as consecutive int8 decode steps (the library's decode-step
+        prefill mode)."""
         t = np.ascontiguousarray(text, np.int32)
         cd = np.ascontiguousarray(codec, np.int32)
         return self.lib.orc_prefill(C.byref(self.om.model), C.byref(self.s), t.ctypes.data_as(C.c_void_p),
                                     cd.ctypes.data_as(C.c_void_p), len(t), C.byref(OrcSampling(*sampling)))
+
+    def prefill_bf16(self, text, codec, sampling):
+        """The reference's bf16 prefill (GEMM attention up to
+        min(max_seq, 512) positions, the exact kernel beyond)."""
+        t = np.ascontiguousarray(text, np.int32)
+        cd = np.ascontiguousarray(codec, np.int32)
+        cap = min(self.s.max_seq, 512)
+        return self.lib.orc_prefill_bf16(C.byref(self.om.model), C.byref(self.s), t.ctypes.data_as(C.c_void_p),
+                                         cd.ctypes.data_as(C.c_void_p), len(t), C.byref(OrcSampling(*sampling)), cap)
 
     def frame(self, semantic, text_token, talker_sampling, predictor_sampling):
         codes = np.zeros(16, np.uint16)
