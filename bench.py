@@ -298,6 +298,49 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
         lib.qwen3_tts_model_destroy(model)
 
 
+# bf16 GEMM flops of one prompt row through the talker (q, k, v, o, gate, up,
+# down at hidden 2048, q width 2048, kv width 1024, FFN 6144), without attention.
+PREFILL_FLOPS_PER_ROW = 2 * 28 * (2048 * 2048 + 2 * 1024 * 2048 + 2048 * 2048 + 3 * 6144 * 2048)
+
+
+def prefill_benchmark(hip, rows_list=(512, 801), repeats: int = 5, max_seq: int = 1024):
+    """The bf16 prompt prefill through the C ABI at VoiceDesign geometry:
+    prompts of `rows_list` positions (512: GEMM attention, the largest the
+    reference's GEMM path takes; 801: the exact per-row attention), the
+    median of `repeats` prefills each (qwen3_tts_session_prefill's own GPU
+    time), as prompt positions per second and the GEMMs' TFLOP/s."""
+    import numpy as np
+
+    lib = hip.load()
+    model, cfg = build_model(hip)
+    out = {}
+    try:
+        session = C.c_void_p()
+        smem = hip.SessionMemory()
+        hip.call("qwen3_tts_session_create", model, max_seq, 5, C.byref(session), C.byref(smem))
+        try:
+            rng = np.random.default_rng(3)
+            for rows in rows_list:
+                times = []
+                for _ in range(repeats + 1):
+                    text = rng.integers(0, cfg.text_vocabulary, rows).astype(np.int32)
+                    codec = rng.integers(0, 2048, rows).astype(np.int32)
+                    pre = hip.PrefillResult()
+                    hip.call("qwen3_tts_session_prefill", session, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                             codec.ctypes.data_as(C.POINTER(C.c_int32)), rows, hip.sampling(0, 0, 1.0, 1.0, 1.0),
+                             C.byref(pre))
+                    times.append(pre.talker_gpu_milliseconds)
+                ms = sorted(times[1:])[len(times[1:]) // 2]
+                out[f"rows{rows}"] = {"gpu_ms": round(ms, 3), "positions_per_second": round(rows / (ms * 1e-3), 1),
+                                      "gemm_tflops": round(rows * PREFILL_FLOPS_PER_ROW / (ms * 1e-3) / 1e12, 2),
+                                      "attention": "GEMM" if rows <= 512 else "exact per-row kernel"}
+        finally:
+            lib.qwen3_tts_session_destroy(session)
+    finally:
+        lib.qwen3_tts_model_destroy(model)
+    return out
+
+
 def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: int = 1024):
     """Multi-session serving through the batch entry point
     (qwen3_tts_model_batch_next_frame_begin_v2, the reference's lockstep
@@ -405,6 +448,9 @@ def main() -> int:
     ap.add_argument("--only-batched-gemv", action="store_true",
                     help="run only config 4's MFMA GEMVs (N = 2, 4, 8; gate+up and down, 28 distinct layers); "
                          "for rocprofv3 --pmc")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="run only the bf16 prompt prefill at VoiceDesign geometry (prompts of 512 and 801 "
+                         "positions, 5 each); for rocprofv3 kernel statistics")
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
@@ -427,6 +473,9 @@ def main() -> int:
         hip.synchronize()
         out["copy_bytes"] = size
         print(json.dumps(out), flush=True)
+        return 0
+    if args.only_prefill:
+        print(json.dumps({"prefill": prefill_benchmark(hip)}), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
@@ -493,6 +542,10 @@ def main() -> int:
             line["frame_step"] = frame_benchmark(hip, frames=args.frames)
         except Exception as e:  # report, never hide
             line["frame_step"] = {"error": str(e)}
+        try:
+            line["prefill"] = prefill_benchmark(hip)
+        except Exception as e:  # report, never hide
+            line["prefill"] = {"error": str(e)}
         try:
             line["batched_frames"] = batched_frames(hip)
         except Exception as e:  # report, never hide

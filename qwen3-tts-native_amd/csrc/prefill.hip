@@ -7,10 +7,11 @@
 //
 // with A and B row-major and K contiguous in both (activations x weights^T,
 // queries x keys^T, probabilities x values^T), batched over heads through
-// gridDim.z with a grouped B index for GQA.  A 128x128 block tile of 256
-// threads (4 waves, 64x64 each = 4x4 v_mfma_f32_16x16x32_bf16 tiles), K in
-// steps of 64 staged through double-buffered LDS (padded rows), the next
-// step's global loads issued before the current step's MFMAs.
+// gridDim.z with a grouped B index for GQA.  A 128x128 (or, when that leaves
+// CUs idle, 64x64) block tile of 256 threads (4 waves in 2x2, each a grid of
+// v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 staged through
+// double-buffered LDS (padded rows), the next step's global loads issued
+// before the current step's MFMAs.
 //
 // The summation order of an fp32 GEMM is not the reference's (cuBLAS leaves
 // it unspecified), so this path is compared with tolerances; everything
@@ -28,8 +29,6 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
 constexpr int kGemmThreads = 256;
@@ -44,7 +43,14 @@ __device__ __forceinline__ uint4 load_chunk(const bf16_t* base, int ld, int row,
     return v;
 }
 
+// Block tile kBM x kBN, four waves in 2 x 2, each (kBM/2) x (kBN/2) as
+// (kBM/32) x (kBN/32) 16x16 MFMA tiles.
+template <int kBM, int kBN>
 __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g) {
+    constexpr int kTM = kBM / 32;                 // MFMA tiles per wave along M
+    constexpr int kTN = kBN / 32;                 // and along N
+    constexpr int kChunksA = kBM * 8 / kGemmThreads;  // 16-byte chunks per thread per K step
+    constexpr int kChunksB = kBN * 8 / kGemmThreads;
     __shared__ __align__(16) bf16_t as[2][kBM * kLdsRow];
     __shared__ __align__(16) bf16_t bs[2][kBN * kLdsRow];
     const int tid = threadIdx.x;
@@ -57,38 +63,41 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
     const bf16_t* b = g.b + static_cast<size_t>(z / g.b_group) * g.b_batch;
     bf16_t* c = g.c + static_cast<size_t>(z) * g.c_batch;
 
-    // Global -> LDS: 128 rows x 8 chunks per operand, 4 chunks per thread.
-    uint4 ra[4], rb[4];
+    uint4 ra[kChunksA], rb[kChunksB];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            const int row = chunk >> 3;
-            const int col = k0 + (chunk & 7) * 8;
-            ra[i] = load_chunk(a, g.lda, m0 + row, g.m, col, g.k);
-            rb[i] = load_chunk(b, g.ldb, n0 + row, g.n, col, g.k);
+            ra[i] = load_chunk(a, g.lda, m0 + (chunk >> 3), g.m, k0 + (chunk & 7) * 8, g.k);
+        }
+#pragma unroll
+        for (int i = 0; i < kChunksB; ++i) {
+            const int chunk = tid + i * kGemmThreads;
+            rb[i] = load_chunk(b, g.ldb, n0 + (chunk >> 3), g.n, k0 + (chunk & 7) * 8, g.k);
         }
     };
     auto stage = [&](int buffer) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            const int row = chunk >> 3;
-            const int col = (chunk & 7) * 8;
-            *reinterpret_cast<uint4*>(&as[buffer][row * kLdsRow + col]) = ra[i];
-            *reinterpret_cast<uint4*>(&bs[buffer][row * kLdsRow + col]) = rb[i];
+            *reinterpret_cast<uint4*>(&as[buffer][(chunk >> 3) * kLdsRow + (chunk & 7) * 8]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kChunksB; ++i) {
+            const int chunk = tid + i * kGemmThreads;
+            *reinterpret_cast<uint4*>(&bs[buffer][(chunk >> 3) * kLdsRow + (chunk & 7) * 8]) = rb[i];
         }
     };
 
-    const int wm = (wave >> 1) * 64;  // wave tile origin inside the block tile
-    const int wn = (wave & 1) * 64;
+    const int wm = (wave >> 1) * (kBM / 2);  // wave tile origin inside the block tile
+    const int wn = (wave & 1) * (kBN / 2);
     const int m = lane & 15;
     const int group = lane >> 4;
-    floatx4_t acc[4][4];
+    floatx4_t acc[kTM][kTN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kTM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kTN; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
     const int steps = (g.k + kBK - 1) / kBK;
     fetch(0);
@@ -99,16 +108,19 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
         if (s + 1 < steps) fetch((s + 1) * kBK);  // in flight under the MFMAs
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
-            bf16x8_t af[4], bfr[4];
+            bf16x8_t af[kTM], bfr[kTN];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < kTM; ++i) {
                 af[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&as[buffer][(wm + 16 * i + m) * kLdsRow + kk + 8 * group]));
-                bfr[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&bs[buffer][(wn + 16 * i + m) * kLdsRow + kk + 8 * group]));
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int j = 0; j < kTN; ++j) {
+                bfr[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&bs[buffer][(wn + 16 * j + m) * kLdsRow + kk + 8 * group]));
+            }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < kTM; ++i)
+#pragma unroll
+                for (int j = 0; j < kTN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
         if (s + 1 < steps) {
             stage(buffer ^ 1);
@@ -117,13 +129,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
     }
     // acc[i][j][r] = C[wm + 16 i + 4 group + r][wn + 16 j + m]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kTM; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = m0 + wm + 16 * i + 4 * group + r;
             if (row >= g.m) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < kTN; ++j) {
                 const int col = n0 + wn + 16 * j + m;
                 if (col < g.n) c[static_cast<size_t>(row) * g.ldc + col] = f2bf(acc[i][j][r]);
             }
@@ -255,8 +267,13 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);
     if ((align & 15u) != 0 || (g.a_batch % 8) != 0 || (g.b_batch % 8) != 0) return hipErrorInvalidValue;
-    const dim3 grid((g.n + kBN - 1) / kBN, (g.m + kBM - 1) / kBM, g.batch);
-    gemm_bf16_kernel<<<grid, kGemmThreads, 0, stream>>>(g);
+    // 128 x 128 tiles when they give at least two workgroups per CU, else 64 x 64
+    const long long big = static_cast<long long>((g.n + 127) / 128) * ((g.m + 127) / 128) * g.batch;
+    if (big >= 512) {
+        gemm_bf16_kernel<128, 128><<<dim3((g.n + 127) / 128, (g.m + 127) / 128, g.batch), kGemmThreads, 0, stream>>>(g);
+    } else {
+        gemm_bf16_kernel<64, 64><<<dim3((g.n + 63) / 64, (g.m + 63) / 64, g.batch), kGemmThreads, 0, stream>>>(g);
+    }
     return hipGetLastError();
 }
 
