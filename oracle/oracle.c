@@ -113,7 +113,7 @@ void orc_set_threads(int threads) {
     g_threads = threads < 1 ? 1 : (threads > 256 ? 256 : threads);
 }
 
-typedef void (*ChannelRangeFn)(void* ctx, int c0, int c1);
+typedef OrcRangeFn ChannelRangeFn;
 typedef struct RangeJob {
     ChannelRangeFn fn;
     void* ctx;
@@ -126,7 +126,7 @@ static void* range_worker(void* arg) {
     return NULL;
 }
 
-static void for_channels(int channels, size_t work, ChannelRangeFn fn, void* ctx) {
+void orc_for_channels(int channels, size_t work, OrcRangeFn fn, void* ctx) {
     int threads = g_threads;
     if (work < ((size_t)1 << 20) || threads <= 1) {
         fn(ctx, 0, channels);
@@ -186,7 +186,7 @@ static void quantize_range(void* p, int r0, int r1) {
 void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
                               float* scales, int in_features, int out_features) {
     QuantCtx q = {weight, quantized, scales, in_features};
-    for_channels(out_features, (size_t)out_features * in_features, quantize_range, &q);
+    orc_for_channels(out_features, (size_t)out_features * in_features, quantize_range, &q);
 }
 
 /* One output channel, one activation row, in the reference's exact order
@@ -249,7 +249,7 @@ void orc_int8_gemm_rows(const int8_t* weight, const float* scales,
                         int out_features, int rows, float* y32, uint16_t* y16) {
     float* x = widen_rows(input, rows, in_features);
     GemmCtx g = {weight, scales, x, in_features, out_features, rows, y32, y16, NULL};
-    for_channels(out_features, (size_t)out_features * in_features * rows, gemm_range, &g);
+    orc_for_channels(out_features, (size_t)out_features * in_features * rows, gemm_range, &g);
     free(x);
 }
 
@@ -288,7 +288,7 @@ void orc_int8_gemm_rows_add(const int8_t* weight, const float* scales,
                             int in_features, int out_features, int rows) {
     float* x = widen_rows(input, rows, in_features);
     GemmCtx g = {weight, scales, x, in_features, out_features, rows, NULL, NULL, inout};
-    for_channels(out_features, (size_t)out_features * in_features * rows, gemm_add_range, &g);
+    orc_for_channels(out_features, (size_t)out_features * in_features * rows, gemm_add_range, &g);
     free(x);
 }
 
@@ -316,7 +316,7 @@ void orc_int8_gate_up_silu_rows(const int8_t* weight, const float* scales,
                                 int in_features, int out_features, int rows) {
     float* x = widen_rows(input, rows, in_features);
     GemmCtx g = {weight, scales, x, in_features, out_features, rows, NULL, NULL, output};
-    for_channels(out_features, (size_t)2 * out_features * in_features * rows, gate_up_range, &g);
+    orc_for_channels(out_features, (size_t)2 * out_features * in_features * rows, gate_up_range, &g);
     free(x);
 }
 
@@ -904,6 +904,7 @@ typedef struct Bf16GemmCtx {
 static int g_gemm_order = 0;
 
 void orc_set_gemm_order(int order) { g_gemm_order = order; }
+int orc_get_gemm_order(void) { return g_gemm_order; }
 
 static void bf16_gemm_range(void* p, int j0, int j1) {
     const Bf16GemmCtx* g = (const Bf16GemmCtx*)p;
@@ -931,7 +932,7 @@ void orc_bf16_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int
     for (int i = 0; i < m; ++i) orc_bf16_to_f32_array(a + (size_t)i * lda, af + (size_t)i * k, (size_t)k);
     for (int j = 0; j < n; ++j) orc_bf16_to_f32_array(b + (size_t)j * ldb, bf_ + (size_t)j * k, (size_t)k);
     Bf16GemmCtx g = {af, bf_, c, m, n, k, ldc};
-    for_channels(n, (size_t)m * n * k, bf16_gemm_range, &g);
+    orc_for_channels(n, (size_t)m * n * k, bf16_gemm_range, &g);
     free(af);
     free(bf_);
 }

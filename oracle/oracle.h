@@ -41,6 +41,10 @@ void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
 /* Threads used by the GEMV restatements for large matrices (default 1);
  * results do not depend on it. */
 void orc_set_threads(int threads);
+/* Runs fn(ctx, c0, c1) over [0, channels) split across the oracle's threads
+ * (one call on the calling thread when work is small). */
+typedef void (*OrcRangeFn)(void* ctx, int c0, int c1);
+void orc_for_channels(int channels, size_t work, OrcRangeFn fn, void* ctx);
 
 /* y32 (optional) receives value*scale before the bf16 store; y16 (optional)
  * receives the bf16 store.  Both are [rows][out]. */
@@ -185,6 +189,7 @@ void orc_bf16_gemm(const uint16_t* a, const uint16_t* b, uint16_t* c, int m, int
  * in double rounded once -- a second valid order, used to measure how far
  * two fp32 GEMM orders drift apart through a deep prefill. */
 void orc_set_gemm_order(int order);
+int orc_get_gemm_order(void);
 /* causal_softmax_kernel (K/talker_kernels.cu:232-260) on [heads][rows][stride]. */
 void orc_causal_softmax(uint16_t* scores, int heads, int rows, int stride, int head_dimension);
 /* run_talker_prefill with the prompt embeddings of prepare_prompt_embedding:

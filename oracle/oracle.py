@@ -230,3 +230,83 @@ def set_gemm_order(order: int) -> None:
     """0: the bf16 GEMM's fp32 chain in k order (default); 1: accumulated in
     double and rounded once."""
     lib().orc_set_gemm_order(int(order))
+
+
+# ---- speech-tokenizer decoder (codec_oracle.c) ----------------------------
+CODEC_TENSORS = 269
+
+
+class _CodecTrace(C.Structure):
+    _fields_ = [("rvq", C.c_void_p), ("preconv", C.c_void_p), ("transformer", C.c_void_p),
+                ("latent1", C.c_void_p), ("latent2", C.c_void_p), ("checkpoints", C.c_void_p * 14),
+                ("stop_after", C.c_int)]
+
+
+def codec_tensor_table():
+    """[(name, float elements)] in the order orc_codec_packet takes them."""
+    L = lib()
+    L.orc_codec_tensor_name.restype = C.c_char_p
+    L.orc_codec_tensor_elements.restype = C.c_uint64
+    return [(L.orc_codec_tensor_name(i).decode(), int(L.orc_codec_tensor_elements(i)))
+            for i in range(CODEC_TENSORS)]
+
+
+# Decoder checkpoint -> (positions per frame, channels), CS:2066-2274.
+CODEC_CHECKPOINTS = {6: (4, 1536), 7: (32, 768), 8: (160, 384), 9: (640, 192), 10: (1920, 96),
+                     11: (1920, 96), 12: (1920, 1), 13: (1920, 1)}
+
+
+class CodecOracle:
+    """One decoding stream of the CPU decoder over fp32 weights given in
+    codec_tensor_table() order (a dict name -> array, or a list)."""
+
+    def __init__(self, weights):
+        table = codec_tensor_table()
+        if isinstance(weights, dict):
+            weights = [weights[name] for name, _ in table]
+        self._weights = [np.ascontiguousarray(w, np.float32).reshape(-1) for w in weights]
+        for (name, count), w in zip(table, self._weights):
+            if w.size != count:
+                raise ValueError(f"{name}: {w.size} elements, expected {count}")
+        self._ptrs = (C.c_void_p * CODEC_TENSORS)(*[w.ctypes.data for w in self._weights])
+        L = lib()
+        L.orc_codec_state_create.restype = C.c_void_p
+        L.orc_codec_state_destroy.argtypes = [C.c_void_p]
+        L.orc_codec_state_reset.argtypes = [C.c_void_p]
+        L.orc_codec_packet.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                       C.POINTER(_CodecTrace)]
+        self._state = L.orc_codec_state_create()
+
+    def __del__(self):
+        if getattr(self, "_state", None):
+            lib().orc_codec_state_destroy(self._state)
+            self._state = None
+
+    def reset(self):
+        lib().orc_codec_state_reset(self._state)
+
+    def packet(self, codes, stop_after=0, trace=True):
+        """Decodes one packet; returns a dict with 'pcm' (int16, empty for a
+        stopped packet) and, with trace, the row-major stage outputs (names
+        and decoder checkpoint numbers 6..13; zeros past a stop)."""
+        codes = _c(np.atleast_2d(codes), np.uint16)
+        frames = codes.shape[0]
+        out = {"pcm": np.zeros(frames * 1920, np.int16)}
+        tr = _CodecTrace()
+        if trace:
+            for name, shape in (("rvq", (frames, 512)), ("preconv", (frames, 1024)),
+                                ("transformer", (frames, 1024)), ("latent1", (2 * frames, 1024)),
+                                ("latent2", (4 * frames, 1024))):
+                out[name] = np.zeros(shape, np.float32)
+                setattr(tr, name, out[name].ctypes.data)
+            for c, (per_frame, channels) in CODEC_CHECKPOINTS.items():
+                out[c] = np.zeros((per_frame * frames, channels), np.float32)
+                tr.checkpoints[c] = out[c].ctypes.data
+        tr.stop_after = stop_after
+        n = lib().orc_codec_packet(self._ptrs, self._state, codes.ctypes.data, frames,
+                                   out["pcm"].ctypes.data, C.byref(tr))
+        if n < 0:
+            raise ValueError("packet must hold 1-4 frames")
+        if n == 0:
+            out["pcm"] = out["pcm"][:0]
+        return out
