@@ -434,6 +434,91 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
         lib.qwen3_tts_model_destroy(model)
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def codec_weights(seed: int = 0):
+    """Random fp32 decoder weights of the real geometry (271 tensors,
+    114,323,137 parameters): N(0, 1/fan_in) matrices, unit norms, small
+    scales, cluster usage U[0.5, 2]."""
+    import numpy as np
+    import qwen3_tts_codec_hip as codec
+
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in codec.tensor_shapes().items():
+        fan_in = int(np.prod(shape[1:])) if len(shape) > 1 else 1
+        if name.endswith("cluster_usage"):
+            w = rng.uniform(0.5, 2.0, shape)
+        elif name.endswith(("scale", "gamma")):
+            w = np.full(shape, 0.1)
+        elif name.endswith(("norm.weight", "layernorm.weight")):
+            w = np.ones(shape)
+        elif len(shape) == 1:
+            w = rng.standard_normal(shape) * 0.05
+        else:
+            w = rng.standard_normal(shape) / np.sqrt(fan_in)
+        out[name] = w.astype(np.float32)
+    return out
+
+
+def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6):
+    """The speech-tokenizer decoder through its C ABI: a continuous stream of
+    `packets` packets per size (1 and 4 frames = 80 / 320 ms of audio) on one
+    session, each packet's own GPU time and end-to-end latency (median); then
+    `streams` concurrent sessions through qwen3_tts_codec_session_process_batch_v1
+    (aggregate audio seconds per wall second).  The reference's published
+    numbers (GB10): 11.65 ms per 1-frame packet, 62.09 ms per 4-frame packet
+    (benchmarks/results/native-codec-decoder-bf16.json, p50)."""
+    import numpy as np
+    import qwen3_tts_codec_hip as codec
+
+    model = codec.SharedModel(codec_weights())
+    rng = np.random.default_rng(5)
+    out = {"weights": "synthetic fp32, real geometry (114,323,137 parameters)"}
+    try:
+        for frames in (1, 4):
+            s = model.session()
+            gpu, e2e = [], []
+            for i in range(warm + packets):
+                if i and i % 500 == 0:
+                    s.reset()
+                codes = rng.integers(0, 2048, (frames, 16), dtype=np.uint16)
+                _, res = s.packet(codes)
+                if i >= warm:
+                    gpu.append(res.gpu_microseconds)
+                    e2e.append(res.end_to_end_microseconds)
+            s.close()
+            g, e = float(np.median(gpu)), float(np.median(e2e))
+            audio_us = frames * 80_000.0
+            flops = codec.packet_flops(frames)
+            out[f"frames{frames}"] = {
+                "gpu_us_p50": round(g, 1), "end_to_end_us_p50": round(e, 1),
+                "end_to_end_us_p99": round(float(np.percentile(e2e, 99)), 1),
+                "rtf_p50": round(e / audio_us, 5), "packet_gflop": round(flops / 1e9, 3),
+                "tflops": round(flops / (g * 1e-6) / 1e12, 2),
+                "frac_of_fp32_mfma_peak": round(flops / (g * 1e-6) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                "weight_gbs": round(4 * 114_323_137 / (g * 1e-6) / 1e9, 1),
+                "vs_reference_gb10_p50": round((11_651.3 if frames == 1 else 62_086.3) / e, 1)}
+        sessions = [model.session() for _ in range(streams)]
+        t0, audio = None, 0.0
+        for i in range(warm + packets // 2):
+            if i == warm:
+                t0 = time.perf_counter()
+            codes = [rng.integers(0, 2048, (4, 16), dtype=np.uint16) for _ in range(streams)]
+            codec.process_batch(sessions, codes)
+            if i >= warm:
+                audio += streams * 0.32
+        wall = time.perf_counter() - t0
+        out[f"batch{streams}_4frame"] = {"audio_seconds_per_second": round(audio / wall, 1),
+                                         "aggregate_rtf": round(wall / audio, 5)}
+        for s in sessions:
+            s.close()
+    finally:
+        model.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -451,6 +536,9 @@ def main() -> int:
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the bf16 prompt prefill at VoiceDesign geometry (prompts of 512 and 801 "
                          "positions, 5 each); for rocprofv3 kernel statistics")
+    ap.add_argument("--only-codec", action="store_true",
+                    help="run only the speech-tokenizer decoder benchmark (packets of 1 and 4 frames, 6 batched "
+                         "streams); for rocprofv3 kernel statistics")
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
@@ -476,6 +564,9 @@ def main() -> int:
         return 0
     if args.only_prefill:
         print(json.dumps({"prefill": prefill_benchmark(hip)}), flush=True)
+        return 0
+    if args.only_codec:
+        print(json.dumps({"codec": codec_benchmark()}), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
@@ -550,6 +641,10 @@ def main() -> int:
             line["batched_frames"] = batched_frames(hip)
         except Exception as e:  # report, never hide
             line["batched_frames"] = {"error": str(e)}
+        try:
+            line["codec"] = codec_benchmark()
+        except Exception as e:  # report, never hide
+            line["codec"] = {"error": str(e)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -63,11 +63,10 @@ struct ConvGemmArgs {
     float* snake_out;
     const float* snake_alpha;
     const float* snake_beta_den;
-    // split-K over `splits` slices: partial sums in `partial`, one arrival
-    // counter per output tile in `counters` (zero between launches)
+    // split-K over `splits` slices: partial sums in `partial`, reduced by a
+    // second launch
     int splits;
     float* partial;
-    unsigned* counters;
 };
 
 enum class GemmShape : int { kSmall = 0, kLarge = 1 };  // 16x64 or 64x64 tiles
@@ -146,7 +145,6 @@ hipError_t launch_repack_transpose(const float* src, int in_ch, int out_ch, int 
                                    hipStream_t stream);
 // alpha -> exp(alpha), beta -> exp(beta) + 1e-9 (in place)
 hipError_t launch_snake_params(float* alpha, float* beta, int channels, hipStream_t stream);
-hipError_t launch_fill_u32(unsigned* dst, size_t count, unsigned value, hipStream_t stream);
 hipError_t launch_fill_f32(float* dst, size_t count, float value, hipStream_t stream);
 
 }  // namespace q3c

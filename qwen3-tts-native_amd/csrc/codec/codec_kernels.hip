@@ -62,50 +62,94 @@ __device__ __forceinline__ void conv_epilogue(const ConvGemmArgs& g, int p, int 
 // fp32 MFMA convolution GEMM.
 //
 // 256 threads = 4 waves in a WM x WN grid; each wave owns TM x TN tiles of
-// 16 x 16 (v_mfma_f32_16x16x4_f32).  K advances 32 floats per step: lane
-// (row = lane & 15, group = lane >> 4) loads 8 consecutive floats at
-// k + 8 * group of its A row and of its W row, and MFMA e (0..7) takes
-// element e, so one MFMA's four k-slots are k + 8g + e for g = 0..3 -- the
-// same k for A and W, hence a valid (reordered) dot product.  Both operands
-// come straight from global memory (L1/L2): a lane's 32 bytes are contiguous
-// and four lanes cover 128 contiguous bytes of a row.
+// 16 x 16 (v_mfma_f32_16x16x4_f32).  K advances 32 floats per step through
+// two LDS buffers: the block's threads read the next step's A rows (from the
+// extended buffer, at the tap's row offset) and W rows from global memory into
+// registers -- 128 contiguous bytes per row, 8 threads per row -- while the
+// waves run the current step's MFMAs from LDS, then store them into the other
+// buffer; one barrier per step.  In a step, lane (row = lane & 15,
+// group = lane >> 4) reads 8 consecutive floats at k = 8 * group of its A row
+// and of its W row, and MFMA e (0..7) takes element e, so one MFMA's four
+// k-slots are 8g + e for g = 0..3: the same k for A and W, a valid
+// (reordered) dot product.  Rows are padded to 36 floats in LDS.
 //
-// Split-K: slice z of Z covers a contiguous range of the 32-float steps.
-// Every slice stores its partial tile; the last to arrive at the tile's
-// counter sums the Z partials in slice order (deterministic), runs the
-// epilogue and re-arms the counter for the next launch.
+// Split-K: slice z of Z covers a contiguous range of the steps and stores its
+// partial tile; conv_gemm_reduce_kernel then sums them.  (An in-kernel
+// last-arriver fix-up needs device-scope release/acquire fences, which write
+// back and invalidate L2 and cost ~100 us per launch here.)
 // ---------------------------------------------------------------------------
+template <int TM, int TN>
+__device__ __forceinline__ float* partial_slot(const ConvGemmArgs& g, size_t tiles, size_t tile, int z, int wave, int i,
+                                               int j, int lane) {
+    return g.partial + ((((size_t)z * tiles + tile) * 4 + wave) * (TM * TN) + (i * TN + j)) * 256 + lane * 4;
+}
+
+// Lane (row16 = lane & 15, group = lane >> 4) of wave `wave` holds, for its
+// 16 x 16 sub-tile (i, j), rows 4 * group + r (r = 0..3) of column row16.
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void subtile_epilogue(const ConvGemmArgs& g, const floatx4& acc, int tile_m, int tile_n,
+                                                 int wave, int i, int j, int lane) {
+    constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
+    const int wm = wave / WN, wn = wave % WN;
+    const int col0 = tile_n * BN + (wn * TN + j) * 16;
+    if (col0 >= g.n) return;  // wave-uniform (n % 16 == 0)
+    const int col = col0 + (lane & 15);
+    const int ch = col % g.channels_out;
+    const int p0 = tile_m * BM + (wm * TM + i) * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (p0 + r < g.m) conv_epilogue(g, p0 + r, col, ch, acc[r]);
+}
+
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void tile_epilogue(const ConvGemmArgs& g, const floatx4 (&acc)[TM][TN], int tile_m,
+                                              int tile_n, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) subtile_epilogue<TM, TN, WM, WN>(g, acc[i][j], tile_m, tile_n, wave, i, j, lane);
+}
+
+constexpr int kLdsRow = 36;
+
 template <int TM, int TN, int WM, int WN>
 __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvGemmArgs g) {
     static_assert(WM * WN == 4, "4 waves");
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int A_VEC = BM * 8, W_VEC = BN * 8;  // float4 per step
+    constexpr int A_PER = (A_VEC + 255) / 256, W_PER = (W_VEC + 255) / 256;
+    // every thread copies A_PER + W_PER vectors; rows past the tile (small
+    // tiles) are loaded from clamped addresses into spare LDS rows, unused
+    __shared__ float lds_a[2][A_PER * 32 * kLdsRow];
+    __shared__ float lds_w[2][W_PER * 32 * kLdsRow];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int row16 = lane & 15, group = lane >> 4;
-    const int p_base = blockIdx.y * BM + wm * 16 * TM;
-    const int col_base = blockIdx.x * BN + wn * 16 * TN;
 
-    const float* a_row[TM];
+    // global -> LDS copy assignment: vector v = tid + 256 * r covers row v / 8, float4 v % 8
+    const float* a_src[A_PER];
+    const float* w_src[W_PER];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int p = min(p_base + i * 16 + row16, g.m - 1);
-        a_row[i] = g.a + (size_t)p * g.channels_in + 8 * group;
+    for (int r = 0; r < A_PER; ++r) {
+        const int v = tid + 256 * r;
+        const int p = min((int)(blockIdx.y * BM) + v / 8, g.m - 1);
+        a_src[r] = g.a + (size_t)p * g.channels_in + (v % 8) * 4;
     }
-    bool n_ok[TN];
-    const float* w_row[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        n_ok[j] = col_base + j * 16 < g.n;  // wave-uniform (n % 16 == 0)
-        const int col = min(col_base + j * 16 + row16, g.n - 1);
-        w_row[j] = g.w + (size_t)col * g.k + 8 * group;
+    for (int r = 0; r < W_PER; ++r) {
+        const int v = tid + 256 * r;
+        const int col = min((int)(blockIdx.x * BN) + v / 8, g.n - 1);
+        w_src[r] = g.w + (size_t)col * g.k + (v % 8) * 4;
     }
 
     const int steps = g.k >> 5;
     const int s0 = (int)((long long)steps * blockIdx.z / g.splits);
     const int s1 = (int)((long long)steps * (blockIdx.z + 1) / g.splits);
-    // (tap, channel) of step s0, advanced incrementally (channels_in % 32 == 0)
+    // (tap, channel) of the next step to load (channels_in % 32 == 0)
     int tap = (s0 * 32) / g.channels_in;
     int chan = s0 * 32 - tap * g.channels_in;
+    int s_load = s0;
     const size_t tap_stride = (size_t)g.dilation * g.channels_in;
 
     floatx4 acc[TM][TN];
@@ -114,189 +158,188 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvGemmArgs g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float4 a_cur[TM][2], w_cur[TN][2];
-    auto load_step = [&](int s, int t, int c, float4 (&av)[TM][2], float4 (&wv)[TN][2]) {
-        const size_t a_off = (size_t)t * tap_stride + c;
+    float4 a_reg[A_PER], w_reg[W_PER];
+    auto fetch = [&]() {
+        const size_t a_off = (size_t)tap * tap_stride + chan;
+        const size_t w_off = (size_t)s_load * 32;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            av[i][0] = load4(a_row[i] + a_off);
-            av[i][1] = load4(a_row[i] + a_off + 4);
-        }
+        for (int r = 0; r < A_PER; ++r) a_reg[r] = load4(a_src[r] + a_off);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            if (n_ok[j]) {
-                wv[j][0] = load4(w_row[j] + (size_t)s * 32);
-                wv[j][1] = load4(w_row[j] + (size_t)s * 32 + 4);
-            }
-        }
-    };
-    if (s0 < s1) load_step(s0, tap, chan, a_cur, w_cur);
-    for (int s = s0; s < s1; ++s) {
-        float4 a_nxt[TM][2], w_nxt[TN][2];
+        for (int r = 0; r < W_PER; ++r) w_reg[r] = load4(w_src[r] + w_off);
+        ++s_load;
         chan += 32;
         if (chan == g.channels_in) {
             chan = 0;
             ++tap;
         }
-        const bool more = s + 1 < s1;
-        if (more) load_step(s + 1, tap, chan, a_nxt, w_nxt);
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < A_PER; ++r) {
+            const int v = tid + 256 * r;
+            *reinterpret_cast<float4*>(&lds_a[buf][(v / 8) * kLdsRow + (v % 8) * 4]) = a_reg[r];
+        }
+#pragma unroll
+        for (int r = 0; r < W_PER; ++r) {
+            const int v = tid + 256 * r;
+            *reinterpret_cast<float4*>(&lds_w[buf][(v / 8) * kLdsRow + (v % 8) * 4]) = w_reg[r];
+        }
+    };
+    auto compute = [&](int buf) {
+        float4 av[TM][2], wv[TN][2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const float* src = &lds_a[buf][((wm * TM + i) * 16 + row16) * kLdsRow + 8 * group];
+            av[i][0] = *reinterpret_cast<const float4*>(src);
+            av[i][1] = *reinterpret_cast<const float4*>(src + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const float* src = &lds_w[buf][((wn * TN + j) * 16 + row16) * kLdsRow + 8 * group];
+            wv[j][0] = *reinterpret_cast<const float4*>(src);
+            wv[j][1] = *reinterpret_cast<const float4*>(src + 4);
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const float4& a4 = a_cur[i][e >> 2];
-                const float av = (e & 3) == 0 ? a4.x : (e & 3) == 1 ? a4.y : (e & 3) == 2 ? a4.z : a4.w;
+                const float4& a4 = av[i][e >> 2];
+                const float x = (e & 3) == 0 ? a4.x : (e & 3) == 1 ? a4.y : (e & 3) == 2 ? a4.z : a4.w;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    if (!n_ok[j]) continue;
-                    const float4& w4 = w_cur[j][e >> 2];
-                    const float wv = (e & 3) == 0 ? w4.x : (e & 3) == 1 ? w4.y : (e & 3) == 2 ? w4.z : w4.w;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wv, acc[i][j], 0, 0, 0);
+                    const float4& w4 = wv[j][e >> 2];
+                    const float y = (e & 3) == 0 ? w4.x : (e & 3) == 1 ? w4.y : (e & 3) == 2 ? w4.z : w4.w;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[i][j], 0, 0, 0);
                 }
             }
         }
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                a_cur[i][0] = a_nxt[i][0];
-                a_cur[i][1] = a_nxt[i][1];
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                w_cur[j][0] = w_nxt[j][0];
-                w_cur[j][1] = w_nxt[j][1];
-            }
+    };
+    if (s0 < s1) {
+        fetch();
+        stash(0);
+        __syncthreads();
+        for (int s = s0; s < s1; ++s) {
+            const int buf = (s - s0) & 1;
+            const bool more = s + 1 < s1;
+            if (more) fetch();
+            compute(buf);
+            if (more) stash(buf ^ 1);
+            __syncthreads();
         }
     }
-
     if (g.splits > 1) {
+        // partial tile of slice z, lane-major: the reduction kernel reads it back
+        // with the same thread mapping
         const size_t tiles = (size_t)gridDim.x * gridDim.y;
         const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
-        auto slot = [&](int z, int i, int j) {
-            return g.partial + ((((size_t)z * tiles + tile) * 4 + wave) * (TM * TN) + (i * TN + j)) * 256 + lane * 4;
-        };
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) *reinterpret_cast<floatx4*>(slot(blockIdx.z, i, j)) = acc[i][j];
-        __threadfence();
-        __syncthreads();
-        __shared__ int last;
-        if (threadIdx.x == 0) {
-            const unsigned prev = __hip_atomic_fetch_add(g.counters + tile, 1u, __ATOMIC_ACQ_REL,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            last = prev == (unsigned)(g.splits - 1);
-        }
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                floatx4 sum = *reinterpret_cast<const floatx4*>(slot(0, i, j));
-                for (int z = 1; z < g.splits; ++z) sum += *reinterpret_cast<const floatx4*>(slot(z, i, j));
-                acc[i][j] = sum;
-            }
-        if (threadIdx.x == 0)
-            __hip_atomic_store(g.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int j = 0; j < TN; ++j)
+                *reinterpret_cast<floatx4*>(partial_slot<TM, TN>(g, tiles, tile, blockIdx.z, wave, i, j, lane)) =
+                    acc[i][j];
+        return;
     }
+    tile_epilogue<TM, TN, WM, WN>(g, acc, blockIdx.y, blockIdx.x, wave, lane);
+}
 
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        if (!n_ok[j]) continue;
-        const int col = col_base + j * 16 + row16;
-        const int ch = col % g.channels_out;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int p = p_base + i * 16 + 4 * group + r;
-                if (p < g.m) conv_epilogue(g, p, col, ch, acc[i][j][r]);
-            }
-        }
-    }
+// Split-K reduction: one 64-lane block per 16 x 16 sub-tile (the lanes of the
+// wave that computed it) sums the slices' partials in slice order
+// (deterministic) and runs the epilogue.
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(64) void conv_gemm_reduce_kernel(ConvGemmArgs g) {
+    const int lane = threadIdx.x;
+    const int sub = blockIdx.z;  // (wave, i, j)
+    const int wave = sub / (TM * TN), i = (sub / TN) % TM, j = sub % TN;
+    const size_t tiles = (size_t)gridDim.x * gridDim.y;
+    const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+    floatx4 sum = *reinterpret_cast<const floatx4*>(partial_slot<TM, TN>(g, tiles, tile, 0, wave, i, j, lane));
+    for (int z = 1; z < g.splits; ++z)
+        sum += *reinterpret_cast<const floatx4*>(partial_slot<TM, TN>(g, tiles, tile, z, wave, i, j, lane));
+    subtile_epilogue<TM, TN, WM, WN>(g, sum, blockIdx.y, blockIdx.x, wave, i, j, lane);
 }
 
 // ---------------------------------------------------------------------------
 // Rows GEMV for 1..4 rows (transformer projections, RVQ projection, causal
-// pre-convolution): the rows are staged in LDS (RMSNorm applied there when
-// asked, CS:414-434), each wave computes whole output channels with float4
-// weight loads along k and a butterfly sum.
+// pre-convolution).  One wave per block computes kCpw output channels: its
+// lanes hold the rows in registers (float4 at k = 256 * c + 4 * lane, read
+// from L2), apply RMSNorm there when asked (CS:414-434: each wave reduces the
+// row's squares itself), stream each channel's weight row with float4 loads
+// and finish with a butterfly sum.  No LDS and no barrier: the launch's
+// latency is one weight read plus one reduction.
 // ---------------------------------------------------------------------------
 constexpr int kMaxRows = 4;
 
-template <int kCpw>
-__global__ __launch_bounds__(256) void rows_gemv_kernel(RowsGemvArgs g) {
-    extern __shared__ float xs[];
-    __shared__ float row_scale[kMaxRows];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int total = g.rows * g.k;
-    for (int idx = threadIdx.x * 4; idx < total; idx += 256 * 4) {
-        const int r = idx / g.k, c = idx - r * g.k;
-        *reinterpret_cast<float4*>(xs + idx) = load4(g.x + (size_t)r * g.ldx + c);
+template <int kChunks, int kCpw>
+__global__ __launch_bounds__(64) void rows_gemv_kernel(RowsGemvArgs g) {
+    const int lane = threadIdx.x;
+    float4 x[kMaxRows][kChunks];
+#pragma unroll
+    for (int r = 0; r < kMaxRows; ++r) {
+        const int rr = min(r, g.rows - 1);
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) x[r][c] = load4(g.x + (size_t)rr * g.ldx + c * 256 + lane * 4);
     }
-    __syncthreads();
     if (g.norm) {
-        if (wave < g.rows) {
-            float sq = 0.f;
-            for (int c = lane; c < g.k; c += 64) sq = fmaf(xs[wave * g.k + c], xs[wave * g.k + c], sq);
-            sq = wave_sum(sq);
-            if (lane == 0) row_scale[wave] = 1.0f / sqrtf(sq / (float)g.k + 1.0e-5f);
-        }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < total; idx += 256) {
-            const int r = idx / g.k, c = idx - r * g.k;
-            xs[idx] = xs[idx] * row_scale[r] * g.norm[c];
-        }
-        __syncthreads();
-    }
-    if (g.advance_position && blockIdx.x == 0 && threadIdx.x == 0) *g.advance_position += g.advance_by;
-
-    const bool pair = g.epilogue == kRowsSiluPair;
-#pragma unroll
-    for (int j = 0; j < kCpw; ++j) {
-        const int ch = (blockIdx.x * 4 + wave) * kCpw + j;
-        if (ch >= g.n) break;
-        const float* wa = g.w + (size_t)ch * g.k;
-        const float* wb = pair ? g.w + (size_t)(g.n + ch) * g.k : nullptr;
-        float acc_a[kMaxRows] = {0.f, 0.f, 0.f, 0.f};
-        float acc_b[kMaxRows] = {0.f, 0.f, 0.f, 0.f};
-        for (int c = lane * 4; c < g.k; c += 256) {
-            const float4 va = load4(wa + c);
-            float4 vb = {0.f, 0.f, 0.f, 0.f};
-            if (pair) vb = load4(wb + c);
-#pragma unroll
-            for (int r = 0; r < kMaxRows; ++r) {
-                if (r >= g.rows) break;
-                const float4 x = *reinterpret_cast<const float4*>(xs + r * g.k + c);
-                float s = acc_a[r];
-                s = fmaf(va.x, x.x, s);
-                s = fmaf(va.y, x.y, s);
-                s = fmaf(va.z, x.z, s);
-                s = fmaf(va.w, x.w, s);
-                acc_a[r] = s;
-                if (pair) {
-                    float t = acc_b[r];
-                    t = fmaf(vb.x, x.x, t);
-                    t = fmaf(vb.y, x.y, t);
-                    t = fmaf(vb.z, x.z, t);
-                    t = fmaf(vb.w, x.w, t);
-                    acc_b[r] = t;
-                }
-            }
-        }
 #pragma unroll
         for (int r = 0; r < kMaxRows; ++r) {
-            if (r >= g.rows) break;
-            const float a = wave_sum(acc_a[r]);
-            const float b = pair ? wave_sum(acc_b[r]) : 0.f;
-            if (lane != r) continue;
+            float sq = 0.f;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                sq = fmaf(x[r][c].x, x[r][c].x, sq);
+                sq = fmaf(x[r][c].y, x[r][c].y, sq);
+                sq = fmaf(x[r][c].z, x[r][c].z, sq);
+                sq = fmaf(x[r][c].w, x[r][c].w, sq);
+            }
+            const float scale = 1.0f / sqrtf(wave_sum(sq) / (float)g.k + 1.0e-5f);
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const float4 nw = load4(g.norm + c * 256 + lane * 4);
+                x[r][c].x = x[r][c].x * scale * nw.x;
+                x[r][c].y = x[r][c].y * scale * nw.y;
+                x[r][c].z = x[r][c].z * scale * nw.z;
+                x[r][c].w = x[r][c].w * scale * nw.w;
+            }
+        }
+    }
+    if (g.advance_position && blockIdx.x == 0 && lane == 0) *g.advance_position += g.advance_by;
+
+    const bool pair = g.epilogue == kRowsSiluPair;
+    auto dot_rows = [&](const float* wrow, float (&acc)[kMaxRows]) {
+        float4 wv[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) wv[c] = load4(wrow + c * 256 + lane * 4);
+#pragma unroll
+        for (int r = 0; r < kMaxRows; ++r) {
+            float s = 0.f;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                s = fmaf(wv[c].x, x[r][c].x, s);
+                s = fmaf(wv[c].y, x[r][c].y, s);
+                s = fmaf(wv[c].z, x[r][c].z, s);
+                s = fmaf(wv[c].w, x[r][c].w, s);
+            }
+            acc[r] = wave_sum(s);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < kCpw; ++j) {
+        const int ch = blockIdx.x * kCpw + j;
+        if (ch >= g.n) break;
+        float a[kMaxRows], b[kMaxRows];
+        dot_rows(g.w + (size_t)ch * g.k, a);
+        if (pair) dot_rows(g.w + (size_t)(g.n + ch) * g.k, b);
+        const int r = lane;
+        if (r < g.rows) {
+            float va = a[0], vb = b[0];
+#pragma unroll
+            for (int q = 1; q < kMaxRows; ++q)
+                if (r == q) va = a[q], vb = b[q];
             float v;
             if (pair) {
-                v = (a / (1.0f + q3_expf(-a))) * b;  // CS:687-698
+                v = (va / (1.0f + q3_expf(-va))) * vb;  // CS:687-698
             } else {
-                v = g.bias ? a + g.bias[ch] : a;
+                v = g.bias ? va + g.bias[ch] : va;
                 if (g.epilogue == kRowsScaledResidual) v = g.residual[(size_t)r * g.ldo + ch] + v * g.scale[ch];
             }
             g.out[(size_t)r * g.ldo + ch] = v;
@@ -306,91 +349,95 @@ __global__ __launch_bounds__(256) void rows_gemv_kernel(RowsGemvArgs g) {
 
 // ---------------------------------------------------------------------------
 // Transformer attention of one packet (CS:464-494 RoPE, CS:496-566 sliding
-// attention).  One block per head; the block assembles in LDS the keys and
-// values of positions [first(frame 0), last frame]: older ones from the ring,
-// the packet's own freshly rotated rows from registers.  Wave f attends for
-// frame f.  Scores, the max, the exponentials, the sequential denominator and
-// the ordered value sum follow the reference's per-head loop.
+// attention).  One block per (head, frame).  Each block rotates the packet's
+// own keys itself (so no block reads a ring slot another block writes in the
+// same launch), takes older keys and values from the ring, and follows the
+// reference's per-head loop: scores, max, exponentials, the sequential
+// denominator and the ordered value sum.  Frame 0's block appends the
+// packet's keys and values to the ring.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void codec_attention_kernel(const float* qkv, int frames,
                                                               const unsigned long long* position, float* kv_k,
                                                               float* kv_v, float* out) {
-    constexpr int kRows = kWindow + kMaxFrames - 1;
-    __shared__ float q_s[kMaxFrames][64];
-    __shared__ float k_s[kRows][65];
-    __shared__ float v_s[kRows][65];
-    __shared__ float p_s[kMaxFrames][kWindow];
-    __shared__ float denom_s[kMaxFrames];
-    const int head = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ float q_s[64];
+    __shared__ float k_s[kWindow][65];
+    __shared__ float v_s[kWindow][65];
+    __shared__ float p_s[kWindow];
+    __shared__ float denom_s;
+    const int head = blockIdx.x, f = blockIdx.y;
+    const int tid = threadIdx.x;
     const unsigned long long pos = *position;
-    const unsigned long long first_all = pos + 1 > (unsigned long long)kWindow ? pos + 1 - kWindow : 0ull;
-    const int old_rows = (int)(pos - first_all);
+    const unsigned long long me = pos + (unsigned long long)f;
+    const unsigned long long first = me + 1 > (unsigned long long)kWindow ? me + 1 - kWindow : 0ull;
+    const int count = (int)(me - first + 1);
+    const int old_rows = (int)(pos - first);  // window rows before the packet
     float* ring_k = kv_k + (size_t)head * kKvSlots * 64;
     float* ring_v = kv_v + (size_t)head * kKvSlots * 64;
     for (int idx = tid; idx < old_rows * 64; idx += 256) {
         const int j = idx >> 6, d = idx & 63;
-        const int slot = (int)((first_all + (unsigned long long)j) % kKvSlots);
+        const int slot = (int)((first + (unsigned long long)j) % kKvSlots);
         k_s[j][d] = ring_k[slot * 64 + d];
         v_s[j][d] = ring_v[slot * 64 + d];
     }
-    if (tid < frames * 32) {
-        const int f = tid >> 5, d = tid & 31;
-        const float* row = qkv + (size_t)f * 3 * 1024 + head * 64;
+    if (tid < (f + 1) * 32) {  // the packet's frames 0..f, rotate-half pairs (d, d + 32)
+        const int g = tid >> 5, d = tid & 31;
+        const float* row = qkv + (size_t)g * 3 * 1024 + head * 64;
         const float frequency = 1.0f / powf(10000.0f, (float)(2 * d) / 64.0f);
-        const float angle = (float)(pos + (unsigned long long)f) * frequency;
+        const float angle = (float)(pos + (unsigned long long)g) * frequency;
         const float sine = sinf(angle), cosine = cosf(angle);
-        const float q1 = row[d], q2 = row[d + 32];
         const float k1 = row[1024 + d], k2 = row[1024 + d + 32];
-        const float v1 = row[2048 + d], v2 = row[2048 + d + 32];
-        q_s[f][d] = q1 * cosine - q2 * sine;
-        q_s[f][d + 32] = q2 * cosine + q1 * sine;
         const float r1 = k1 * cosine - k2 * sine, r2 = k2 * cosine + k1 * sine;
-        const int j = old_rows + f;
+        const float v1 = row[2048 + d], v2 = row[2048 + d + 32];
+        const int j = old_rows + g;
         k_s[j][d] = r1;
         k_s[j][d + 32] = r2;
         v_s[j][d] = v1;
         v_s[j][d + 32] = v2;
-        const int slot = (int)((pos + (unsigned long long)f) % kKvSlots);
-        ring_k[slot * 64 + d] = r1;
-        ring_k[slot * 64 + d + 32] = r2;
-        ring_v[slot * 64 + d] = v1;
-        ring_v[slot * 64 + d + 32] = v2;
-    }
-    __syncthreads();
-    const int f = wave;
-    const bool active = f < frames;
-    const unsigned long long me = pos + (unsigned long long)f;
-    const unsigned long long first = me + 1 > (unsigned long long)kWindow ? me + 1 - kWindow : 0ull;
-    const int j0 = (int)(first - first_all);
-    const int count = (int)(me - first + 1);
-    float local_max = -3.402823466e+38f;
-    if (active) {
-        for (int jj = lane; jj < count; jj += 64) {
-            float score = 0.f;
-            for (int d = 0; d < 64; ++d) score = fmaf(q_s[f][d], k_s[j0 + jj][d], score);
-            score *= 0.125f;
-            p_s[f][jj] = score;
-            local_max = fmaxf(local_max, score);
+        if (g == f) {
+            const float q1 = row[d], q2 = row[d + 32];
+            q_s[d] = q1 * cosine - q2 * sine;
+            q_s[d + 32] = q2 * cosine + q1 * sine;
         }
     }
-    const float maximum = wave_max(local_max);
-    __syncthreads();
-    if (active) {
-        for (int jj = lane; jj < count; jj += 64) p_s[f][jj] = q3_expf(p_s[f][jj] - maximum);
+    if (f == 0 && tid < frames * 32) {  // append the packet's rows to the ring
+        const int g = tid >> 5, d = tid & 31;
+        const float* row = qkv + (size_t)g * 3 * 1024 + head * 64;
+        const float frequency = 1.0f / powf(10000.0f, (float)(2 * d) / 64.0f);
+        const float angle = (float)(pos + (unsigned long long)g) * frequency;
+        const float sine = sinf(angle), cosine = cosf(angle);
+        const float k1 = row[1024 + d], k2 = row[1024 + d + 32];
+        const int slot = (int)((pos + (unsigned long long)g) % kKvSlots);
+        ring_k[slot * 64 + d] = k1 * cosine - k2 * sine;
+        ring_k[slot * 64 + d + 32] = k2 * cosine + k1 * sine;
+        ring_v[slot * 64 + d] = row[2048 + d];
+        ring_v[slot * 64 + d + 32] = row[2048 + d + 32];
     }
     __syncthreads();
-    if (active && lane == 0) {
+    float score = -3.402823466e+38f;
+    if (tid < count) {
+        float sc = 0.f;
+        for (int d = 0; d < 64; ++d) sc = fmaf(q_s[d], k_s[tid][d], sc);
+        score = sc * 0.125f;
+    }
+    // max over the window: waves, then the block
+    __shared__ float wmax[4];
+    float m = wave_max(score);
+    if ((tid & 63) == 0) wmax[tid >> 6] = m;
+    __syncthreads();
+    const float maximum = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    if (tid < count) p_s[tid] = q3_expf(score - maximum);
+    __syncthreads();
+    if (tid == 0) {
         float denominator = 0.f;
-        for (int jj = 0; jj < count; ++jj) denominator += p_s[f][jj];
-        denom_s[f] = denominator;
+        for (int j = 0; j < count; ++j) denominator += p_s[j];
+        denom_s = denominator;
     }
     __syncthreads();
-    if (active) {
-        const float denominator = denom_s[f];
+    if (tid < 64) {
+        const float denominator = denom_s;
         float result = 0.f;
-        for (int jj = 0; jj < count; ++jj) result = fmaf(p_s[f][jj] / denominator, v_s[j0 + jj][lane], result);
-        out[(size_t)f * 1024 + head * 64 + lane] = result;
+        for (int j = 0; j < count; ++j) result = fmaf(p_s[j] / denominator, v_s[j][tid], result);
+        out[(size_t)f * 1024 + head * 64 + tid] = result;
     }
 }
 
@@ -402,27 +449,38 @@ struct FrontendTables {
     const float* usage[kCodebooks];
 };
 
-__device__ void copy_segments_block(const CopySegment* seg, int segments, int block, int blocks) {
-    for (int s = 0; s < segments; ++s) {
-        const unsigned n4 = seg[s].floats >> 2;
-        const float4* src = reinterpret_cast<const float4*>(seg[s].src);
-        float4* dst = reinterpret_cast<float4*>(seg[s].dst);
-        for (unsigned i = block * 256 + threadIdx.x; i < n4; i += blocks * 256) dst[i] = src[i];
-    }
+// Segment blockIdx.y, chunk `block` of `blocks`.
+__device__ void copy_segment_chunk(const CopySegment* seg, int block, int blocks) {
+    const CopySegment sg = seg[blockIdx.y];
+    const unsigned n4 = sg.floats >> 2;
+    const float4* src = reinterpret_cast<const float4*>(sg.src);
+    float4* dst = reinterpret_cast<float4*>(sg.dst);
+    for (unsigned i = block * 256 + threadIdx.x; i < n4; i += blocks * 256) dst[i] = src[i];
 }
 
+// blockIdx.y = segment; on segment row 0 the first `frames` blocks also
+// gather frame blockIdx.x's codebook entries (all 16 lookups issued at once).
 __global__ __launch_bounds__(256) void codec_frontend_kernel(const uint16_t* codes, int frames, FrontendTables t,
-                                                             float* x, const CopySegment* seg, int segments) {
-    if ((int)blockIdx.x < frames) {
+                                                             float* x, const CopySegment* seg) {
+    if (blockIdx.y == 0 && (int)blockIdx.x < frames) {
         const int f = blockIdx.x, d = threadIdx.x;
-        float acoustic = 0.f;
-#pragma unroll 1
+        int code[kCodebooks];
+        float usage[kCodebooks], emb[kCodebooks];
+#pragma unroll
         for (int cb = 0; cb < kCodebooks; ++cb) {
             // codes beyond the 2048-entry codebooks are clamped so a corrupt
             // device frame cannot read outside the table
-            const int code = min((int)codes[f * kCodebooks + cb], 2047);
-            const float usage = fmaxf(t.usage[cb][code], 1.0e-5f);
-            const float value = t.emb[cb][(size_t)code * 256 + d] / usage;
+            code[cb] = min((int)codes[f * kCodebooks + cb], 2047);
+        }
+#pragma unroll
+        for (int cb = 0; cb < kCodebooks; ++cb) {
+            usage[cb] = t.usage[cb][code[cb]];
+            emb[cb] = t.emb[cb][(size_t)code[cb] * 256 + d];
+        }
+        float acoustic = 0.f;
+#pragma unroll
+        for (int cb = 0; cb < kCodebooks; ++cb) {
+            const float value = emb[cb] / fmaxf(usage[cb], 1.0e-5f);
             if (cb == 0) {
                 x[f * 512 + d] = value;
             } else {
@@ -430,13 +488,12 @@ __global__ __launch_bounds__(256) void codec_frontend_kernel(const uint16_t* cod
             }
         }
         x[f * 512 + 256 + d] = acoustic;
-    } else {
-        copy_segments_block(seg, segments, blockIdx.x - frames, gridDim.x - frames);
     }
+    copy_segment_chunk(seg, blockIdx.x, gridDim.x);
 }
 
-__global__ __launch_bounds__(256) void copy_segments_kernel(const CopySegment* seg, int segments) {
-    copy_segments_block(seg, segments, blockIdx.x, gridDim.x);
+__global__ __launch_bounds__(256) void copy_segments_kernel(const CopySegment* seg) {
+    copy_segment_chunk(seg, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -484,18 +541,30 @@ __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(const float* ext,
 // Final causal convolution 96 -> 1 (CS:1699-1782 with the im2col column order
 // channel-major, tap-minor), bias, clamp (CS:1126-1131), PCM (CS:1133-1143).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void final_conv_pcm_kernel(const float* ext, int positions, const float* w,
-                                                             const float* b, int16_t* pcm, float* preclamp,
-                                                             float* clamped) {
+// One wave per 64 positions: the 70 input rows it needs are staged in LDS
+// (rows padded to 97 floats: conflict-free column reads); each lane keeps the
+// sequential channel-major, tap-minor fmaf chain of its position.
+__global__ __launch_bounds__(64) void final_conv_pcm_kernel(const float* ext, int positions, const float* w,
+                                                            const float* b, int16_t* pcm, float* preclamp,
+                                                            float* clamped) {
+    constexpr int kRow = 97;
     __shared__ float ws[96 * 7];
-    for (int i = threadIdx.x; i < 96 * 7; i += 256) ws[i] = w[i];
+    __shared__ float xs[70 * kRow];
+    const int p0 = blockIdx.x * 64;
+    for (int i = threadIdx.x; i < 96 * 7; i += 64) ws[i] = w[i];
+    const int rows = min(70, positions - p0 + 6);
+    for (int i = threadIdx.x; i < rows * 96; i += 64) {
+        const int r = i / 96, c = i - r * 96;
+        xs[r * kRow + c] = ext[(size_t)(p0 + r) * 96 + c];
+    }
     __syncthreads();
-    const int p = blockIdx.x * 256 + threadIdx.x;
+    const int p = p0 + threadIdx.x;
     if (p >= positions) return;
+    const float* xp = xs + threadIdx.x * kRow;
     float acc = 0.f;
     for (int c = 0; c < 96; ++c) {
 #pragma unroll
-        for (int t = 0; t < 7; ++t) acc = fmaf(ext[(size_t)(p + t) * 96 + c], ws[c * 7 + t], acc);
+        for (int t = 0; t < 7; ++t) acc = fmaf(xp[t * kRow + c], ws[c * 7 + t], acc);
     }
     const float v = acc + b[0];
     if (preclamp) preclamp[p] = v;
@@ -546,10 +615,6 @@ __global__ void snake_params_kernel(float* alpha, float* beta, int channels) {
     }
 }
 
-__global__ void fill_u32_kernel(unsigned* dst, size_t count, unsigned value) {
-    for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) dst[i] = value;
-}
-
 __global__ void fill_f32_kernel(float* dst, size_t count, float value) {
     for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) dst[i] = value;
 }
@@ -571,38 +636,49 @@ GemmPlan plan_conv_gemm(int m, int n, int k, int cus) {
     const int bm = plan.shape == GemmShape::kSmall ? 16 : 64;
     plan.tiles_m = (m + bm - 1) / bm;
     plan.tiles_n = (n + 63) / 64;
-    const int steps = k / 32;
     const long long tiles = (long long)plan.tiles_m * plan.tiles_n;
-    // aim for two blocks per CU, each slice keeping at least 4 K-steps
-    long long want = (2LL * cus + tiles - 1) / tiles;
-    want = std::min<long long>(want, std::max(1, steps / 4));
-    plan.splits = (int)std::max<long long>(1, want);
+    // Weight-streaming shapes (16-row tiles) want ~2 blocks per CU in flight;
+    // MFMA-bound shapes one per CU, and none split once the tiles alone cover
+    // ~90 % of the CUs (the extra partial traffic and reduction cost more).
+    // Each slice keeps at least 4 K-steps.  (Measured on MI355X per layer.)
+    long long splits = 1;
+    if (plan.shape == GemmShape::kSmall) {
+        splits = (2LL * cus + tiles - 1) / tiles;
+    } else if (tiles * 10 < 9LL * cus) {
+        splits = (cus + tiles - 1) / tiles;
+    }
+    splits = std::min<long long>(splits, std::max(1, (k / 32) / 4));
+    plan.splits = (int)std::max<long long>(1, splits);
     return plan;
 }
 
 hipError_t launch_conv_gemm(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream) {
     if (args.k % 32 || args.channels_in % 32 || args.n % 16 || args.m < 1 || args.splits != plan.splits ||
-        (plan.splits > 1 && (!args.partial || !args.counters)))
+        (plan.splits > 1 && !args.partial))
         return hipErrorInvalidValue;
     const dim3 grid(plan.tiles_n, plan.tiles_m, plan.splits);
     if (plan.shape == GemmShape::kSmall) {
         conv_gemm_kernel<1, 1, 1, 4><<<grid, 256, 0, stream>>>(args);
+        if (plan.splits > 1)
+            conv_gemm_reduce_kernel<1, 1, 1, 4><<<dim3(plan.tiles_n, plan.tiles_m, 4), 64, 0, stream>>>(args);
     } else {
         conv_gemm_kernel<2, 2, 2, 2><<<grid, 256, 0, stream>>>(args);
+        if (plan.splits > 1)
+            conv_gemm_reduce_kernel<2, 2, 2, 2><<<dim3(plan.tiles_n, plan.tiles_m, 16), 64, 0, stream>>>(args);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_rows_gemv(const RowsGemvArgs& g, hipStream_t stream) {
     if (g.rows < 1 || g.rows > kMaxRows || g.k % 256 || g.ldx % 4 || g.n < 1) return hipErrorInvalidValue;
-    const size_t lds = (size_t)g.rows * g.k * sizeof(float);
-    if (lds > 64 * 1024) return hipErrorInvalidValue;
-    const int cpw = g.n >= 3072 ? 2 : 1;
-    const unsigned blocks = (unsigned)((g.n + 4 * cpw - 1) / (4 * cpw));
-    if (cpw == 2) {
-        rows_gemv_kernel<2><<<blocks, 256, lds, stream>>>(g);
-    } else {
-        rows_gemv_kernel<1><<<blocks, 256, lds, stream>>>(g);
+    // one output channel per single-wave block: >= 512 blocks for every
+    // projection of the decoder (n = 512 .. 3072)
+    const unsigned blocks = (unsigned)g.n;
+    switch (g.k / 256) {
+        case 2: rows_gemv_kernel<2, 1><<<blocks, 64, 0, stream>>>(g); break;
+        case 4: rows_gemv_kernel<4, 1><<<blocks, 64, 0, stream>>>(g); break;
+        case 6: rows_gemv_kernel<6, 1><<<blocks, 64, 0, stream>>>(g); break;
+        default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -610,7 +686,7 @@ hipError_t launch_rows_gemv(const RowsGemvArgs& g, hipStream_t stream) {
 hipError_t launch_codec_attention(const float* qkv, int frames, const unsigned long long* position, float* kv_k,
                                   float* kv_v, float* out, hipStream_t stream) {
     if (frames < 1 || frames > kMaxFrames) return hipErrorInvalidValue;
-    codec_attention_kernel<<<kHeads, 256, 0, stream>>>(qkv, frames, position, kv_k, kv_v, out);
+    codec_attention_kernel<<<dim3(kHeads, frames), 256, 0, stream>>>(qkv, frames, position, kv_k, kv_v, out);
     return hipGetLastError();
 }
 
@@ -623,14 +699,14 @@ hipError_t launch_codec_frontend(const uint16_t* codes, int frames, const float*
         t.emb[i] = embeddings[i];
         t.usage[i] = usages[i];
     }
-    const int copy_blocks = segments > 0 ? 64 : 0;
-    codec_frontend_kernel<<<frames + copy_blocks, 256, 0, stream>>>(codes, frames, t, x, seg, segments);
+    if (segments < 1) return hipErrorInvalidValue;
+    codec_frontend_kernel<<<dim3(8, segments), 256, 0, stream>>>(codes, frames, t, x, seg);
     return hipGetLastError();
 }
 
 hipError_t launch_copy_segments(const CopySegment* seg, int segments, hipStream_t stream) {
     if (segments <= 0) return hipSuccess;
-    copy_segments_kernel<<<64, 256, 0, stream>>>(seg, segments);
+    copy_segments_kernel<<<dim3(8, segments), 256, 0, stream>>>(seg);
     return hipGetLastError();
 }
 
@@ -642,8 +718,7 @@ hipError_t launch_dwconv_layernorm(const float* ext, int positions, const float*
 
 hipError_t launch_final_conv_pcm(const float* ext, int positions, const float* w, const float* b, int16_t* pcm,
                                  float* preclamp, float* clamped, hipStream_t stream) {
-    final_conv_pcm_kernel<<<(positions + 255) / 256, 256, 0, stream>>>(ext, positions, w, b, pcm, preclamp,
-                                                                        clamped);
+    final_conv_pcm_kernel<<<(positions + 63) / 64, 64, 0, stream>>>(ext, positions, w, b, pcm, preclamp, clamped);
     return hipGetLastError();
 }
 
@@ -666,11 +741,6 @@ hipError_t launch_repack_transpose(const float* src, int in_ch, int out_ch, int 
 
 hipError_t launch_snake_params(float* alpha, float* beta, int channels, hipStream_t stream) {
     snake_params_kernel<<<(channels + 255) / 256, 256, 0, stream>>>(alpha, beta, channels);
-    return hipGetLastError();
-}
-
-hipError_t launch_fill_u32(unsigned* dst, size_t count, unsigned value, hipStream_t stream) {
-    fill_u32_kernel<<<blocks_for(count), 256, 0, stream>>>(dst, count, value);
     return hipGetLastError();
 }
 

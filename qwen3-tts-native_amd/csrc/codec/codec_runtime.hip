@@ -275,7 +275,6 @@ struct Qwen3TtsCodecContextV1 {
     float *cur[4] = {}, *ext2[4] = {};
     float *preclamp = nullptr, *clamped = nullptr;
     float* partial = nullptr;
-    unsigned* counters = nullptr;
     CopySegment* seg_in[kMaxFrames + 1] = {};
     CopySegment* seg_out[kMaxFrames + 1] = {};
     Plans plans[kMaxFrames + 1];
@@ -348,7 +347,7 @@ void layout_session(Qwen3TtsCodecContextV1* s, Arena& a) {
     s->clamped = a.take<float>((size_t)F * kSamplesPerFrame);
     s->history_bytes = hist;
     // split-K workspace: the largest plan over every frame count
-    size_t partial = 0, tiles = 0;
+    size_t partial = 0;
     for (int f = 1; f <= kMaxFrames; ++f) {
         Plans& p = s->plans[f];
         for (int u = 0; u < 2; ++u) {
@@ -370,11 +369,9 @@ void layout_session(Qwen3TtsCodecContextV1* s, Arena& a) {
                                  &p.conv1[3]};
         for (const GemmPlan* g : all) {
             partial = std::max(partial, g->partial_floats());
-            tiles = std::max(tiles, g->tiles());
         }
     }
     s->partial = a.take<float>(std::max<size_t>(partial, 1));
-    s->counters = a.take<unsigned>(std::max<size_t>(tiles, 1));
     for (int f = 0; f <= kMaxFrames; ++f) {
         s->seg_in[f] = a.take<CopySegment>(kSegments);
         s->seg_out[f] = a.take<CopySegment>(kSegments);
@@ -458,7 +455,7 @@ struct Launcher {
               const float* gamma, float* out, float* snake_out, const float* alpha, const float* beta) {
         ConvGemmArgs g{a,   cin,    taps,     dilation, wt,    bias,      m,     n,     k,
                        cout, epilogue, residual, gamma,    out,   snake_out, alpha, beta, plan.splits,
-                       s->partial, s->counters};
+                       s->partial};
         ok(launch_conv_gemm(g, plan, s->stream));
     }
 

@@ -110,6 +110,79 @@ class DevicePacketFinish(C.Structure):
                 ("reserved_3", C.c_uint64)]
 
 
+STRIDES = (8, 5, 4, 3)
+STAGE_IN = (1536, 768, 384, 192)
+STAGE_OUT = (768, 384, 192, 96)
+
+
+def tensor_shapes() -> dict:
+    """Name -> PyTorch shape of the 271 decoder tensors a provider hands over
+    (the loader requires exactly 271 "decoder." tensors, CS:3281; the two RVQ
+    input projections are counted but not executed)."""
+    s = {}
+    q = "decoder.quantizer."
+    for cb in range(16):
+        p = q + ("rvq_first.vq.layers.0._codebook." if cb == 0 else f"rvq_rest.vq.layers.{cb - 1}._codebook.")
+        s[p + "embedding_sum"] = (2048, 256)
+        s[p + "cluster_usage"] = (2048,)
+    for part in ("rvq_first", "rvq_rest"):
+        s[f"{q}{part}.output_proj.weight"] = (512, 256, 1)
+        s[f"{q}{part}.input_proj.weight"] = (256, 512, 1)
+    s["decoder.pre_conv.conv.weight"], s["decoder.pre_conv.conv.bias"] = (1024, 512, 3), (1024,)
+    t = "decoder.pre_transformer."
+    s[t + "input_proj.weight"], s[t + "input_proj.bias"] = (512, 1024), (512,)
+    for l in range(8):
+        p = f"{t}layers.{l}."
+        for n, shape in (("input_layernorm.weight", (512,)), ("self_attn.q_proj.weight", (1024, 512)),
+                         ("self_attn.k_proj.weight", (1024, 512)), ("self_attn.v_proj.weight", (1024, 512)),
+                         ("self_attn.o_proj.weight", (512, 1024)), ("self_attn_layer_scale.scale", (512,)),
+                         ("post_attention_layernorm.weight", (512,)), ("mlp.gate_proj.weight", (1024, 512)),
+                         ("mlp.up_proj.weight", (1024, 512)), ("mlp.down_proj.weight", (512, 1024)),
+                         ("mlp_layer_scale.scale", (512,))):
+            s[p + n] = shape
+    s[t + "norm.weight"], s[t + "output_proj.weight"], s[t + "output_proj.bias"] = (512,), (1024, 512), (1024,)
+    for u in range(2):
+        p = f"decoder.upsample.{u}."
+        for n, shape in (("0.conv.weight", (1024, 1024, 2)), ("0.conv.bias", (1024,)),
+                         ("1.dwconv.conv.weight", (1024, 1, 7)), ("1.dwconv.conv.bias", (1024,)),
+                         ("1.norm.weight", (1024,)), ("1.norm.bias", (1024,)), ("1.pwconv1.weight", (4096, 1024)),
+                         ("1.pwconv1.bias", (4096,)), ("1.pwconv2.weight", (1024, 4096)),
+                         ("1.pwconv2.bias", (1024,)), ("1.gamma", (1024,))):
+            s[p + n] = shape
+    s["decoder.decoder.0.conv.weight"], s["decoder.decoder.0.conv.bias"] = (1536, 1024, 7), (1536,)
+    for b in range(4):
+        ci, co, st = STAGE_IN[b], STAGE_OUT[b], STRIDES[b]
+        p = f"decoder.decoder.{b + 1}.block."
+        s[p + "0.alpha"], s[p + "0.beta"] = (ci,), (ci,)
+        s[p + "1.conv.weight"], s[p + "1.conv.bias"] = (ci, co, 2 * st), (co,)
+        for u in range(3):
+            r = f"{p}{u + 2}."
+            for n, shape in (("act1.alpha", (co,)), ("act1.beta", (co,)), ("conv1.conv.weight", (co, co, 7)),
+                             ("conv1.conv.bias", (co,)), ("act2.alpha", (co,)), ("act2.beta", (co,)),
+                             ("conv2.conv.weight", (co, co, 1)), ("conv2.conv.bias", (co,))):
+                s[r + n] = shape
+    s["decoder.decoder.5.alpha"], s["decoder.decoder.5.beta"] = (96,), (96,)
+    s["decoder.decoder.6.conv.weight"], s["decoder.decoder.6.conv.bias"] = (1, 96, 7), (1,)
+    return s
+
+
+def packet_flops(frames: int) -> int:
+    """Multiply-add flops (2 per MAC) of one packet's matrix products."""
+    f = frames
+    t = 2 * f * (512 * 512 + 1024 * 1536 + 512 * 1024 + 8 * (3072 * 512 + 512 * 1024 + 2048 * 512 + 512 * 1024)
+                 + 1024 * 512)
+    up = sum(2 * (m * 2048 * 1024 + 2 * m * 4096 * 1024 * 2) for m in (f, 2 * f))
+    dec = 2 * 4 * f * 1536 * 7 * 1024
+    p = 4 * f
+    for b in range(4):
+        ci, co, st = STAGE_IN[b], STAGE_OUT[b], STRIDES[b]
+        dec += 2 * p * (st * co) * (2 * ci)
+        p *= st
+        dec += 3 * 2 * p * co * (7 * co + co)
+    dec += 2 * p * 96 * 7
+    return t + up + dec
+
+
 # Layouts pinned by the reference's Rust tests (ffi.rs:169-201).
 ABI_SIZES = {PacketResult: 40, DevicePacketBegin: 40, DevicePacketBeginResult: 32, DevicePacketFinish: 56}
 
