@@ -261,7 +261,7 @@ __global__ __launch_bounds__(64) void conv_gemm_reduce_kernel(ConvGemmArgs g) {
 
 // ---------------------------------------------------------------------------
 // Rows GEMV for 1..4 rows (transformer projections, RVQ projection, causal
-// pre-convolution).  One wave per block computes kCpw output channels: its
+// pre-convolution).  One wave per block computes one output channel: its
 // lanes hold the rows in registers (float4 at k = 256 * c + 4 * lane, read
 // from L2), apply RMSNorm there when asked (CS:414-434: each wave reduces the
 // row's squares itself), stream each channel's weight row with float4 loads
@@ -270,9 +270,19 @@ __global__ __launch_bounds__(64) void conv_gemm_reduce_kernel(ConvGemmArgs g) {
 // ---------------------------------------------------------------------------
 constexpr int kMaxRows = 4;
 
-template <int kChunks, int kCpw>
+template <int kChunks>
 __global__ __launch_bounds__(64) void rows_gemv_kernel(RowsGemvArgs g) {
     const int lane = threadIdx.x;
+    const int ch = blockIdx.x;
+    const bool pair = g.epilogue == kRowsSiluPair;
+    // the channel's weight row(s) first: the longest-latency reads
+    float4 wa[kChunks], wb[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) wa[c] = load4(g.w + (size_t)ch * g.k + c * 256 + lane * 4);
+    if (pair) {
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) wb[c] = load4(g.w + (size_t)(g.n + ch) * g.k + c * 256 + lane * 4);
+    }
     float4 x[kMaxRows][kChunks];
 #pragma unroll
     for (int r = 0; r < kMaxRows; ++r) {
@@ -281,6 +291,9 @@ __global__ __launch_bounds__(64) void rows_gemv_kernel(RowsGemvArgs g) {
         for (int c = 0; c < kChunks; ++c) x[r][c] = load4(g.x + (size_t)rr * g.ldx + c * 256 + lane * 4);
     }
     if (g.norm) {
+        float4 nw[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) nw[c] = load4(g.norm + c * 256 + lane * 4);
 #pragma unroll
         for (int r = 0; r < kMaxRows; ++r) {
             float sq = 0.f;
@@ -294,21 +307,16 @@ __global__ __launch_bounds__(64) void rows_gemv_kernel(RowsGemvArgs g) {
             const float scale = 1.0f / sqrtf(wave_sum(sq) / (float)g.k + 1.0e-5f);
 #pragma unroll
             for (int c = 0; c < kChunks; ++c) {
-                const float4 nw = load4(g.norm + c * 256 + lane * 4);
-                x[r][c].x = x[r][c].x * scale * nw.x;
-                x[r][c].y = x[r][c].y * scale * nw.y;
-                x[r][c].z = x[r][c].z * scale * nw.z;
-                x[r][c].w = x[r][c].w * scale * nw.w;
+                x[r][c].x = x[r][c].x * scale * nw[c].x;
+                x[r][c].y = x[r][c].y * scale * nw[c].y;
+                x[r][c].z = x[r][c].z * scale * nw[c].z;
+                x[r][c].w = x[r][c].w * scale * nw[c].w;
             }
         }
     }
-    if (g.advance_position && blockIdx.x == 0 && lane == 0) *g.advance_position += g.advance_by;
+    if (g.advance_position && ch == 0 && lane == 0) *g.advance_position += g.advance_by;
 
-    const bool pair = g.epilogue == kRowsSiluPair;
-    auto dot_rows = [&](const float* wrow, float (&acc)[kMaxRows]) {
-        float4 wv[kChunks];
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c) wv[c] = load4(wrow + c * 256 + lane * 4);
+    auto dot_rows = [&](const float4 (&wv)[kChunks], float (&acc)[kMaxRows]) {
 #pragma unroll
         for (int r = 0; r < kMaxRows; ++r) {
             float s = 0.f;
@@ -322,28 +330,23 @@ __global__ __launch_bounds__(64) void rows_gemv_kernel(RowsGemvArgs g) {
             acc[r] = wave_sum(s);
         }
     };
+    float a[kMaxRows], b[kMaxRows] = {0.f, 0.f, 0.f, 0.f};
+    dot_rows(wa, a);
+    if (pair) dot_rows(wb, b);
+    const int r = lane;
+    if (r < g.rows) {
+        float va = a[0], vb = b[0];
 #pragma unroll
-    for (int j = 0; j < kCpw; ++j) {
-        const int ch = blockIdx.x * kCpw + j;
-        if (ch >= g.n) break;
-        float a[kMaxRows], b[kMaxRows];
-        dot_rows(g.w + (size_t)ch * g.k, a);
-        if (pair) dot_rows(g.w + (size_t)(g.n + ch) * g.k, b);
-        const int r = lane;
-        if (r < g.rows) {
-            float va = a[0], vb = b[0];
-#pragma unroll
-            for (int q = 1; q < kMaxRows; ++q)
-                if (r == q) va = a[q], vb = b[q];
-            float v;
-            if (pair) {
-                v = (va / (1.0f + q3_expf(-va))) * vb;  // CS:687-698
-            } else {
-                v = g.bias ? va + g.bias[ch] : va;
-                if (g.epilogue == kRowsScaledResidual) v = g.residual[(size_t)r * g.ldo + ch] + v * g.scale[ch];
-            }
-            g.out[(size_t)r * g.ldo + ch] = v;
+        for (int q = 1; q < kMaxRows; ++q)
+            if (r == q) va = a[q], vb = b[q];
+        float v;
+        if (pair) {
+            v = (va / (1.0f + q3_expf(-va))) * vb;  // CS:687-698
+        } else {
+            v = g.bias ? va + g.bias[ch] : va;
+            if (g.epilogue == kRowsScaledResidual) v = g.residual[(size_t)r * g.ldo + ch] + v * g.scale[ch];
         }
+        g.out[(size_t)r * g.ldo + ch] = v;
     }
 }
 
@@ -373,11 +376,14 @@ __global__ __launch_bounds__(256) void codec_attention_kernel(const float* qkv, 
     const int old_rows = (int)(pos - first);  // window rows before the packet
     float* ring_k = kv_k + (size_t)head * kKvSlots * 64;
     float* ring_v = kv_v + (size_t)head * kKvSlots * 64;
-    for (int idx = tid; idx < old_rows * 64; idx += 256) {
-        const int j = idx >> 6, d = idx & 63;
-        const int slot = (int)((first + (unsigned long long)j) % kKvSlots);
-        k_s[j][d] = ring_k[slot * 64 + d];
-        v_s[j][d] = ring_v[slot * 64 + d];
+    const int first_slot = (int)(first % kKvSlots);
+    for (int idx = tid; idx < old_rows * 16; idx += 256) {  // float4 per thread
+        const int j = idx >> 4, d = (idx & 15) * 4;
+        int slot = first_slot + j;
+        slot -= slot >= kKvSlots ? kKvSlots : 0;
+        const float4 kk = load4(ring_k + slot * 64 + d), vv = load4(ring_v + slot * 64 + d);
+        k_s[j][d] = kk.x, k_s[j][d + 1] = kk.y, k_s[j][d + 2] = kk.z, k_s[j][d + 3] = kk.w;
+        v_s[j][d] = vv.x, v_s[j][d + 1] = vv.y, v_s[j][d + 2] = vv.z, v_s[j][d + 3] = vv.w;
     }
     if (tid < (f + 1) * 32) {  // the packet's frames 0..f, rotate-half pairs (d, d + 32)
         const int g = tid >> 5, d = tid & 31;
@@ -425,18 +431,23 @@ __global__ __launch_bounds__(256) void codec_attention_kernel(const float* qkv, 
     if ((tid & 63) == 0) wmax[tid >> 6] = m;
     __syncthreads();
     const float maximum = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    if (tid < count) p_s[tid] = q3_expf(score - maximum);
+    const float e = tid < count ? q3_expf(score - maximum) : 0.f;
+    if (tid < count) p_s[tid] = e;
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // sequential, in window order
         float denominator = 0.f;
-        for (int j = 0; j < count; ++j) denominator += p_s[j];
+#pragma unroll
+        for (int j = 0; j < kWindow; ++j)
+            if (j < count) denominator += p_s[j];
         denom_s = denominator;
     }
     __syncthreads();
+    if (tid < count) p_s[tid] = e / denom_s;  // the reference's per-term probability
+    __syncthreads();
     if (tid < 64) {
-        const float denominator = denom_s;
         float result = 0.f;
-        for (int j = 0; j < count; ++j) result = fmaf(p_s[j] / denominator, v_s[j][tid], result);
+#pragma unroll 8
+        for (int j = 0; j < count; ++j) result = fmaf(p_s[j], v_s[j][tid], result);
         out[(size_t)f * 1024 + head * 64 + tid] = result;
     }
 }
@@ -541,32 +552,42 @@ __global__ __launch_bounds__(256) void dwconv_layernorm_kernel(const float* ext,
 // Final causal convolution 96 -> 1 (CS:1699-1782 with the im2col column order
 // channel-major, tap-minor), bias, clamp (CS:1126-1131), PCM (CS:1133-1143).
 // ---------------------------------------------------------------------------
-// One wave per 64 positions: the 70 input rows it needs are staged in LDS
-// (rows padded to 97 floats: conflict-free column reads); each lane keeps the
-// sequential channel-major, tap-minor fmaf chain of its position.
-__global__ __launch_bounds__(64) void final_conv_pcm_kernel(const float* ext, int positions, const float* w,
-                                                            const float* b, int16_t* pcm, float* preclamp,
-                                                            float* clamped) {
-    constexpr int kRow = 97;
+// Four lanes per position, each a sequential channel-major, tap-minor fmaf
+// chain over 24 of the 96 channels (float4 reads), then the four partial sums
+// added in channel-group order.
+__global__ __launch_bounds__(256) void final_conv_pcm_kernel(const float* ext, int positions, const float* w,
+                                                             const float* b, int16_t* pcm, float* preclamp,
+                                                             float* clamped) {
     __shared__ float ws[96 * 7];
-    __shared__ float xs[70 * kRow];
-    const int p0 = blockIdx.x * 64;
-    for (int i = threadIdx.x; i < 96 * 7; i += 64) ws[i] = w[i];
-    const int rows = min(70, positions - p0 + 6);
-    for (int i = threadIdx.x; i < rows * 96; i += 64) {
-        const int r = i / 96, c = i - r * 96;
-        xs[r * kRow + c] = ext[(size_t)(p0 + r) * 96 + c];
-    }
+    for (int i = threadIdx.x; i < 96 * 7; i += 256) ws[i] = w[i];
     __syncthreads();
-    const int p = p0 + threadIdx.x;
-    if (p >= positions) return;
-    const float* xp = xs + threadIdx.x * kRow;
-    float acc = 0.f;
-    for (int c = 0; c < 96; ++c) {
+    const int lane = threadIdx.x & 63;
+    const int group = lane >> 4;  // channels 24 * group .. + 23
+    const int p = blockIdx.x * 64 + (threadIdx.x >> 6) * 16 + (lane & 15);
+    const int pc = min(p, positions - 1);
+    float4 x[7][6];
 #pragma unroll
-        for (int t = 0; t < 7; ++t) acc = fmaf(xp[t * kRow + c], ws[c * 7 + t], acc);
+    for (int t = 0; t < 7; ++t)
+#pragma unroll
+        for (int q = 0; q < 6; ++q) x[t][q] = load4(ext + (size_t)(pc + t) * 96 + group * 24 + q * 4);
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = group * 24 + q * 4 + e;
+#pragma unroll
+            for (int t = 0; t < 7; ++t) {
+                const float xv = e == 0 ? x[t][q].x : e == 1 ? x[t][q].y : e == 2 ? x[t][q].z : x[t][q].w;
+                acc = fmaf(xv, ws[c * 7 + t], acc);
+            }
+        }
     }
-    const float v = acc + b[0];
+    // lanes r, r + 16, r + 32, r + 48 hold the four groups of position r
+    const float g1 = __shfl(acc, (lane & 15) + 16, 64), g2 = __shfl(acc, (lane & 15) + 32, 64),
+                g3 = __shfl(acc, (lane & 15) + 48, 64);
+    if (group != 0 || p >= positions) return;
+    const float v = ((acc + g1) + g2) + g3 + b[0];
     if (preclamp) preclamp[p] = v;
     const float c = fminf(1.0f, fmaxf(-1.0f, v));
     if (clamped) clamped[p] = c;
@@ -675,9 +696,9 @@ hipError_t launch_rows_gemv(const RowsGemvArgs& g, hipStream_t stream) {
     // projection of the decoder (n = 512 .. 3072)
     const unsigned blocks = (unsigned)g.n;
     switch (g.k / 256) {
-        case 2: rows_gemv_kernel<2, 1><<<blocks, 64, 0, stream>>>(g); break;
-        case 4: rows_gemv_kernel<4, 1><<<blocks, 64, 0, stream>>>(g); break;
-        case 6: rows_gemv_kernel<6, 1><<<blocks, 64, 0, stream>>>(g); break;
+        case 2: rows_gemv_kernel<2><<<blocks, 64, 0, stream>>>(g); break;
+        case 4: rows_gemv_kernel<4><<<blocks, 64, 0, stream>>>(g); break;
+        case 6: rows_gemv_kernel<6><<<blocks, 64, 0, stream>>>(g); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -718,7 +739,7 @@ hipError_t launch_dwconv_layernorm(const float* ext, int positions, const float*
 
 hipError_t launch_final_conv_pcm(const float* ext, int positions, const float* w, const float* b, int16_t* pcm,
                                  float* preclamp, float* clamped, hipStream_t stream) {
-    final_conv_pcm_kernel<<<(positions + 63) / 64, 64, 0, stream>>>(ext, positions, w, b, pcm, preclamp, clamped);
+    final_conv_pcm_kernel<<<(positions + 63) / 64, 256, 0, stream>>>(ext, positions, w, b, pcm, preclamp, clamped);
     return hipGetLastError();
 }
 
