@@ -69,7 +69,9 @@ struct ConvGemmArgs {
     float* partial;
 };
 
-enum class GemmShape : int { kSmall = 0, kLarge = 1 };  // 16x64 or 64x64 tiles
+// block tiles (rows x columns): 16x64 for 1..16 rows (weight streaming),
+// 32x32, 32x64 and 64x64 for longer sequences
+enum class GemmShape : int { k16x64 = 0, k32x32 = 1, k32x64 = 2, k64x64 = 3 };
 
 struct GemmPlan {
     GemmShape shape;

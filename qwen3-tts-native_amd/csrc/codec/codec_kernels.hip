@@ -645,47 +645,67 @@ __global__ void fill_f32_kernel(float* dst, size_t count, float value) {
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+namespace {
+constexpr int kTileRows[4] = {16, 32, 32, 64};
+constexpr int kTileCols[4] = {64, 32, 64, 64};
+}  // namespace
+
 size_t GemmPlan::partial_floats() const {
     if (splits <= 1) return 0;
-    const size_t tile = shape == GemmShape::kSmall ? 16 * 64 : 64 * 64;
-    return (size_t)splits * tiles() * tile;
+    const int s = (int)shape;
+    return (size_t)splits * tiles() * kTileRows[s] * kTileCols[s];
 }
 
 GemmPlan plan_conv_gemm(int m, int n, int k, int cus) {
+    // Blocks in flight hide the per-step load latency: weight-streaming shapes
+    // (<= 16 rows) take 16x64 tiles and split K to ~2 blocks per CU; longer
+    // sequences take the largest tile that still gives ~2 blocks per CU, then
+    // split K (each slice keeping >= 4 steps of 32) if the tiles alone fall
+    // short.  (Chosen from per-layer measurements on MI355X.)
     GemmPlan plan;
-    plan.shape = m <= 16 ? GemmShape::kSmall : GemmShape::kLarge;
-    const int bm = plan.shape == GemmShape::kSmall ? 16 : 64;
-    plan.tiles_m = (m + bm - 1) / bm;
-    plan.tiles_n = (n + 63) / 64;
-    const long long tiles = (long long)plan.tiles_m * plan.tiles_n;
-    // Weight-streaming shapes (16-row tiles) want ~2 blocks per CU in flight;
-    // MFMA-bound shapes one per CU, and none split once the tiles alone cover
-    // ~90 % of the CUs (the extra partial traffic and reduction cost more).
-    // Each slice keeps at least 4 K-steps.  (Measured on MI355X per layer.)
-    long long splits = 1;
-    if (plan.shape == GemmShape::kSmall) {
-        splits = (2LL * cus + tiles - 1) / tiles;
-    } else if (tiles * 10 < 9LL * cus) {
-        splits = (cus + tiles - 1) / tiles;
+    const long long want = 2LL * cus;
+    auto tiles_for = [&](GemmShape sh) {
+        const int s = (int)sh;
+        return (long long)((m + kTileRows[s] - 1) / kTileRows[s]) * ((n + kTileCols[s] - 1) / kTileCols[s]);
+    };
+    if (m <= 16) {
+        plan.shape = GemmShape::k16x64;
+    } else if (tiles_for(GemmShape::k64x64) >= want) {
+        plan.shape = GemmShape::k64x64;
+    } else if (tiles_for(GemmShape::k32x64) >= want && n % 64 == 0) {
+        plan.shape = GemmShape::k32x64;
+    } else {
+        plan.shape = GemmShape::k32x32;
     }
+    const int s = (int)plan.shape;
+    plan.tiles_m = (m + kTileRows[s] - 1) / kTileRows[s];
+    plan.tiles_n = (n + kTileCols[s] - 1) / kTileCols[s];
+    const long long tiles = (long long)plan.tiles_m * plan.tiles_n;
+    long long splits = tiles < want ? (want + tiles - 1) / tiles : 1;
     splits = std::min<long long>(splits, std::max(1, (k / 32) / 4));
     plan.splits = (int)std::max<long long>(1, splits);
     return plan;
 }
 
+namespace {
+template <int TM, int TN, int WM, int WN>
+void launch_shape(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream) {
+    conv_gemm_kernel<TM, TN, WM, WN><<<dim3(plan.tiles_n, plan.tiles_m, plan.splits), 256, 0, stream>>>(args);
+    if (plan.splits > 1)
+        conv_gemm_reduce_kernel<TM, TN, WM, WN>
+            <<<dim3(plan.tiles_n, plan.tiles_m, 4 * TM * TN), 64, 0, stream>>>(args);
+}
+}  // namespace
+
 hipError_t launch_conv_gemm(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream) {
     if (args.k % 32 || args.channels_in % 32 || args.n % 16 || args.m < 1 || args.splits != plan.splits ||
         (plan.splits > 1 && !args.partial))
         return hipErrorInvalidValue;
-    const dim3 grid(plan.tiles_n, plan.tiles_m, plan.splits);
-    if (plan.shape == GemmShape::kSmall) {
-        conv_gemm_kernel<1, 1, 1, 4><<<grid, 256, 0, stream>>>(args);
-        if (plan.splits > 1)
-            conv_gemm_reduce_kernel<1, 1, 1, 4><<<dim3(plan.tiles_n, plan.tiles_m, 4), 64, 0, stream>>>(args);
-    } else {
-        conv_gemm_kernel<2, 2, 2, 2><<<grid, 256, 0, stream>>>(args);
-        if (plan.splits > 1)
-            conv_gemm_reduce_kernel<2, 2, 2, 2><<<dim3(plan.tiles_n, plan.tiles_m, 16), 64, 0, stream>>>(args);
+    switch (plan.shape) {
+        case GemmShape::k16x64: launch_shape<1, 1, 1, 4>(args, plan, stream); break;
+        case GemmShape::k32x32: launch_shape<1, 1, 2, 2>(args, plan, stream); break;
+        case GemmShape::k32x64: launch_shape<1, 2, 2, 2>(args, plan, stream); break;
+        case GemmShape::k64x64: launch_shape<2, 2, 2, 2>(args, plan, stream); break;
     }
     return hipGetLastError();
 }
