@@ -462,7 +462,7 @@ def codec_weights(seed: int = 0):
     return out
 
 
-def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6):
+def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=(1, 4)):
     """The speech-tokenizer decoder through its C ABI: a continuous stream of
     `packets` packets per size (1 and 4 frames = 80 / 320 ms of audio) on one
     session, each packet's own GPU time and end-to-end latency (median); then
@@ -477,7 +477,7 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6):
     rng = np.random.default_rng(5)
     out = {"weights": "synthetic fp32, real geometry (114,323,137 parameters)"}
     try:
-        for frames in (1, 4):
+        for frames in sizes:
             s = model.session()
             gpu, e2e = [], []
             for i in range(warm + packets):
@@ -501,8 +501,8 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6):
                 "weight_gbs": round(4 * 114_323_137 / (g * 1e-6) / 1e9, 1),
                 "vs_reference_gb10_p50": round((11_651.3 if frames == 1 else 62_086.3) / e, 1)}
         sessions = [model.session() for _ in range(streams)]
-        t0, audio = None, 0.0
-        for i in range(warm + packets // 2):
+        t0, audio = time.perf_counter(), 0.0
+        for i in range(warm + packets // 2 if streams else 0):
             if i == warm:
                 t0 = time.perf_counter()
             codes = [rng.integers(0, 2048, (4, 16), dtype=np.uint16) for _ in range(streams)]
@@ -510,8 +510,9 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6):
             if i >= warm:
                 audio += streams * 0.32
         wall = time.perf_counter() - t0
-        out[f"batch{streams}_4frame"] = {"audio_seconds_per_second": round(audio / wall, 1),
-                                         "aggregate_rtf": round(wall / audio, 5)}
+        if streams:
+            out[f"batch{streams}_4frame"] = {"audio_seconds_per_second": round(audio / wall, 1),
+                                             "aggregate_rtf": round(wall / audio, 5)}
         for s in sessions:
             s.close()
     finally:
@@ -539,6 +540,9 @@ def main() -> int:
     ap.add_argument("--only-codec", action="store_true",
                     help="run only the speech-tokenizer decoder benchmark (packets of 1 and 4 frames, 6 batched "
                          "streams); for rocprofv3 kernel statistics")
+    ap.add_argument("--codec-frames", type=int, default=0,
+                    help="with --only-codec: one packet size only (1..4) and no batched streams (a clean "
+                         "per-layer kernel trace)")
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
@@ -566,7 +570,11 @@ def main() -> int:
         print(json.dumps({"prefill": prefill_benchmark(hip)}), flush=True)
         return 0
     if args.only_codec:
-        print(json.dumps({"codec": codec_benchmark()}), flush=True)
+        if args.codec_frames:
+            out = codec_benchmark(packets=50, warm=5, streams=0, sizes=(args.codec_frames,))
+        else:
+            out = codec_benchmark()
+        print(json.dumps({"codec": out}), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)

@@ -13,11 +13,6 @@
  * As in the reference, this header and qwen3_tts_native.h both name
  * QWEN3_TTS_CODEC_CODEBOOKS (a macro there, an enumerator here): a translation
  * unit includes one of them.
- *
- * Not provided: qwen3_tts_codec_process_fixture_packet_v1, the reference's
- * deterministic state-machine fixture that executes no neural weights
- * (C:338-351); it is a test double of the reference's own harness, not part of
- * the decoding path.
  */
 #ifndef QWEN3_TTS_CODEC_H
 #define QWEN3_TTS_CODEC_H
@@ -282,6 +277,18 @@ QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_packet_v1(Qwen3TtsCodecConte
                                                               size_t error_capacity);
 QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_batch_v1(Qwen3TtsCodecBatchItemV1* items, uint32_t item_count,
                                                              char* error, size_t error_capacity);
+
+/* C:337-351: the deterministic state-machine fixture.  It executes no neural
+ * weights (integer stand-ins for each stage, carried across packets) and is no
+ * model-quality or latency measurement; the reference's Rust loader requires
+ * the symbol. */
+QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_fixture_packet_v1(Qwen3TtsCodecContextV1* context,
+                                                                      const uint16_t* codec_frames,
+                                                                      uint32_t frame_count, int32_t is_final,
+                                                                      int16_t* pcm_output,
+                                                                      size_t pcm_capacity_samples,
+                                                                      Qwen3TtsCodecPacketResultV1* result,
+                                                                      char* error, size_t error_capacity);
 
 /* Shared-model API (C:353-392). */
 QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_shared_model_create_v1(int32_t device_index,

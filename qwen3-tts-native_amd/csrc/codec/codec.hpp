@@ -136,6 +136,9 @@ hipError_t launch_dwconv_layernorm(const float* ext, int positions, const float*
 hipError_t launch_final_conv_pcm(const float* ext, int positions, const float* w, const float* b, int16_t* pcm,
                                  float* preclamp, float* clamped, hipStream_t stream);
 
+// ---- the reference's weight-free state-machine fixture (22 ints of state) -----
+hipError_t launch_fixture_packet(const uint16_t* codes, int frames, int* state, int16_t* pcm, hipStream_t stream);
+
 // ---- load-time helpers ----------------------------------------------------------
 hipError_t launch_bf16_to_f32(const uint16_t* src, size_t count, float* dst, hipStream_t stream);
 // [o][c][taps] -> [o][taps][c]

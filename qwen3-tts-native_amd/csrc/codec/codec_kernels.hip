@@ -596,6 +596,59 @@ __global__ __launch_bounds__(256) void final_conv_pcm_kernel(const float* ext, i
 }
 
 // ---------------------------------------------------------------------------
+// Deterministic state-machine fixture (CS:185-318, 4518-4740): integer
+// stand-ins for the pre-convolution (3x + 2 h1 - h2) / 4 over the weighted code
+// sum, two repeats, four transposed-convolution overlaps (3x + previous) / 4
+// with carried tails, and x * 8 saturated to 16 bits.  One block; the stages
+// alternate between two LDS buffers.  state: [0..1] pre-conv history,
+// [2..21] the tails of strides 8, 5, 4, 3.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fixture_packet_kernel(const uint16_t* codes, int frames, int* state,
+                                                             int16_t* pcm) {
+    __shared__ int buf[2][kMaxFrames * kSamplesPerFrame];
+    __shared__ int tails[20];
+    const int tid = threadIdx.x;
+    if (tid < 20) tails[tid] = state[2 + tid];
+    if (tid == 0) {
+        int h1 = state[0], h2 = state[1];
+        for (int f = 0; f < frames; ++f) {
+            int sum = 0;
+            for (int cb = 0; cb < kCodebooks; ++cb) sum += (codes[f * kCodebooks + cb] & 2047) * (cb + 1);
+            const int centered = (sum & 4095) - 2048;
+            const int filtered = (3 * centered + 2 * h1 - h2) / 4;
+            h2 = h1;
+            h1 = centered;
+            for (int r = 0; r < 4; ++r) buf[0][4 * f + r] = filtered;  // repeat x2, x2
+        }
+        state[0] = h1;
+        state[1] = h2;
+    }
+    __syncthreads();
+    int n = 4 * frames, src = 0, tail_base = 0;
+    for (int stage = 0; stage < 4; ++stage) {
+        const int stride = kStride[stage];
+        const int* in = buf[src];
+        int* out = buf[src ^ 1];
+        for (int i = tid; i < n * stride; i += 256) {
+            const int ip = i / stride, phase = i - ip * stride;
+            const int previous = ip == 0 ? tails[tail_base + phase] : in[ip - 1];
+            out[i] = (3 * in[ip] + previous) / 4;
+        }
+        __syncthreads();
+        if (tid < stride) tails[tail_base + tid] = in[n - 1];
+        __syncthreads();
+        tail_base += stride;
+        n *= stride;
+        src ^= 1;
+    }
+    for (int i = tid; i < n; i += 256) {
+        const int v = buf[src][i] * 8;
+        pcm[i] = (int16_t)(v > 32767 ? 32767 : (v < -32768 ? -32768 : v));
+    }
+    if (tid < 20) state[2 + tid] = tails[tid];
+}
+
+// ---------------------------------------------------------------------------
 // load-time kernels
 // ---------------------------------------------------------------------------
 __global__ void bf16_to_f32_kernel(const uint16_t* src, size_t count, float* dst) {
@@ -760,6 +813,12 @@ hipError_t launch_dwconv_layernorm(const float* ext, int positions, const float*
 hipError_t launch_final_conv_pcm(const float* ext, int positions, const float* w, const float* b, int16_t* pcm,
                                  float* preclamp, float* clamped, hipStream_t stream) {
     final_conv_pcm_kernel<<<(positions + 63) / 64, 256, 0, stream>>>(ext, positions, w, b, pcm, preclamp, clamped);
+    return hipGetLastError();
+}
+
+hipError_t launch_fixture_packet(const uint16_t* codes, int frames, int* state, int16_t* pcm, hipStream_t stream) {
+    if (frames < 1 || frames > kMaxFrames) return hipErrorInvalidValue;
+    fixture_packet_kernel<<<1, 256, 0, stream>>>(codes, frames, state, pcm);
     return hipGetLastError();
 }
 

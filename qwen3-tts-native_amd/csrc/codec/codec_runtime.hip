@@ -252,7 +252,7 @@ struct Qwen3TtsCodecContextV1 {
 
     // host-side stream state (CS:1240-1290)
     uint64_t frame_position = 0, emitted_samples = 0, neural_frame_position = 0;
-    uint32_t next_ring_slot = 0;
+    uint32_t next_ring_slot = 0, kv_ring_head = 0;
     bool finalized = false, cancelled = false, device_packet_pending = false;
     uint64_t next_ticket = 1, pending_ticket = 0;
     uint32_t pending_frames = 0, pending_slot = 0;
@@ -267,6 +267,7 @@ struct Qwen3TtsCodecContextV1 {
     int16_t* pcm_ring = nullptr;
     int16_t* pcm_dev = nullptr;
     unsigned long long* position = nullptr;
+    int* fixture_state = nullptr;
     float *x_rvq = nullptr, *t_in = nullptr, *h = nullptr, *h2 = nullptr, *qkv = nullptr, *attn = nullptr,
           *act = nullptr, *t_out = nullptr;
     float *kv_k = nullptr, *kv_v = nullptr;
@@ -306,6 +307,7 @@ void layout_session(Qwen3TtsCodecContextV1* s, Arena& a) {
     s->pcm_ring = a.take<int16_t>((size_t)kRingSlots * kMaxSamples);
     s->pcm_dev = a.take<int16_t>(kMaxSamples);
     s->position = a.take<unsigned long long>(1);
+    s->fixture_state = a.take<int>(22);
     const size_t kv_start = a.used;
     s->kv_k = a.take<float>((size_t)kLayers * kHeads * kKvSlots * kHeadDim);
     s->kv_v = a.take<float>((size_t)kLayers * kHeads * kKvSlots * kHeadDim);
@@ -427,6 +429,7 @@ hipError_t reset_device_state(Qwen3TtsCodecContextV1* s) {
     }
     if (st == hipSuccess)
         st = hipMemsetAsync(s->position, 0, sizeof(unsigned long long), s->stream);
+    if (st == hipSuccess) st = hipMemsetAsync(s->fixture_state, 0, 22 * sizeof(int), s->stream);
     if (st == hipSuccess) st = hipStreamSynchronize(s->stream);
     return st;
 }
@@ -788,6 +791,7 @@ int32_t finish_staged_packet(Qwen3TtsCodecContextV1* s, uint32_t slot, uint32_t 
     s->frame_position += frames;
     s->emitted_samples += samples;
     s->neural_frame_position += frames;
+    s->kv_ring_head = (uint32_t)(s->neural_frame_position % kWindow);
     s->next_ring_slot = (s->next_ring_slot + 1) % kRingSlots;
     s->finalized = is_final != 0;
     const float e2e = std::chrono::duration<float, std::micro>(std::chrono::steady_clock::now() - start).count();
@@ -932,7 +936,7 @@ int32_t reset_context(Qwen3TtsCodecContextV1* s, char* error, size_t capacity) {
     if (st == hipSuccess) st = reset_device_state(s);
     if (st != hipSuccess) return hip_error(error, capacity, "reset decoder state", st);
     s->frame_position = s->emitted_samples = s->neural_frame_position = 0;
-    s->next_ring_slot = 0;
+    s->next_ring_slot = s->kv_ring_head = 0;
     s->finalized = s->cancelled = s->device_packet_pending = false;
     s->pending_ticket = 0;
     s->pending_frames = s->pending_slot = 0;
@@ -966,7 +970,10 @@ int32_t run_debug_prefix(Qwen3TtsCodecContextV1* s, const uint16_t* codes, uint3
     st = l.st;
     if (st == hipSuccess) st = hipStreamSynchronize(s->stream);
     if (st != hipSuccess) return hip_error(error, capacity, "run decoder stages", st);
-    if (stop >= 2) s->neural_frame_position += frames;
+    if (stop >= 2) {
+        s->neural_frame_position += frames;
+        s->kv_ring_head = (uint32_t)(s->neural_frame_position % kWindow);
+    }
     return kOk;
 }
 
@@ -1043,7 +1050,7 @@ QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_state_info_v1(const Qwen3TtsCodecCon
         context->history_bytes,
         (uint64_t)kRingSlots * kMaxFrames * kCodebooks * sizeof(uint16_t),
         pcm_ring,
-        (uint32_t)(context->neural_frame_position % kWindow),
+        context->kv_ring_head,
         context->next_ring_slot,
         (uint32_t)kRingSlots,
         (uint32_t)kMaxFrames,
@@ -1399,6 +1406,65 @@ QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_batch_v1(Qwen3TtsCodecBatchI
         if (status == kOk && r != kOk) status = r;
     }
     return status;
+}
+
+QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_fixture_packet_v1(Qwen3TtsCodecContextV1* context,
+                                                                      const uint16_t* codec_frames,
+                                                                      uint32_t frame_count, int32_t is_final,
+                                                                      int16_t* pcm_output,
+                                                                      size_t pcm_capacity_samples,
+                                                                      Qwen3TtsCodecPacketResultV1* result,
+                                                                      char* error, size_t error_capacity) {
+    clear_error(error, error_capacity);
+    if (!context || !codec_frames || !pcm_output || !result) {
+        write_error(error, error_capacity, "context, codec frames, PCM output, and result are required");
+        return kInvalid;
+    }
+    if (frame_count == 0 || frame_count > QWEN3_TTS_CODEC_MAX_PACKET_FRAMES || (is_final != 0 && is_final != 1)) {
+        write_error(error, error_capacity, "packet must contain 1-4 frames");
+        return kInvalid;
+    }
+    const size_t samples = (size_t)frame_count * kSamplesPerFrame;
+    if (pcm_capacity_samples < samples) {
+        write_error(error, error_capacity, "PCM output capacity is too small");
+        return kInvalid;
+    }
+    if (context->finalized || context->device_packet_pending) {
+        write_error(error, error_capacity, "stream is finalized; reset is required");
+        return kState;
+    }
+    hipError_t st = hipSetDevice(context->device);
+    if (st != hipSuccess) return hip_error(error, error_capacity, "select HIP device", st);
+    const auto start = std::chrono::steady_clock::now();
+    const uint32_t slot = context->next_ring_slot;
+    uint16_t* codes = context->code_ring + (size_t)slot * kMaxFrames * kCodebooks;
+    int16_t* dev_pcm = context->pcm_ring + (size_t)slot * kMaxSamples;
+    int16_t* host_pcm = context->host_pcm + (size_t)slot * kMaxSamples;
+    st = hipEventRecord(context->start_event, context->stream);
+    if (st == hipSuccess)
+        st = hipMemcpyAsync(codes, codec_frames, (size_t)frame_count * kCodebooks * sizeof(uint16_t),
+                            hipMemcpyHostToDevice, context->stream);
+    if (st != hipSuccess) return hip_error(error, error_capacity, "queue codec copy", st);
+    st = launch_fixture_packet(codes, (int)frame_count, context->fixture_state, dev_pcm, context->stream);
+    if (st != hipSuccess) return hip_error(error, error_capacity, "launch fixture packet", st);
+    st = hipMemcpyAsync(host_pcm, dev_pcm, samples * sizeof(int16_t), hipMemcpyDeviceToHost, context->stream);
+    if (st == hipSuccess) st = hipEventRecord(context->stop_event, context->stream);
+    if (st == hipSuccess) st = hipEventSynchronize(context->stop_event);
+    if (st != hipSuccess) return hip_error(error, error_capacity, "complete fixture packet", st);
+    float ms = 0.f;
+    st = hipEventElapsedTime(&ms, context->start_event, context->stop_event);
+    if (st != hipSuccess) return hip_error(error, error_capacity, "measure packet GPU time", st);
+    std::memcpy(pcm_output, host_pcm, samples * sizeof(int16_t));
+    const uint64_t first_frame = context->frame_position, first_sample = context->emitted_samples;
+    context->frame_position += frame_count;
+    context->emitted_samples += samples;
+    context->kv_ring_head = (uint32_t)(context->frame_position % kWindow);
+    context->next_ring_slot = (context->next_ring_slot + 1) % kRingSlots;
+    context->finalized = is_final != 0;
+    const float e2e = std::chrono::duration<float, std::micro>(std::chrono::steady_clock::now() - start).count();
+    *result = Qwen3TtsCodecPacketResultV1{first_frame, first_sample, frame_count, (uint32_t)samples,
+                                          slot,        (uint32_t)is_final, ms * 1000.f, e2e};
+    return kOk;
 }
 
 QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_shared_model_create_v1(int32_t device_index,

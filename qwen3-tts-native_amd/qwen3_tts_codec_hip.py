@@ -204,6 +204,8 @@ SIGNATURES = {
     "qwen3_tts_codec_debug_decoder_checkpoint_v1": (_I32, [_P, _P, _U32, _U32, _P, C.c_size_t] + _E),
     "qwen3_tts_codec_process_packet_v1": (_I32, [_P, _P, _U32, _I32, _P, C.c_size_t, C.POINTER(PacketResult)] + _E),
     "qwen3_tts_codec_process_batch_v1": (_I32, [C.POINTER(BatchItem), _U32] + _E),
+    "qwen3_tts_codec_process_fixture_packet_v1": (
+        _I32, [_P, _P, _U32, _I32, _P, C.c_size_t, C.POINTER(PacketResult)] + _E),
     "qwen3_tts_codec_shared_model_create_v1": (_I32, [_I32, C.POINTER(_P)] + _E),
     "qwen3_tts_codec_shared_model_destroy_v1": (_I32, [_P] + _E),
     "qwen3_tts_codec_shared_model_load_v1": (_I32, [_P, C.POINTER(WeightProvider), C.POINTER(ModelInfo)] + _E),
@@ -338,6 +340,15 @@ class Session:
         pcm = np.zeros(MAX_PACKET_SAMPLES, np.int16)
         res = PacketResult()
         call("qwen3_tts_codec_session_process_packet_v1", self.handle, _ptr(codes), codes.shape[0],
+             1 if is_final else 0, _ptr(pcm), pcm.size, C.byref(res))
+        return pcm[: res.sample_count].copy(), res
+
+    def fixture_packet(self, codes, is_final: bool = False):
+        """The reference's weight-free state-machine fixture packet."""
+        codes = np.ascontiguousarray(np.atleast_2d(codes), np.uint16)
+        pcm = np.zeros(MAX_PACKET_SAMPLES, np.int16)
+        res = PacketResult()
+        call("qwen3_tts_codec_process_fixture_packet_v1", self.handle, _ptr(codes), codes.shape[0],
              1 if is_final else 0, _ptr(pcm), pcm.size, C.byref(res))
         return pcm[: res.sample_count].copy(), res
 

@@ -23,7 +23,7 @@ def declared_symbols():
 def test_every_declared_symbol_is_exported():
     lib = codec.load()
     names = declared_symbols()
-    assert len(names) == 31
+    assert len(names) == 32
     assert not [n for n in names if not hasattr(lib, n)]
     assert set(names) == set(codec.SIGNATURES)
     assert lib.qwen3_tts_codec_abi_version_v1() == 1
@@ -31,13 +31,12 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_reference_symbols_are_declared():
-    """Every decoder entry point of the reference header is declared, except
-    its weight-free state-machine fixture (a harness test double)."""
+    """Every decoder entry point of the reference header is declared."""
     ref = pathlib.Path("/root/reference/native/qwen3-tts-native-codec/native/include/qwen3_tts_codec.h")
     if not ref.exists():
         pytest.skip("reference tree not present")
     text = re.sub(r"/\*.*?\*/", "", ref.read_text(), flags=re.S)
-    theirs = set(re.findall(r"\b(qwen3_tts_codec_\w+)\s*\(", text)) - {"qwen3_tts_codec_process_fixture_packet_v1"}
+    theirs = set(re.findall(r"\b(qwen3_tts_codec_\w+)\s*\(", text))
     assert theirs == set(declared_symbols())
 
 

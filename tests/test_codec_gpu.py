@@ -298,3 +298,35 @@ def test_legacy_context_api(codec, weights, codes):
     codec.call("qwen3_tts_codec_warmup_v1", s.handle)
     pcm, res = s.packet(codes[:4])
     assert res.sample_count == 7680 and res.first_frame_position == 0
+
+
+def test_fixture_packets_match_reference_model(codec):
+    """The weight-free fixture: 83 deterministic frames in the reference's
+    1/4/2/3/4/1/3/2 packets equal its CPU model decoding them at once; after
+    the final packet another is rejected; a reset restarts the stream
+    (the reference's fixture parity record: 34 packets, 159,360 samples,
+    max error 0, benchmarks/results/codec-incremental-fixture-parity.json)."""
+    import codec_fixture as FX
+
+    print("codec fixture", flush=True)
+    frames = FX.deterministic_frames(83)
+    want = FX.FixtureState().process(frames)
+    s = codec.Session(None)  # a context; the fixture needs no weights
+    got, positions = [], []
+    plan = FX.packets(83)
+    for i, (a, b) in enumerate(plan):
+        pcm, res = s.fixture_packet(frames[a:b], is_final=i == len(plan) - 1)
+        got.append(pcm)
+        positions.append((res.first_frame_position, res.first_sample_position, res.ring_slot))
+    got = np.concatenate(got)
+    assert len(plan) == 34 and got.size == 159_360
+    np.testing.assert_array_equal(got, want)
+    assert positions[5] == (plan[5][0], plan[5][0] * 1920, 5 % 3)
+    st = s.state()
+    assert st.frame_position == 83 and st.emitted_samples == 159_360 and st.kv_ring_head == 83 % 72
+    with pytest.raises(codec.CodecError) as e:
+        s.fixture_packet(frames[:1])
+    assert e.value.status == -3
+    s.reset()
+    again, _ = s.fixture_packet(frames[:1])
+    np.testing.assert_array_equal(again, want[:1920])

@@ -127,3 +127,18 @@ def test_stopped_packet_matches_prefix(weights, codes, streamed):
     assert out["pcm"].size == 0
     np.testing.assert_array_equal(out["rvq"], streamed["rvq"][:4])
     np.testing.assert_array_equal(out["preconv"], streamed["preconv"][:4])
+
+
+def test_fixture_restatement_is_packet_invariant():
+    """The fixture model decodes 83 frames identically in one call and in the
+    reference's 1/4/2/3/4/1/3/2 packets (its own parity design), and its
+    sample count is 1920 per frame."""
+    import codec_fixture as FX
+
+    frames = FX.deterministic_frames(83)
+    whole = FX.FixtureState().process(frames)
+    st = FX.FixtureState()
+    parts = np.concatenate([st.process(frames[a:b]) for a, b in FX.packets(83)])
+    assert whole.size == 83 * 1920
+    np.testing.assert_array_equal(parts, whole)
+    assert np.abs(whole).max() > 1000 and len(FX.packets(83)) == 34
