@@ -434,6 +434,28 @@ def batched_frames(hip, ns=(2, 4, 8), frames: int = 30, warm: int = 2, max_seq: 
         lib.qwen3_tts_model_destroy(model)
 
 
+def codec_cpu_baseline(weights, packets: int = 2):
+    """The CPU oracle of the decoder (oracle/codec_oracle.c) decoding
+    `packets` 4-frame packets of one stream on every core of this process's
+    affinity set (bounded sample: a few seconds)."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    orc = oracle.CodecOracle(weights)
+    rng = np.random.default_rng(7)
+    t0 = time.perf_counter()
+    for _ in range(packets):
+        orc.packet(rng.integers(0, 2048, (4, 16), dtype=np.uint16), trace=False)
+    dt = (time.perf_counter() - t0) / packets
+    return {"value": round(dt * 1e3, 1), "unit": "ms per 4-frame packet", "rtf": round(dt / 0.32, 3),
+            "cores": threads, "kind": "port",
+            "sample": f"{packets} packets of 4 frames, one stream, the oracle's fp32 decoder on {threads} threads"}
+
+
 FP32_MFMA_PEAK_TFLOPS = 157.3
 
 
@@ -462,7 +484,7 @@ def codec_weights(seed: int = 0):
     return out
 
 
-def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=(1, 4)):
+def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=(1, 4), cpu: bool = True):
     """The speech-tokenizer decoder through its C ABI: a continuous stream of
     `packets` packets per size (1 and 4 frames = 80 / 320 ms of audio) on one
     session, each packet's own GPU time and end-to-end latency (median); then
@@ -473,7 +495,8 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=
     import numpy as np
     import qwen3_tts_codec_hip as codec
 
-    model = codec.SharedModel(codec_weights())
+    weights = codec_weights()
+    model = codec.SharedModel(weights)
     rng = np.random.default_rng(5)
     out = {"weights": "synthetic fp32, real geometry (114,323,137 parameters)"}
     try:
@@ -517,6 +540,8 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=
             s.close()
     finally:
         model.close()
+    if cpu:
+        out["cpu_baseline"] = codec_cpu_baseline(weights)
     return out
 
 
@@ -571,7 +596,7 @@ def main() -> int:
         return 0
     if args.only_codec:
         if args.codec_frames:
-            out = codec_benchmark(packets=50, warm=5, streams=0, sizes=(args.codec_frames,))
+            out = codec_benchmark(packets=50, warm=5, streams=0, sizes=(args.codec_frames,), cpu=False)
         else:
             out = codec_benchmark()
         print(json.dumps({"codec": out}), flush=True)
@@ -650,7 +675,7 @@ def main() -> int:
         except Exception as e:  # report, never hide
             line["batched_frames"] = {"error": str(e)}
         try:
-            line["codec"] = codec_benchmark()
+            line["codec"] = codec_benchmark(cpu=not args.no_cpu)
         except Exception as e:  # report, never hide
             line["codec"] = {"error": str(e)}
     if not args.no_cpu:

@@ -76,10 +76,11 @@ enum class GemmShape : int { k16x64 = 0, k32x32 = 1, k32x64 = 2, k64x64 = 3 };
 struct GemmPlan {
     GemmShape shape;
     int tiles_m, tiles_n, splits;
+    int k_step;  // 32 or 64 floats of K per pipeline step
     size_t partial_floats() const;
     size_t tiles() const { return (size_t)tiles_m * tiles_n; }
 };
-GemmPlan plan_conv_gemm(int m, int n, int k, int cus);
+GemmPlan plan_conv_gemm(int m, int n, int k, int channels_in, int cus);
 hipError_t launch_conv_gemm(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream);
 
 // ---- rows GEMV (1..4 rows) -------------------------------------------------

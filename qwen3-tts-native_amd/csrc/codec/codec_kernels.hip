@@ -110,45 +110,46 @@ __device__ __forceinline__ void tile_epilogue(const ConvGemmArgs& g, const float
         for (int i = 0; i < TM; ++i) subtile_epilogue<TM, TN, WM, WN>(g, acc[i][j], tile_m, tile_n, wave, i, j, lane);
 }
 
-constexpr int kLdsRow = 36;
-
-template <int TM, int TN, int WM, int WN>
+template <int TM, int TN, int WM, int WN, int BK>
 __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvGemmArgs g) {
     static_assert(WM * WN == 4, "4 waves");
+    static_assert(BK == 32 || BK == 64, "K step");
     constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
-    constexpr int A_VEC = BM * 8, W_VEC = BN * 8;  // float4 per step
+    constexpr int VPR = BK / 4;      // float4 per row per step
+    constexpr int ROW = BK + 4;      // LDS row pitch (floats)
+    constexpr int A_VEC = BM * VPR, W_VEC = BN * VPR;
     constexpr int A_PER = (A_VEC + 255) / 256, W_PER = (W_VEC + 255) / 256;
     // every thread copies A_PER + W_PER vectors; rows past the tile (small
     // tiles) are loaded from clamped addresses into spare LDS rows, unused
-    __shared__ float lds_a[2][A_PER * 32 * kLdsRow];
-    __shared__ float lds_w[2][W_PER * 32 * kLdsRow];
+    __shared__ float lds_a[2][A_PER * (256 / VPR) * ROW];
+    __shared__ float lds_w[2][W_PER * (256 / VPR) * ROW];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int row16 = lane & 15, group = lane >> 4;
 
-    // global -> LDS copy assignment: vector v = tid + 256 * r covers row v / 8, float4 v % 8
+    // global -> LDS copy assignment: vector v = tid + 256 * r covers row v / VPR, float4 v % VPR
     const float* a_src[A_PER];
     const float* w_src[W_PER];
 #pragma unroll
     for (int r = 0; r < A_PER; ++r) {
         const int v = tid + 256 * r;
-        const int p = min((int)(blockIdx.y * BM) + v / 8, g.m - 1);
-        a_src[r] = g.a + (size_t)p * g.channels_in + (v % 8) * 4;
+        const int p = min((int)(blockIdx.y * BM) + v / VPR, g.m - 1);
+        a_src[r] = g.a + (size_t)p * g.channels_in + (v % VPR) * 4;
     }
 #pragma unroll
     for (int r = 0; r < W_PER; ++r) {
         const int v = tid + 256 * r;
-        const int col = min((int)(blockIdx.x * BN) + v / 8, g.n - 1);
-        w_src[r] = g.w + (size_t)col * g.k + (v % 8) * 4;
+        const int col = min((int)(blockIdx.x * BN) + v / VPR, g.n - 1);
+        w_src[r] = g.w + (size_t)col * g.k + (v % VPR) * 4;
     }
 
-    const int steps = g.k >> 5;
+    const int steps = g.k / BK;
     const int s0 = (int)((long long)steps * blockIdx.z / g.splits);
     const int s1 = (int)((long long)steps * (blockIdx.z + 1) / g.splits);
-    // (tap, channel) of the next step to load (channels_in % 32 == 0)
-    int tap = (s0 * 32) / g.channels_in;
-    int chan = s0 * 32 - tap * g.channels_in;
+    // (tap, channel) of the next step to load (channels_in % BK == 0)
+    int tap = (s0 * BK) / g.channels_in;
+    int chan = s0 * BK - tap * g.channels_in;
     int s_load = s0;
     const size_t tap_stride = (size_t)g.dilation * g.channels_in;
 
@@ -161,13 +162,13 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvGemmArgs g) {
     float4 a_reg[A_PER], w_reg[W_PER];
     auto fetch = [&]() {
         const size_t a_off = (size_t)tap * tap_stride + chan;
-        const size_t w_off = (size_t)s_load * 32;
+        const size_t w_off = (size_t)s_load * BK;
 #pragma unroll
         for (int r = 0; r < A_PER; ++r) a_reg[r] = load4(a_src[r] + a_off);
 #pragma unroll
         for (int r = 0; r < W_PER; ++r) w_reg[r] = load4(w_src[r] + w_off);
         ++s_load;
-        chan += 32;
+        chan += BK;
         if (chan == g.channels_in) {
             chan = 0;
             ++tap;
@@ -177,39 +178,42 @@ __global__ __launch_bounds__(256) void conv_gemm_kernel(ConvGemmArgs g) {
 #pragma unroll
         for (int r = 0; r < A_PER; ++r) {
             const int v = tid + 256 * r;
-            *reinterpret_cast<float4*>(&lds_a[buf][(v / 8) * kLdsRow + (v % 8) * 4]) = a_reg[r];
+            *reinterpret_cast<float4*>(&lds_a[buf][(v / VPR) * ROW + (v % VPR) * 4]) = a_reg[r];
         }
 #pragma unroll
         for (int r = 0; r < W_PER; ++r) {
             const int v = tid + 256 * r;
-            *reinterpret_cast<float4*>(&lds_w[buf][(v / 8) * kLdsRow + (v % 8) * 4]) = w_reg[r];
+            *reinterpret_cast<float4*>(&lds_w[buf][(v / VPR) * ROW + (v % VPR) * 4]) = w_reg[r];
         }
     };
     auto compute = [&](int buf) {
-        float4 av[TM][2], wv[TN][2];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const float* src = &lds_a[buf][((wm * TM + i) * 16 + row16) * kLdsRow + 8 * group];
-            av[i][0] = *reinterpret_cast<const float4*>(src);
-            av[i][1] = *reinterpret_cast<const float4*>(src + 4);
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const float* src = &lds_w[buf][((wn * TN + j) * 16 + row16) * kLdsRow + 8 * group];
-            wv[j][0] = *reinterpret_cast<const float4*>(src);
-            wv[j][1] = *reinterpret_cast<const float4*>(src + 4);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int kh = 0; kh < BK / 32; ++kh) {
+            float4 av[TM][2], wv[TN][2];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const float4& a4 = av[i][e >> 2];
-                const float x = (e & 3) == 0 ? a4.x : (e & 3) == 1 ? a4.y : (e & 3) == 2 ? a4.z : a4.w;
+                const float* src = &lds_a[buf][((wm * TM + i) * 16 + row16) * ROW + kh * 32 + 8 * group];
+                av[i][0] = *reinterpret_cast<const float4*>(src);
+                av[i][1] = *reinterpret_cast<const float4*>(src + 4);
+            }
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const float4& w4 = wv[j][e >> 2];
-                    const float y = (e & 3) == 0 ? w4.x : (e & 3) == 1 ? w4.y : (e & 3) == 2 ? w4.z : w4.w;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[i][j], 0, 0, 0);
+            for (int j = 0; j < TN; ++j) {
+                const float* src = &lds_w[buf][((wn * TN + j) * 16 + row16) * ROW + kh * 32 + 8 * group];
+                wv[j][0] = *reinterpret_cast<const float4*>(src);
+                wv[j][1] = *reinterpret_cast<const float4*>(src + 4);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const float4& a4 = av[i][e >> 2];
+                    const float x = (e & 3) == 0 ? a4.x : (e & 3) == 1 ? a4.y : (e & 3) == 2 ? a4.z : a4.w;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const float4& w4 = wv[j][e >> 2];
+                        const float y = (e & 3) == 0 ? w4.x : (e & 3) == 1 ? w4.y : (e & 3) == 2 ? w4.z : w4.w;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[i][j], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -709,13 +713,15 @@ size_t GemmPlan::partial_floats() const {
     return (size_t)splits * tiles() * kTileRows[s] * kTileCols[s];
 }
 
-GemmPlan plan_conv_gemm(int m, int n, int k, int cus) {
+GemmPlan plan_conv_gemm(int m, int n, int k, int channels_in, int cus) {
     // Blocks in flight hide the per-step load latency: weight-streaming shapes
     // (<= 16 rows) take 16x64 tiles and split K to ~2 blocks per CU; longer
     // sequences take the largest tile that still gives ~2 blocks per CU, then
     // split K (each slice keeping >= 4 steps of 32) if the tiles alone fall
     // short.  (Chosen from per-layer measurements on MI355X.)
     GemmPlan plan;
+    // 64-float K steps (half the barriers) wherever the channels allow
+    plan.k_step = channels_in % 64 == 0 ? 64 : 32;
     const long long want = 2LL * cus;
     auto tiles_for = [&](GemmShape sh) {
         const int s = (int)sh;
@@ -735,7 +741,7 @@ GemmPlan plan_conv_gemm(int m, int n, int k, int cus) {
     plan.tiles_n = (n + kTileCols[s] - 1) / kTileCols[s];
     const long long tiles = (long long)plan.tiles_m * plan.tiles_n;
     long long splits = tiles < want ? (want + tiles - 1) / tiles : 1;
-    splits = std::min<long long>(splits, std::max(1, (k / 32) / 4));
+    splits = std::min<long long>(splits, std::max(1, (k / plan.k_step) / 4));
     plan.splits = (int)std::max<long long>(1, splits);
     return plan;
 }
@@ -743,7 +749,12 @@ GemmPlan plan_conv_gemm(int m, int n, int k, int cus) {
 namespace {
 template <int TM, int TN, int WM, int WN>
 void launch_shape(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream) {
-    conv_gemm_kernel<TM, TN, WM, WN><<<dim3(plan.tiles_n, plan.tiles_m, plan.splits), 256, 0, stream>>>(args);
+    const dim3 grid(plan.tiles_n, plan.tiles_m, plan.splits);
+    if (plan.k_step == 64) {
+        conv_gemm_kernel<TM, TN, WM, WN, 64><<<grid, 256, 0, stream>>>(args);
+    } else {
+        conv_gemm_kernel<TM, TN, WM, WN, 32><<<grid, 256, 0, stream>>>(args);
+    }
     if (plan.splits > 1)
         conv_gemm_reduce_kernel<TM, TN, WM, WN>
             <<<dim3(plan.tiles_n, plan.tiles_m, 4 * TM * TN), 64, 0, stream>>>(args);
@@ -751,7 +762,8 @@ void launch_shape(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t st
 }  // namespace
 
 hipError_t launch_conv_gemm(const ConvGemmArgs& args, const GemmPlan& plan, hipStream_t stream) {
-    if (args.k % 32 || args.channels_in % 32 || args.n % 16 || args.m < 1 || args.splits != plan.splits ||
+    if (args.k % plan.k_step || args.channels_in % plan.k_step || args.n % 16 || args.m < 1 ||
+        args.splits != plan.splits ||
         (plan.splits > 1 && !args.partial))
         return hipErrorInvalidValue;
     switch (plan.shape) {

@@ -354,16 +354,16 @@ void layout_session(Qwen3TtsCodecContextV1* s, Arena& a) {
         Plans& p = s->plans[f];
         for (int u = 0; u < 2; ++u) {
             const int m = f << u;  // 1x / 2x frames in, then 2x / 4x after the transposed conv
-            p.up_tconv[u] = plan_conv_gemm(m, 2048, 1024, s->cus);
-            p.pw1[u] = plan_conv_gemm(2 * m, 4096, 1024, s->cus);
-            p.pw2[u] = plan_conv_gemm(2 * m, 1024, 4096, s->cus);
+            p.up_tconv[u] = plan_conv_gemm(m, 2048, 1024, 1024, s->cus);
+            p.pw1[u] = plan_conv_gemm(2 * m, 4096, 1024, 1024, s->cus);
+            p.pw2[u] = plan_conv_gemm(2 * m, 1024, 4096, 4096, s->cus);
         }
-        p.conv0 = plan_conv_gemm(4 * f, 1536, 7 * 1024, s->cus);
+        p.conv0 = plan_conv_gemm(4 * f, 1536, 7 * 1024, 1024, s->cus);
         for (int t = 0; t < 4; ++t) {
             const int p_in = (int)stage_input_positions(t, f), p_out = p_in * kStride[t];
-            p.tconv[t] = plan_conv_gemm(p_in, kStride[t] * kStageOut[t], 2 * kStageIn[t], s->cus);
-            p.conv7[t] = plan_conv_gemm(p_out, kStageOut[t], 7 * kStageOut[t], s->cus);
-            p.conv1[t] = plan_conv_gemm(p_out, kStageOut[t], kStageOut[t], s->cus);
+            p.tconv[t] = plan_conv_gemm(p_in, kStride[t] * kStageOut[t], 2 * kStageIn[t], kStageIn[t], s->cus);
+            p.conv7[t] = plan_conv_gemm(p_out, kStageOut[t], 7 * kStageOut[t], kStageOut[t], s->cus);
+            p.conv1[t] = plan_conv_gemm(p_out, kStageOut[t], kStageOut[t], kStageOut[t], s->cus);
         }
         const GemmPlan* all[] = {&p.up_tconv[0], &p.up_tconv[1], &p.pw1[0], &p.pw1[1], &p.pw2[0], &p.pw2[1],
                                  &p.conv0, &p.tconv[0], &p.tconv[1], &p.tconv[2], &p.tconv[3], &p.conv7[0],
