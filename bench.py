@@ -598,7 +598,7 @@ def main() -> int:
         if args.codec_frames:
             out = codec_benchmark(packets=50, warm=5, streams=0, sizes=(args.codec_frames,), cpu=False)
         else:
-            out = codec_benchmark()
+            out = codec_benchmark(cpu=not args.no_cpu)
         print(json.dumps({"codec": out}), flush=True)
         return 0
     if args.only_batched_frames:

@@ -716,9 +716,11 @@ size_t GemmPlan::partial_floats() const {
 GemmPlan plan_conv_gemm(int m, int n, int k, int channels_in, int cus) {
     // Blocks in flight hide the per-step load latency: weight-streaming shapes
     // (<= 16 rows) take 16x64 tiles and split K to ~2 blocks per CU; longer
-    // sequences take the largest tile that still gives ~2 blocks per CU, then
-    // split K (each slice keeping >= 4 steps of 32) if the tiles alone fall
-    // short.  (Chosen from per-layer measurements on MI355X.)
+    // sequences take the largest tile that still gives ~2 blocks per CU, and
+    // split K (to ~1.5 blocks per CU, each slice keeping >= 4 steps) only when
+    // the tiles alone do not cover the CUs: the partial round trip and the
+    // reduction launch cost more than they gain above that.  (Chosen from
+    // per-layer measurements on MI355X.)
     GemmPlan plan;
     // 64-float K steps (half the barriers) wherever the channels allow
     plan.k_step = channels_in % 64 == 0 ? 64 : 32;
@@ -740,7 +742,12 @@ GemmPlan plan_conv_gemm(int m, int n, int k, int channels_in, int cus) {
     plan.tiles_m = (m + kTileRows[s] - 1) / kTileRows[s];
     plan.tiles_n = (n + kTileCols[s] - 1) / kTileCols[s];
     const long long tiles = (long long)plan.tiles_m * plan.tiles_n;
-    long long splits = tiles < want ? (want + tiles - 1) / tiles : 1;
+    long long splits = 1;
+    if (plan.shape == GemmShape::k16x64) {
+        splits = (want + tiles - 1) / tiles;
+    } else if (tiles < cus) {
+        splits = (3LL * cus / 2 + tiles - 1) / tiles;
+    }
     splits = std::min<long long>(splits, std::max(1, (k / plan.k_step) / 4));
     plan.splits = (int)std::max<long long>(1, splits);
     return plan;
