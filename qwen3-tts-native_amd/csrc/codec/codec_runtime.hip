@@ -26,10 +26,31 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
 using namespace q3c;
+
+// The ABI's layouts, as the reference's Rust binding and its contract test
+// pin them (native/qwen3-tts-native-codec/src/ffi.rs:169-201,
+// native/qwen3-tts-native-codec/native/tests/abi_v2_contract.cpp).
+static_assert(sizeof(Qwen3TtsCodecPacketResultV1) == 40 && alignof(Qwen3TtsCodecPacketResultV1) == 8, "ABI");
+static_assert(sizeof(Qwen3TtsCodecDevicePacketBeginV2) == 40 && alignof(Qwen3TtsCodecDevicePacketBeginV2) == 8, "ABI");
+static_assert(sizeof(Qwen3TtsCodecDevicePacketBeginResultV2) == 32, "ABI");
+static_assert(sizeof(Qwen3TtsCodecDevicePacketFinishV2) == 56, "ABI");
+static_assert(std::is_standard_layout<Qwen3TtsCodecDevicePacketBeginV2>::value &&
+                  std::is_standard_layout<Qwen3TtsCodecDevicePacketBeginResultV2>::value &&
+                  std::is_standard_layout<Qwen3TtsCodecDevicePacketFinishV2>::value,
+              "ABI");
+static_assert(offsetof(Qwen3TtsCodecDevicePacketBeginV2, struct_size) == 0 &&
+                  offsetof(Qwen3TtsCodecDevicePacketBeginResultV2, struct_size) == 0 &&
+                  offsetof(Qwen3TtsCodecDevicePacketFinishV2, struct_size) == 0,
+              "ABI");
+static_assert(sizeof(Qwen3TtsCodecStateInfoV1) == 80 && sizeof(Qwen3TtsCodecBatchItemV1) == 48 &&
+                  sizeof(Qwen3TtsCodecTensorViewV1) == 56 && sizeof(Qwen3TtsCodecWeightProviderV1) == 32 &&
+                  sizeof(Qwen3TtsCodecModelInfoV1) == 40,
+              "ABI");
 
 namespace {
 

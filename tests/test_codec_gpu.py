@@ -330,3 +330,25 @@ def test_fixture_packets_match_reference_model(codec):
     s.reset()
     again, _ = s.fixture_packet(frames[:1])
     np.testing.assert_array_equal(again, want[:1920])
+
+
+def test_every_packet_size_with_bf16_sources(codec):
+    """Packets of 2, 3, 1, 4, 2 frames (every graph size) from a model whose
+    271 tensors arrive as bf16 (widened on the device, CS:3206-3240), against
+    the oracle on the same bf16-rounded weights."""
+    print("codec bf16 model, packets 2/3/1/4/2", flush=True)
+    w32 = M.make_weights(5)
+    bits = {k: O.f32_to_bf16(v) for k, v in w32.items()}
+    rounded = {k: O.bf16_to_f32(v) for k, v in bits.items()}
+    m = codec.SharedModel(bits)
+    assert m.info.source_dtype_bf16_count == 271 and m.info.source_bytes == 2 * 114_323_137
+    codes = M.random_codes(12, 9)
+    plan = ((0, 2), (2, 5), (5, 6), (6, 10), (10, 12))
+    s = m.session()
+    orc = O.CodecOracle(rounded)
+    got = np.concatenate([s.packet(codes[a:b])[0] for a, b in plan])
+    want = np.concatenate([orc.packet(codes[a:b], trace=False)["pcm"] for a, b in plan])
+    diff = np.abs(got.astype(np.int32) - want)
+    print(f"  PCM vs oracle: max diff {diff.max()}, identical {(diff == 0).mean():.4f}", flush=True)
+    assert got.size == 12 * 1920 and diff.max() <= 1 and (diff == 0).mean() > 0.85
+    m.close()
