@@ -8,7 +8,7 @@
 // with A and B row-major and K contiguous in both (activations x weights^T,
 // queries x keys^T, probabilities x values^T), batched over heads through
 // gridDim.z with a grouped B index for GQA.  A 128x128 (or, when that leaves
-// CUs idle, 64x64) block tile of 256 threads (4 waves in 2x2, each a grid of
+// CUs idle, 64x64 or 32x32) block tile of 256 threads (4 waves in 2x2, each a grid of
 // v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 staged through
 // double-buffered LDS (padded rows), the next step's global loads issued
 // before the current step's MFMAs.
@@ -267,12 +267,15 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);
     if ((align & 15u) != 0 || (g.a_batch % 8) != 0 || (g.b_batch % 8) != 0) return hipErrorInvalidValue;
-    // 128 x 128 tiles when they give at least two workgroups per CU, else 64 x 64
-    const long long big = static_cast<long long>((g.n + 127) / 128) * ((g.m + 127) / 128) * g.batch;
-    if (big >= 512) {
+    // the largest tile (128, 64 or 32 square) that still gives at least two
+    // workgroups per CU
+    auto blocks = [&](int t) { return static_cast<long long>((g.n + t - 1) / t) * ((g.m + t - 1) / t) * g.batch; };
+    if (blocks(128) >= 512) {
         gemm_bf16_kernel<128, 128><<<dim3((g.n + 127) / 128, (g.m + 127) / 128, g.batch), kGemmThreads, 0, stream>>>(g);
-    } else {
+    } else if (blocks(64) >= 512) {
         gemm_bf16_kernel<64, 64><<<dim3((g.n + 63) / 64, (g.m + 63) / 64, g.batch), kGemmThreads, 0, stream>>>(g);
+    } else {
+        gemm_bf16_kernel<32, 32><<<dim3((g.n + 31) / 32, (g.m + 31) / 32, g.batch), kGemmThreads, 0, stream>>>(g);
     }
     return hipGetLastError();
 }

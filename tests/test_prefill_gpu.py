@@ -56,8 +56,9 @@ def within_bound(got_bits, a_bits, b_bits):
     return np.abs(gen.f32(got_bits).astype(np.float64) - ref) <= bound
 
 
+# every tile size the launcher picks: 32 (all but the last two), 64, 128
 @pytest.mark.parametrize("m,n,k", [(1, 3072, 2048), (66, 2048, 2048), (130, 1024, 6144), (257, 384, 1024),
-                                   (5, 100, 64), (200, 136, 8)])
+                                   (5, 100, 64), (200, 136, 8), (1000, 2048, 256), (2048, 4096, 128)])
 def test_bf16_gemm_matches_float64(hip, orc, m, n, k):
     rng = np.random.default_rng(m * 7 + n + k)
     a = gen.activations(rng, m, k)
