@@ -352,3 +352,69 @@ def test_every_packet_size_with_bf16_sources(codec):
     print(f"  PCM vs oracle: max diff {diff.max()}, identical {(diff == 0).mean():.4f}", flush=True)
     assert got.size == 12 * 1920 and diff.max() <= 1 and (diff == 0).mean() > 0.85
     m.close()
+
+
+def test_argument_and_state_errors(codec, model, codes):
+    """Status codes and states of the reference's state machine
+    (codec_state.cu:3984-4009, 4345-4380, 5004-5027, 5144-5330)."""
+    lib = codec.load()
+    err = C.create_string_buffer(256)
+    s = model.session()
+    pcm = np.zeros(7680, np.int16)
+    res = codec.PacketResult()
+    c5 = np.zeros((5, 16), np.uint16)
+    # 0 or 5 frames, bad is_final, small capacity, codes out of range
+    assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, c5.ctypes.data, 0, 0, pcm.ctypes.data, 7680,
+                                                         C.byref(res), err, 256) == -1
+    assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, c5.ctypes.data, 5, 0, pcm.ctypes.data, 7680,
+                                                         C.byref(res), err, 256) == -1
+    assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, c5.ctypes.data, 1, 2, pcm.ctypes.data, 7680,
+                                                         C.byref(res), err, 256) == -1
+    assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, c5.ctypes.data, 2, 0, pcm.ctypes.data, 1919 * 2,
+                                                         C.byref(res), err, 256) == -1
+    assert b"capacity" in err.value
+    bad = np.full((1, 16), 2048, np.uint16)
+    assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, bad.ctypes.data, 1, 0, pcm.ctypes.data, 7680,
+                                                         C.byref(res), err, 256) == -1
+    # none of these advanced the stream
+    assert s.state().frame_position == 0
+    # debug hooks: bad checkpoint id, small capacity
+    out = np.zeros(16, np.float32)
+    assert lib.qwen3_tts_codec_debug_decoder_checkpoint_v1(s.handle, codes.ctypes.data, 1, 14, out.ctypes.data,
+                                                           out.size, err, 256) == -1
+    assert lib.qwen3_tts_codec_debug_transformer_packet_v1(s.handle, codes.ctypes.data, 1, out.ctypes.data, 16,
+                                                           err, 256) == -1
+    # cancel while a device ticket is pending: the ticket is dropped, the
+    # stream needs a reset
+    hip = _hip_runtime()
+    buf, ready = C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(buf), 64) == 0 and hip.hipEventCreate(C.byref(ready)) == 0
+    try:
+        one = np.ascontiguousarray(codes[:1])
+        assert hip.hipMemcpy(buf, one.ctypes.data, 32, 1) == 0
+        assert hip.hipEventRecord(ready, None) == 0
+        begin = codec.DevicePacketBegin(C.sizeof(codec.DevicePacketBegin), 0, buf.value, 1, 0, ready.value, 0)
+        outb = codec.DevicePacketBeginResult(C.sizeof(codec.DevicePacketBeginResult), 0, 0, None, 0)
+        codec.call("qwen3_tts_codec_session_process_device_packet_begin_v2", s.handle, C.byref(begin), C.byref(outb))
+        # a host packet while the ticket is pending is a state error
+        assert lib.qwen3_tts_codec_session_process_packet_v1(s.handle, one.ctypes.data, 1, 0, pcm.ctypes.data,
+                                                             7680, C.byref(res), err, 256) == -3
+        s.cancel()
+        fin = codec.DevicePacketFinish(C.sizeof(codec.DevicePacketFinish), 0, outb.ticket_id, 0, 0,
+                                       pcm.ctypes.data, pcm.size, C.pointer(res), 0)
+        assert lib.qwen3_tts_codec_session_process_device_packet_finish_v2(s.handle, C.byref(fin), err, 256) == -3
+        # a wrong struct size is rejected before anything runs
+        s.reset()
+        begin.struct_size = 8
+        assert lib.qwen3_tts_codec_session_process_device_packet_begin_v2(s.handle, C.byref(begin), C.byref(outb),
+                                                                           err, 256) == -1
+        # after the reset the stream decodes from the start again
+        first, r = s.packet(codes[:1])
+        assert r.first_frame_position == 0 and first.size == 1920
+    finally:
+        hip.hipFree(buf)
+        hip.hipEventDestroy(ready)
+    mem = s.memory()
+    st = s.state()
+    assert mem.device_bytes == st.device_bytes > mem.transformer_kv_bytes > 0
+    assert mem.codec_ring_bytes == 3 * 4 * 16 * 2 and mem.pcm_ring_bytes == 3 * 7680 * 2
