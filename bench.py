@@ -303,10 +303,11 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
 PREFILL_FLOPS_PER_ROW = 2 * 28 * (2048 * 2048 + 2 * 1024 * 2048 + 2048 * 2048 + 3 * 6144 * 2048)
 
 
-def prefill_benchmark(hip, rows_list=(512, 801), repeats: int = 5, max_seq: int = 1024):
+def prefill_benchmark(hip, rows_list=(96, 512, 801), repeats: int = 5, max_seq: int = 1024):
     """The bf16 prompt prefill through the C ABI at VoiceDesign geometry:
-    prompts of `rows_list` positions (512: GEMM attention, the largest the
-    reference's GEMM path takes; 801: the exact per-row attention), the
+    prompts of `rows_list` positions (96: a short voice-design prompt, whose
+    GEMMs split K; 512: GEMM attention, the largest the reference's GEMM path
+    takes; 801: the exact per-row attention), the
     median of `repeats` prefills each (qwen3_tts_session_prefill's own GPU
     time), as prompt positions per second and the GEMMs' TFLOP/s."""
     import numpy as np
@@ -545,6 +546,93 @@ def codec_benchmark(packets: int = 200, warm: int = 20, streams: int = 6, sizes=
     return out
 
 
+def streaming_benchmark(hip, requests: int = 6, prompt: int = 96, frames: int = 100, packet_frames: int = 4):
+    """One voice-design request after another on one warm talker session and
+    one decoder session, both libraries in this process, as a serving loop
+    would run them (the reference's qwen3-tts-bench defaults: 4-frame
+    packets; session_bench.rs measures TTFA from request start to the first
+    frame's codes).  Each request: session reset, prefill of a `prompt`-token
+    prompt (bf16 path), then `frames` frames (top-k 50 / T 0.9), every
+    `packet_frames` frames decoded to PCM through the host-code packet API;
+    talker and decoder run one after the other on this thread (no overlap).
+    Reports the median TTFA to the first frame's codes and to the first PCM
+    packet, and the end-to-end RTF (wall time over audio time).  Random
+    weights: the reference's published figures (0.287-0.47 RTF, TTFA p50
+    55-60 ms on a DGX Spark) are for its real checkpoint and
+    prompts, so the comparison is of work per frame, not of audio."""
+    import numpy as np
+    import qwen3_tts_codec_hip as codec
+
+    lib = hip.load()
+    model, cfg = build_model(hip)
+    cmodel = codec.SharedModel(codec_weights())
+    try:
+        session = C.c_void_p()
+        smem = hip.SessionMemory()
+        hip.call("qwen3_tts_session_create", model, 1024, 9, C.byref(session), C.byref(smem))
+        dec = cmodel.session()
+        try:
+            rng = np.random.default_rng(11)
+            ts = hip.sampling(1, 50, 1.0, 0.9, 1.05)
+            ps = hip.sampling(1, 50, 1.0, 0.9, 1.0)
+            codes = (C.c_uint16 * 16)()
+            info = hip.CodecFrameInfo()
+            nxt = C.c_uint16()
+            ttfa_codes, ttfa_pcm, rtf, done_frames, eos = [], [], [], 0, 0
+            for r in range(requests + 1):  # the first request warms up
+                text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
+                cprompt = rng.integers(0, 2048, prompt).astype(np.int32)
+                trailing = rng.integers(0, cfg.text_vocabulary, frames).astype(np.int32)
+                hip.synchronize()
+                t0 = time.perf_counter()
+                hip.call("qwen3_tts_session_reset", session, 100 + r)
+                dec.reset()
+                pre = hip.PrefillResult()
+                hip.call("qwen3_tts_session_prefill", session, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                         cprompt.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(pre))
+                semantic = C.c_uint16(pre.first_semantic_token)
+                pending, first_codes, first_pcm, n = [], None, None, 0
+                for f in range(frames):
+                    if semantic.value == cfg.codec_eos_token:
+                        eos += 1
+                        break
+                    hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts, ps, codes, 16,
+                             C.byref(nxt), C.byref(info))
+                    if first_codes is None:
+                        first_codes = time.perf_counter() - t0
+                    pending.append(np.frombuffer(codes, np.uint16).copy())
+                    semantic = C.c_uint16(nxt.value)
+                    n += 1
+                    if len(pending) == packet_frames:
+                        dec.packet(np.stack(pending))
+                        pending = []
+                        if first_pcm is None:
+                            first_pcm = time.perf_counter() - t0
+                if pending:
+                    dec.packet(np.stack(pending), is_final=True)
+                wall = time.perf_counter() - t0
+                if r and n >= packet_frames:
+                    ttfa_codes.append(first_codes * 1e3)
+                    ttfa_pcm.append(first_pcm * 1e3)
+                    rtf.append(wall / (n * 0.08))
+                    done_frames += n
+            if not rtf:
+                raise RuntimeError("every timed request ended by the end token before its first packet")
+            return {"requests": len(rtf), "prompt_tokens": prompt, "frames_per_request": frames,
+                    "frames_decoded": done_frames, "packet_frames": packet_frames,
+                    "ttfa_codes_ms_p50": round(float(np.median(ttfa_codes)), 2),
+                    "ttfa_pcm_ms_p50": round(float(np.median(ttfa_pcm)), 2),
+                    "rtf_end_to_end_p50": round(float(np.median(rtf)), 4),
+                    "requests_ended_by_eos": eos,
+                    "reference_dgx_spark": {"rtf": "0.287-0.47", "ttfa_p50_ms": "55-60"}}
+        finally:
+            dec.close()
+            lib.qwen3_tts_session_destroy(session)
+    finally:
+        cmodel.close()
+        lib.qwen3_tts_model_destroy(model)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -568,6 +656,9 @@ def main() -> int:
     ap.add_argument("--codec-frames", type=int, default=0,
                     help="with --only-codec: one packet size only (1..4) and no batched streams (a clean "
                          "per-layer kernel trace)")
+    ap.add_argument("--only-streaming", action="store_true",
+                    help="run only the end-to-end streaming requests (talker prefill and frames, 4-frame "
+                         "decoder packets; TTFA and RTF)")
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
@@ -600,6 +691,9 @@ def main() -> int:
         else:
             out = codec_benchmark(cpu=not args.no_cpu)
         print(json.dumps({"codec": out}), flush=True)
+        return 0
+    if args.only_streaming:
+        print(json.dumps({"streaming": streaming_benchmark(hip)}), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
@@ -674,6 +768,10 @@ def main() -> int:
             line["batched_frames"] = batched_frames(hip)
         except Exception as e:  # report, never hide
             line["batched_frames"] = {"error": str(e)}
+        try:
+            line["streaming"] = streaming_benchmark(hip)
+        except Exception as e:  # report, never hide
+            line["streaming"] = {"error": str(e)}
         try:
             line["codec"] = codec_benchmark(cpu=not args.no_cpu)
         except Exception as e:  # report, never hide

@@ -9,9 +9,11 @@
 // queries x keys^T, probabilities x values^T), batched over heads through
 // gridDim.z with a grouped B index for GQA.  A 128x128 (or, when that leaves
 // CUs idle, 64x64 or 32x32) block tile of 256 threads (4 waves in 2x2, each a grid of
-// v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 staged through
-// double-buffered LDS (padded rows), the next step's global loads issued
-// before the current step's MFMAs.
+// v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 (128, 256 for the smaller
+// tiles) staged through double-buffered LDS (padded rows), the next step's
+// global loads issued before the current step's MFMAs.  Short prompts, whose
+// grids leave CUs idle and whose steps each wait one memory latency, split K
+// into slices (fp32 partial sums, added in slice order by a second launch).
 //
 // The summation order of an fp32 GEMM is not the reference's (cuBLAS leaves
 // it unspecified), so this path is compared with tolerances; everything
@@ -29,8 +31,6 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;
-constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
 constexpr int kGemmThreads = 256;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -45,12 +45,16 @@ __device__ __forceinline__ uint4 load_chunk(const bf16_t* base, int ld, int row,
 
 // Block tile kBM x kBN, four waves in 2 x 2, each (kBM/2) x (kBN/2) as
 // (kBM/32) x (kBN/32) 16x16 MFMA tiles.
-template <int kBM, int kBN>
-__global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g) {
+// gridDim.z = batch * splits: slice `split` covers K steps
+// [split * steps_per_split, ...) and writes fp32 partial sums when splits > 1.
+template <int kBM, int kBN, int kBK>
+__global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g, int splits, int steps_per_split) {
+    constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
+    constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per row and K step
     constexpr int kTM = kBM / 32;                 // MFMA tiles per wave along M
     constexpr int kTN = kBN / 32;                 // and along N
-    constexpr int kChunksA = kBM * 8 / kGemmThreads;  // 16-byte chunks per thread per K step
-    constexpr int kChunksB = kBN * 8 / kGemmThreads;
+    constexpr int kChunksA = kBM * kRowChunks / kGemmThreads;  // 16-byte chunks per thread per K step
+    constexpr int kChunksB = kBN * kRowChunks / kGemmThreads;
     __shared__ __align__(16) bf16_t as[2][kBM * kLdsRow];
     __shared__ __align__(16) bf16_t bs[2][kBN * kLdsRow];
     const int tid = threadIdx.x;
@@ -58,7 +62,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
     const int lane = tid & 63;
     const int m0 = blockIdx.y * kBM;
     const int n0 = blockIdx.x * kBN;
-    const int z = blockIdx.z;
+    const int z = blockIdx.z % g.batch;
+    const int split = blockIdx.z / g.batch;
     const bf16_t* a = g.a + static_cast<size_t>(z) * g.a_batch;
     const bf16_t* b = g.b + static_cast<size_t>(z / g.b_group) * g.b_batch;
     bf16_t* c = g.c + static_cast<size_t>(z) * g.c_batch;
@@ -68,24 +73,24 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
 #pragma unroll
         for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            ra[i] = load_chunk(a, g.lda, m0 + (chunk >> 3), g.m, k0 + (chunk & 7) * 8, g.k);
+            ra[i] = load_chunk(a, g.lda, m0 + chunk / kRowChunks, g.m, k0 + (chunk % kRowChunks) * 8, g.k);
         }
 #pragma unroll
         for (int i = 0; i < kChunksB; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            rb[i] = load_chunk(b, g.ldb, n0 + (chunk >> 3), g.n, k0 + (chunk & 7) * 8, g.k);
+            rb[i] = load_chunk(b, g.ldb, n0 + chunk / kRowChunks, g.n, k0 + (chunk % kRowChunks) * 8, g.k);
         }
     };
     auto stage = [&](int buffer) {
 #pragma unroll
         for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            *reinterpret_cast<uint4*>(&as[buffer][(chunk >> 3) * kLdsRow + (chunk & 7) * 8]) = ra[i];
+            *reinterpret_cast<uint4*>(&as[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < kChunksB; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            *reinterpret_cast<uint4*>(&bs[buffer][(chunk >> 3) * kLdsRow + (chunk & 7) * 8]) = rb[i];
+            *reinterpret_cast<uint4*>(&bs[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) = rb[i];
         }
     };
 
@@ -99,13 +104,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
 #pragma unroll
         for (int j = 0; j < kTN; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int steps = (g.k + kBK - 1) / kBK;
-    fetch(0);
+    const int first = split * steps_per_split;
+    const int steps = min((g.k + kBK - 1) / kBK - first, steps_per_split);
+    const int k_base = first * kBK;
+    fetch(k_base);
     stage(0);
     __syncthreads();
     for (int s = 0; s < steps; ++s) {
         const int buffer = s & 1;
-        if (s + 1 < steps) fetch((s + 1) * kBK);  // in flight under the MFMAs
+        if (s + 1 < steps) fetch(k_base + (s + 1) * kBK);  // in flight under the MFMAs
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
             bf16x8_t af[kTM], bfr[kTN];
@@ -128,6 +135,23 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
         }
     }
     // acc[i][j][r] = C[wm + 16 i + 4 group + r][wn + 16 j + m]
+    if (splits > 1) {
+        float* p = g.partial + (static_cast<size_t>(split) * g.batch + z) * g.m * g.n;
+#pragma unroll
+        for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm + 16 * i + 4 * group + r;
+                if (row >= g.m) continue;
+#pragma unroll
+                for (int j = 0; j < kTN; ++j) {
+                    const int col = n0 + wn + 16 * j + m;
+                    if (col < g.n) p[static_cast<size_t>(row) * g.n + col] = acc[i][j][r];
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
 #pragma unroll
@@ -141,6 +165,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g)
             }
         }
     }
+}
+
+// Split-K reduction: C[z][row][col] = bf16(sum over slices, in slice order,
+// of the fp32 partials).  Block (column block, row, batch entry), one thread
+// per column.
+__global__ __launch_bounds__(256) void gemm_bf16_reduce_kernel(Bf16GemmArgs g, int splits) {
+    const int col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= g.n) return;
+    const int row = blockIdx.y;
+    const int z = blockIdx.z;
+    const size_t slice = static_cast<size_t>(g.m) * g.n * g.batch;
+    const float* p = g.partial + (static_cast<size_t>(z) * g.m + row) * g.n + col;
+    float sum = p[0];
+    for (int s = 1; s < splits; ++s) sum += p[s * slice];
+    g.c[static_cast<size_t>(z) * g.c_batch + static_cast<size_t>(row) * g.ldc + col] = f2bf(sum);
 }
 
 // causal_softmax_kernel (talker_kernels.cu:232-260) on bf16 scores
@@ -267,15 +306,65 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);
     if ((align & 15u) != 0 || (g.a_batch % 8) != 0 || (g.b_batch % 8) != 0) return hipErrorInvalidValue;
-    // the largest tile (128, 64 or 32 square) that still gives at least two
-    // workgroups per CU
+    // Tiles and K steps (measured on MI355X over the prefill's shapes, 16..801
+    // rows): 128-square only where it still gives two workgroups per CU,
+    // else 64-square for more than 128 rows and 32-square below; K steps of
+    // 256 / 128 / 64 -- each step waits one memory latency, so short prompts
+    // want long steps, but a 256-step 32-square tile holds 66 KB of LDS (two
+    // workgroups per CU), which costs more than it saves from 65 rows on.
     auto blocks = [&](int t) { return static_cast<long long>((g.n + t - 1) / t) * ((g.m + t - 1) / t) * g.batch; };
-    if (blocks(128) >= 512) {
-        gemm_bf16_kernel<128, 128><<<dim3((g.n + 127) / 128, (g.m + 127) / 128, g.batch), kGemmThreads, 0, stream>>>(g);
-    } else if (blocks(64) >= 512) {
-        gemm_bf16_kernel<64, 64><<<dim3((g.n + 63) / 64, (g.m + 63) / 64, g.batch), kGemmThreads, 0, stream>>>(g);
+    int tile = g.force_tile;
+    if (tile == 0) tile = blocks(128) >= 512 ? 128 : g.m > 128 ? 64 : 32;
+    if (tile != 32 && tile != 64 && tile != 128) return hipErrorInvalidValue;
+    int bk = g.force_k_step;
+    if (bk == 0) bk = tile == 32 ? (g.m <= 64 ? 256 : 128) : tile == 64 ? 128 : 64;
+    if (!((tile == 32 && (bk == 64 || bk == 128 || bk == 256)) || (tile == 64 && (bk == 64 || bk == 128)) ||
+          (tile == 128 && bk == 64))) {
+        return hipErrorInvalidValue;
+    }
+    const int steps = (g.k + bk - 1) / bk;
+    int splits = g.force_splits;
+    if (splits == 0) {
+        // K slices (with a workspace): the 32-square tile keeps a slice to
+        // 2048 K and spreads a grid of under 128 workgroups to about 512 (two
+        // steps a slice at least); the larger tiles split a grid of under 384
+        // workgroups toward 512, a slice keeping 12 steps at least
+        const long long tiles = blocks(tile);
+        if (tile == 32) {
+            splits = (g.k + 2047) / 2048;
+            if (tiles < 128) {
+                splits = std::max<long long>(splits, std::min<long long>((512 + tiles - 1) / tiles, steps / 2));
+            }
+        } else {
+            splits = tiles < 384 ? static_cast<int>(std::min<long long>((512 + tiles - 1) / tiles, (steps + 11) / 12))
+                                 : 1;
+        }
+    }
+    splits = std::max(1, std::min(splits, steps));
+    const size_t plane = static_cast<size_t>(g.m) * g.n * g.batch;
+    if (g.partial == nullptr) {
+        splits = 1;
     } else {
-        gemm_bf16_kernel<32, 32><<<dim3((g.n + 31) / 32, (g.m + 31) / 32, g.batch), kGemmThreads, 0, stream>>>(g);
+        splits = std::min<size_t>(splits, g.partial_floats / plane);
+        if (splits < 1) splits = 1;
+    }
+    const int per = (steps + splits - 1) / splits;
+    splits = (steps + per - 1) / per;  // no empty slice
+    const dim3 grid((g.n + tile - 1) / tile, (g.m + tile - 1) / tile, g.batch * splits);
+    if (tile == 128) {
+        gemm_bf16_kernel<128, 128, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+    } else if (tile == 64) {
+        if (bk == 128) gemm_bf16_kernel<64, 64, 128><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else gemm_bf16_kernel<64, 64, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+    } else {
+        if (bk == 256) gemm_bf16_kernel<32, 32, 256><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else if (bk == 128) gemm_bf16_kernel<32, 32, 128><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else gemm_bf16_kernel<32, 32, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+    }
+    if (splits > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        gemm_bf16_reduce_kernel<<<dim3((g.n + 255) / 256, g.m, g.batch), 256, 0, stream>>>(g, splits);
     }
     return hipGetLastError();
 }

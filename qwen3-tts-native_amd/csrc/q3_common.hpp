@@ -359,6 +359,14 @@ struct Bf16GemmArgs {
     int batch = 1;
     int b_group = 1;
     long long a_batch = 0, b_batch = 0, c_batch = 0;
+    // Split-K workspace (may be null: no split).  With `splits` > 1 each K
+    // slice writes fp32 partial sums here and a second launch adds the slices
+    // in slice order and rounds to bf16.
+    float* partial = nullptr;
+    size_t partial_floats = 0;
+    int force_tile = 0;    // 0: planned; else 32, 64 or 128
+    int force_k_step = 0;  // 0: planned; else K per pipeline step (32 tile: 64/128/256; 64: 64/128; 128: 64)
+    int force_splits = 0;  // 0: planned; else the K slices (bounded by the workspace)
 };
 hipError_t launch_bf16_gemm(const Bf16GemmArgs& args, hipStream_t stream);
 // Prompts of at most this many positions run the reference's GEMM attention

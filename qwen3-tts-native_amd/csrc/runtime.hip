@@ -732,6 +732,39 @@ QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_v1(const uint16_t* a, const uint16_
     return launch_status(launch_bf16_gemm(g, as_stream(stream)), "bf16 GEMM", error, cap);
 }
 
+QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_split_v1(const uint16_t* a, const uint16_t* b, uint16_t* c, int32_t m,
+                                                      int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t ldc,
+                                                      int32_t batch, int32_t b_group, int64_t a_batch, int64_t b_batch,
+                                                      int64_t c_batch, float* partial, uint64_t partial_floats,
+                                                      int32_t tile, int32_t k_step, int32_t splits, void* stream,
+                                                      char* error, size_t cap) {
+    if (tile < 0 || k_step < 0 || splits < 0 || (partial == nullptr && partial_floats != 0)) {
+        write_error(error, cap, "bf16 GEMM: negative tile, K step or split count, or a workspace size without a workspace");
+        return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
+    }
+    Bf16GemmArgs g;
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    g.batch = batch;
+    g.b_group = b_group;
+    g.a_batch = a_batch;
+    g.b_batch = b_batch;
+    g.c_batch = c_batch;
+    g.partial = partial;
+    g.partial_floats = static_cast<size_t>(partial_floats);
+    g.force_tile = tile;
+    g.force_k_step = k_step;
+    g.force_splits = splits;
+    return launch_status(launch_bf16_gemm(g, as_stream(stream)), "bf16 GEMM (split)", error, cap);
+}
+
 QWEN3_TTS_API int32_t qwen3_tts_op_causal_softmax_v1(uint16_t* scores, int32_t heads, int32_t rows, int32_t stride,
                                                      int32_t head_dimension, void* stream, char* error, size_t cap) {
     return launch_status(launch_causal_softmax(scores, heads, rows, stride, head_dimension, as_stream(stream)),

@@ -744,6 +744,8 @@ public:
             g.lda = lda;
             g.ldb = k;
             g.ldc = ldc;
+            g.partial = w.partial.as<float>();
+            g.partial_floats = kPrefillPartialFloats;
             check_hip(launch_bf16_gemm(g, stream_), what);
         };
         bf16_t* xn = w.normalized.as<bf16_t>();
@@ -782,6 +784,8 @@ public:
                 s.n = rows;
                 s.k = hd;
                 s.batch = T.query_heads;
+                s.partial = w.partial.as<float>();
+                s.partial_floats = kPrefillPartialFloats;
                 check_hip(launch_bf16_gemm(s, stream_), "prefill score GEMM");
                 check_hip(launch_causal_softmax(scores, T.query_heads, rows, rp, hd, stream_), "prefill causal softmax");
                 check_hip(launch_transpose_values(qkv, qkvw, qw + kvw, rows, rp, T.key_value_heads, vt, stream_),
@@ -801,6 +805,8 @@ public:
                 o.n = hd;
                 o.k = rp;
                 o.batch = T.query_heads;
+                o.partial = w.partial.as<float>();
+                o.partial_floats = kPrefillPartialFloats;
                 check_hip(launch_bf16_gemm(o, stream_), "prefill value GEMM");
             } else {
                 // the exact kernel, row r over positions 0..r, in chunks that
@@ -843,6 +849,8 @@ public:
         g.lda = H;
         g.ldb = H;
         g.ldc = cfg_.talker_vocab;
+        g.partial = prefill_.partial.as<float>();
+        g.partial_floats = kPrefillPartialFloats;
         check_hip(launch_bf16_gemm(g, stream_), "prefill codec head GEMM");
         pinned_[1] = rows;
         check_hip(hipMemcpyAsync(ints_.as<int>(), &pinned_[1], sizeof(int), hipMemcpyHostToDevice, stream_),
@@ -1040,11 +1048,14 @@ private:
 
     // Row buffers of the bf16 prefill, grown on demand and kept.
     static constexpr int kPrefillChunk = 128;  // rows per exact-attention launch
+    // split-K partial sums of the prefill GEMMs (short prompts), 16 MB
+    static constexpr size_t kPrefillPartialFloats = size_t{4} << 20;
     struct PrefillBuffers {
-        DeviceBuffer hidden, normalized, qkv, attn, proj, gate, up, scores, values_t, positions, workspace;
+        DeviceBuffer hidden, normalized, qkv, attn, proj, gate, up, scores, values_t, positions, workspace, partial;
         int rows = 0, score_stride = 0, capacity = 0;
         void ensure(int r, int H, int I, int qkvw, int qw, int query_heads, int kv_heads, int rp, int exact_capacity) {
             const size_t b = sizeof(bf16_t);
+            if (partial.as<void>() == nullptr) partial = DeviceBuffer(kPrefillPartialFloats * sizeof(float));
             if (r > rows) {
                 hidden = DeviceBuffer(static_cast<size_t>(r) * H * b);
                 normalized = DeviceBuffer(static_cast<size_t>(r) * H * b);

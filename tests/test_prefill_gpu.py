@@ -87,6 +87,76 @@ def test_bf16_gemm_batched_gqa_strides(hip, orc):
         assert not got[h, :, rows:].any()  # columns past n untouched
 
 
+def gemm_split(hip, a, b, m, n, k, tile, k_step, splits, workspace_floats=4 << 20, batch=1, b_group=1, a_batch=0,
+               b_batch=0, c_batch=0, lda=None, ldb=None, ldc=None, c_shape=None):
+    c_shape = c_shape or (m, n)
+    c = hip.DeviceArray(c_shape, np.uint16)
+    c.upload(np.zeros(c_shape, np.uint16))
+    part = hip.DeviceArray(max(workspace_floats, 1), np.float32)
+    hip.call("qwen3_tts_op_bf16_gemm_split_v1", a.ptr, b.ptr, c.ptr, m, n, k, lda or k, ldb or k, ldc or n, batch,
+             b_group, a_batch, b_batch, c_batch, part.ptr, workspace_floats, tile, k_step, splits, None)
+    return c.numpy()
+
+
+# short prompts (K split into slices added by a second launch), K not a
+# multiple of the step, columns not a multiple of the tile, and the planned form
+@pytest.mark.parametrize("m,n,k,tile,k_step,splits", [
+    (16, 1024, 2048, 32, 256, 4), (32, 2048, 6144, 32, 256, 8), (96, 2048, 6144, 32, 128, 3),
+    (5, 100, 1000, 32, 64, 5), (192, 2048, 6144, 64, 128, 4), (130, 200, 3000, 64, 64, 7),
+    (40, 300, 4096, 128, 64, 16), (16, 1024, 2048, 0, 0, 0), (96, 3072, 2048, 0, 0, 0),
+    (801, 1024, 6144, 0, 0, 0)])
+def test_bf16_gemm_split_matches_float64(hip, orc, m, n, k, tile, k_step, splits):
+    rng = np.random.default_rng(m + n + k + splits)
+    a = gen.activations(rng, m, k)
+    b = gen.bf16(0.05 * rng.standard_normal((n, k)).astype(np.float32))
+    da, db = dev(hip, a), dev(hip, b)
+    got = gemm_split(hip, da, db, m, n, k, tile, k_step, splits)
+    assert within_bound(got, a, b).all()
+    # no workspace: one slice, the same as the workspace-free entry point
+    plain = gemm(hip, da, db, m, n, k, k, k, n, (m, n))
+    if tile:
+        one = gemm_split(hip, da, db, m, n, k, tile, k_step, splits, workspace_floats=0)
+        assert within_bound(one, a, b).all()
+    assert within_bound(plain, a, b).all()
+
+
+def test_bf16_gemm_k_step_keeps_summation_order(hip, orc):
+    """Without a split the MFMA chain runs over K in the same 32-element
+    chunks whatever the pipeline step, so every K step gives identical bits."""
+    rng = np.random.default_rng(12)
+    m, n, k = 70, 160, 2056
+    a = gen.activations(rng, m, k)
+    b = gen.bf16(0.05 * rng.standard_normal((n, k)).astype(np.float32))
+    da, db = dev(hip, a), dev(hip, b)
+    for tile, steps in ((32, (64, 128, 256)), (64, (64, 128))):
+        outs = [gemm_split(hip, da, db, m, n, k, tile, s, 1) for s in steps]
+        for o in outs[1:]:
+            assert np.array_equal(o, outs[0]), tile
+
+
+def test_bf16_gemm_split_batched_gqa(hip, orc):
+    """The value GEMM shape of a short prompt with K slices: per head h,
+    probabilities [rows][k] times values^T of kv head h // 2."""
+    rng = np.random.default_rng(13)
+    heads, kvh, rows, k, d = 4, 2, 24, 512, 128
+    p = gen.activations(rng, heads * rows, k).reshape(heads, rows, k)
+    vt = gen.bf16(0.05 * rng.standard_normal((kvh, d, k)).astype(np.float32))
+    got = gemm_split(hip, dev(hip, p), dev(hip, vt), rows, d, k, 32, 64, 4, batch=heads, b_group=heads // kvh,
+                     a_batch=rows * k, b_batch=d * k, c_batch=rows * d, c_shape=(heads, rows, d))
+    for h in range(heads):
+        assert within_bound(got[h], p[h], vt[h // 2]).all(), h
+
+
+def test_bf16_gemm_split_rejects_bad_arguments(hip):
+    a = hip.DeviceArray(64 * 64, np.uint16)
+    with pytest.raises(hip.Qwen3TtsError):
+        gemm_split(hip, a, a, 8, 8, 64, 48, 0, 0)  # no such tile
+    with pytest.raises(hip.Qwen3TtsError):
+        gemm_split(hip, a, a, 8, 8, 64, 64, 256, 0)  # no such K step for the tile
+    with pytest.raises(hip.Qwen3TtsError):
+        gemm_split(hip, a, a, 8, 8, 64, 0, 0, -1)
+
+
 @pytest.mark.parametrize("rows,stride", [(1, 8), (9, 16), (70, 72), (512, 512)])
 def test_causal_softmax_bit_exact(hip, orc, rows, stride):
     rng = np.random.default_rng(rows)
