@@ -24,6 +24,8 @@
 // MFMA mode (rows 2..8): weights are dequantized int8 -> bf16 (exact) in
 // registers and fed to v_mfma_f32_16x16x32_bf16 with the session rows padded
 // to 16; the per-channel scale is applied after accumulation.
+#include <type_traits>
+
 #include "gemv_device.hpp"
 
 namespace q3 {
@@ -377,17 +379,18 @@ __global__ __launch_bounds__(kThreads) void gemv_mfma(GemvArgs a) {
 
 // ---------------------------------------------------------------------------
 // Batched rows (2..8 sessions) on MFMA, K = 64 * kWaves * kIters known at
-// compile time.  A block owns 16 output channels (16 gate + 16 up rows for the
-// SiLU epilogues); its 4 or 8 waves split K.  Latency order: with the RMSNorm
-// prologue the session rows are requested first; then every weight vector of
-// the wave's K slice (8 lanes per row, 128 contiguous bytes per row per load),
-// held in registers; the epilogue operands.  The rows are staged in LDS (and
-// normalized there with the RMSNorm prologue: statistic per row by one wave
-// with the reference's 256-thread tree) as the MFMA B operands.  Each 16-row
-// x 128-byte weight step is transposed through a per-wave LDS tile into the
-// v_mfma_f32_16x16x32_bf16 A operand layout.
+// compile time.  A block owns kGroups groups of 8 output channels (as many
+// gate and up rows for the SiLU epilogues); its 4 or 8 waves split K.
+// Latency order: the session rows are requested first; then every weight
+// vector of the wave's K slice, loaded straight in the
+// v_mfma_f32_16x16x32_bf16 A operand layout and held in registers; the
+// epilogue operands.  The rows are staged in LDS (and normalized there with
+// the RMSNorm prologue: statistic per row by one wave with the reference's
+// 256-thread tree) as the MFMA B operands, once per block for all of its
+// groups: more groups per block, fewer blocks repeating that work (the
+// launcher sizes the grid to one block per CU where the channel count allows).
 // ---------------------------------------------------------------------------
-template <int kIters, int kWaves, int kEpi, bool kNorm, int kSplit>
+template <int kIters, int kWaves, int kEpi, bool kNorm, int kGroups>
 __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     constexpr int kBlock = 64 * kWaves;
     if (a.input_row_index != nullptr) {
@@ -398,25 +401,29 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     constexpr int kIn = 64 * kWaves * kIters;
     constexpr int kStride = kIn + 8;  // bf16 elements per LDS row (16-byte pad)
     extern __shared__ __align__(16) bf16_t xs[];  // [rows][kStride]
-    __shared__ float fold[kWaves][kTiles][16][16];
+    __shared__ float fold[kWaves][kTiles][kGroups][16][16];
     __shared__ float inverse_lds[8];
     __shared__ __align__(16) float statistic[kNorm ? 8 : 1][256];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int rows = a.rows;
-    // kSplit = 2: the block owns 8 channels and the 16x16 tile is used
-    // block-diagonally -- A rows m and B columns m take channel / session
-    // m % 8 over the K half m / 8, so C[c][s] + C[c + 8][s + 8] is the sum
-    // over all of K with every weight byte still consumed once (twice the
-    // blocks for the same out_features).
-    static_assert(kSplit == 1 || kSplit == 2, "one or two K halves");
-    constexpr int kCh = 16 / kSplit;            // channels per block
-    constexpr int kSteps = kIters / kSplit;     // 64-wide k steps per wave
-    static_assert(kSteps * kSplit == kIters, "whole k steps per K part");
+    // Each group's 16x16 tile is used block-diagonally: A rows m and B
+    // columns m take channel / session m % 8 over the k in the first (m < 8)
+    // or second (m >= 8) 64 bytes of each 128-byte piece of the row, so
+    // C[c][s] + C[c + 8][s + 8] is the sum over all of K with every weight
+    // byte consumed once.  A wave's load instruction then covers 8 rows x 128
+    // contiguous bytes -- whole cache lines -- where a 16-channel tile would
+    // read 16 rows x 64 bytes (measured on MI355X at N = 8: gate/up
+    // 12288x2048 8.1 -> 6.8 us with the rest of the kernel stripped).
+    static_assert(kGroups >= 1 && kGroups <= 3, "one to three groups of 8 channels");
+    static_assert(kIters % 2 == 0, "whole 128-byte pieces per wave");
+    constexpr int kCh = 8 * kGroups;      // channels per block
+    constexpr int kSteps = kIters / 2;    // load instructions per wave, tile and group
     const int c0 = blockIdx.x * kCh;
     const int m = lane & 15;
-    const int part_k = (m / kCh) * (kIn / kSplit);  // first k of this lane's K part
     const int group = lane >> 4;
+    // k of this lane's 16 bytes in load step i (weights and activations alike)
+    auto lane_k = [&](int i) { return wave * (kIn / kWaves) + 128 * i + 64 * (m / 8) + 16 * group; };
     constexpr int kChunks = kIn / 8;  // 16-byte chunks per row
 
     // 0. With the RMSNorm prologue the session rows are needed before any
@@ -489,26 +496,32 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. weights of this wave's K slice, loaded straight in the MFMA operand
-    //    layout: lane (m, g) takes 16 bytes of channel row m at k = 64 i +
-    //    16 g, which feed two MFMAs (bytes 0-7 and 8-15; the activations use
-    //    the same k order, so the sum covers every k once).
-    int4 wq[kTiles][kSteps];
+    //    layout: lane (m, g) takes 16 bytes of channel row m % kCh at
+    //    lane_k(i), which feed two MFMAs (bytes 0-7 and 8-15; the activations
+    //    use the same k order, so the sum covers every k once).
+    //    Issued in the order the MFMA loop consumes them (memory returns in
+    //    order), so the conversions and MFMAs of the first steps run while the
+    //    later weights are still streaming in.
+    int4 wq[kTiles][kGroups][kSteps];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
+    for (int i = 0; i < kSteps; ++i) {
 #pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            const int ch = c0 + m % kCh;
-            const int row = (t == 0 ? 0 : a.out_features) + (ch < a.out_features ? ch : 0);
-            const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + part_k + wave * (kIn / kSplit / kWaves) +
-                                64 * i + 16 * group;
-            wq[t][i] = stream_load(reinterpret_cast<const int4*>(src));
+        for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+            for (int q = 0; q < kGroups; ++q) {
+                const int ch = c0 + 8 * q + m % 8;
+                const int row = (t == 0 ? 0 : a.out_features) + (ch < a.out_features ? ch : 0);
+                const int8_t* src = a.weight + static_cast<size_t>(row) * kIn + lane_k(i);
+                wq[t][q][i] = stream_load(reinterpret_cast<const int4*>(src));
+            }
         }
     }
     // epilogue operands of this thread's (channel, session) output
-    const int out_row = threadIdx.x >> 4;
-    const int out_col = threadIdx.x & 15;
+    static_assert(kCh <= kBlock / 8, "one thread per (channel, session) output");
+    const int out_row = threadIdx.x >> 3;
+    const int out_col = threadIdx.x & 7;
     const int out_ch = c0 + out_row;
-    const bool writes = threadIdx.x < 16 * kCh && out_col < rows && out_ch < a.out_features;
+    const bool writes = out_row < kCh && out_col < rows && out_ch < a.out_features;
     GemvArgs out_args = a;
     out_args.out16 = a.out16 ? a.out16 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
     out_args.out32 = a.out32 ? a.out32 + static_cast<size_t>(writes ? out_col : 0) * a.out_features : nullptr;
@@ -598,15 +611,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
         __syncthreads();
     }
 
-    // 3. MFMAs: columns m < rows are sessions, the rest zero
-    const bool real_col = m % kCh < rows;
-    const bf16_t* xrow = xs + (real_col ? m % kCh : 0) * kStride + part_k;
-    floatx4_t acc[kTiles];
+    // 3. MFMAs: columns m % 8 < rows are sessions, the rest zero
+    const bool real_col = m % 8 < rows;
+    const bf16_t* xrow = xs + (real_col ? m % 8 : 0) * kStride;
+    floatx4_t acc[kTiles][kGroups];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q) acc[t][q] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < kSteps; ++i) {
-        const int k = wave * (kIn / kSplit / kWaves) + 64 * i + 16 * group;
+        const int k = lane_k(i);
         bf16x8_t b0 = {}, b1 = {};
         if (real_col) {
             b0 = load_bf16x8(xrow + k);
@@ -614,29 +629,36 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) {
-            const bf16x8_t a0 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t][i].x), static_cast<uint32_t>(wq[t][i].y));
-            const bf16x8_t a1 = bytes_to_bf16x8(static_cast<uint32_t>(wq[t][i].z), static_cast<uint32_t>(wq[t][i].w));
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kGroups; ++q) {
+                const int4 w = wq[t][q][i];
+                const bf16x8_t a0 = bytes_to_bf16x8(static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y));
+                const bf16x8_t a1 = bytes_to_bf16x8(static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w));
+                acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[t][q], 0, 0, 0);
+                acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[t][q], 0, 0, 0);
+            }
         }
     }
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fold[wave][t][4 * group + j][m] = acc[t][j];  // [channel][session]
+        for (int q = 0; q < kGroups; ++q) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fold[wave][t][q][4 * group + j][m] = acc[t][q][j];  // [channel][session]
+        }
     }
     __syncthreads();
     if (writes) {
+        const int q = out_row / 8;
+        const int r = out_row % 8;
         float value[kTiles];
 #pragma unroll
         for (int t = 0; t < kTiles; ++t) {
-            float v = fold[0][t][out_row][out_col];
+            float v = fold[0][t][q][r][out_col];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) v += fold[w][t][out_row][out_col];
-            if constexpr (kSplit == 2) {
+            for (int w = 1; w < kWaves; ++w) v += fold[w][t][q][r][out_col];
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) v += fold[w][t][out_row + kCh][out_col + kCh];
-            }
+            for (int w = 0; w < kWaves; ++w) v += fold[w][t][q][r + 8][out_col + 8];
             value[t] = v;
         }
         if constexpr (kSilu) {
@@ -647,17 +669,17 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_mfma_fixed(GemvArgs a) {
     }
 }
 
-template <int kIters, int kWaves, int kEpi, bool kNorm, int kSplit>
+template <int kIters, int kWaves, int kEpi, bool kNorm, int kGroups>
 hipError_t launch_mfma_fixed(const GemvArgs& a, hipStream_t s) {
     constexpr int kIn = 64 * kWaves * kIters;
-    constexpr int kCh = 16 / kSplit;
+    constexpr int kCh = 8 * kGroups;
     const size_t lds = static_cast<size_t>(a.rows) * (kIn + 8) * sizeof(bf16_t);
     static std::atomic<unsigned long long> configured{0};
     const hipError_t st = set_dynamic_lds_once(
-        configured, reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit>),
+        configured, reinterpret_cast<const void*>(gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kGroups>),
         static_cast<int>(8 * (kIn + 8) * sizeof(bf16_t)));
     if (st != hipSuccess) return st;
-    gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kSplit><<<(a.out_features + kCh - 1) / kCh, 64 * kWaves, lds, s>>>(a);
+    gemv_mfma_fixed<kIters, kWaves, kEpi, kNorm, kGroups><<<(a.out_features + kCh - 1) / kCh, 64 * kWaves, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -741,18 +763,28 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
         if (a.in_features % 256 != 0 || (kNorm && a.in_features > 6144)) {
             return hipErrorInvalidValue;
         }
-        // 8-channel blocks (K halves on the tile's diagonal blocks) where
-        // 16-channel blocks would leave CUs idle; with the RMSNorm prologue
-        // every block stages and normalizes all rows, which only pays off
-        // for the wide fused gate/up (measured on MI355X, rows 2..8).
-        constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
-        const bool split = kNorm ? (kSilu && a.in_features >= 2048) : a.out_features / 16 < 256;
+        // Groups of 8 channels per block: as many as still leave a block for
+        // every CU (each block stages -- and with the RMSNorm prologue
+        // normalizes -- all session rows once for its groups).
+        const int groups = (a.out_features + 7) / 8;
+        const int cus = device_cu_count();
+        const int per = a.out_features % 8 != 0 ? 1 : groups % 3 == 0 && groups / 3 >= cus ? 3
+                                                    : groups % 2 == 0 && groups / 2 >= cus ? 2 : 1;
+        auto launch = [&](auto iters, auto waves) {
+            constexpr int kI = decltype(iters)::value, kW = decltype(waves)::value;
+            return per == 3 ? launch_mfma_fixed<kI, kW, kEpi, kNorm, 3>(a, s)
+                 : per == 2 ? launch_mfma_fixed<kI, kW, kEpi, kNorm, 2>(a, s)
+                            : launch_mfma_fixed<kI, kW, kEpi, kNorm, 1>(a, s);
+        };
+        using I4 = std::integral_constant<int, 4>;
+        using W4 = std::integral_constant<int, 4>;
+        using W8 = std::integral_constant<int, 8>;
         switch (a.in_features) {
             // kIters = K / (64 * waves); 8 waves where K is long
-            case 1024: return split ? launch_mfma_fixed<4, 4, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<4, 4, kEpi, kNorm, 1>(a, s);
-            case 2048: return split ? launch_mfma_fixed<8, 4, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<8, 4, kEpi, kNorm, 1>(a, s);
-            case 3072: return split ? launch_mfma_fixed<6, 8, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<6, 8, kEpi, kNorm, 1>(a, s);
-            case 6144: return split ? launch_mfma_fixed<12, 8, kEpi, kNorm, 2>(a, s) : launch_mfma_fixed<12, 8, kEpi, kNorm, 1>(a, s);
+            case 1024: return launch(I4{}, W4{});
+            case 2048: return launch(std::integral_constant<int, 8>{}, W4{});
+            case 3072: return launch(std::integral_constant<int, 6>{}, W8{});
+            case 6144: return launch(std::integral_constant<int, 12>{}, W8{});
             default: break;
         }
         const int grid = (a.out_features + 15) / 16;
