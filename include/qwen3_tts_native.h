@@ -402,6 +402,16 @@ QWEN3_TTS_API int32_t qwen3_tts_op_attention(
     uint16_t* const* value_bases, const int32_t* positions, uint16_t* output, int32_t rows,
     int32_t query_heads, int32_t key_value_heads, int32_t head_dimension,
     int32_t max_sequence_length, void* stream, char* error, size_t error_capacity);
+/* The prefill's exact attention for prompts beyond the GEMM path
+ * (talker.cu:3035-3054): query rows r = 0..rows-1 against one shared, complete
+ * cache (key_cache and value_cache [capacity][key_value_heads*head_dimension]),
+ * row r attending to positions 0..positions[r]; causal_gqa_attention
+ * semantics when exact != 0. */
+QWEN3_TTS_API int32_t qwen3_tts_op_prompt_attention_v1(
+    int32_t exact, const uint16_t* query, int32_t query_stride, const uint16_t* key_cache,
+    const uint16_t* value_cache, const int32_t* positions, uint16_t* output, int32_t rows,
+    int32_t query_heads, int32_t key_value_heads, int32_t head_dimension, int32_t capacity,
+    void* stream, char* error, size_t error_capacity);
 /* qk_norm_rope_kv_append followed by attention, as one fused decode step:
  * qkv holds the raw fused q|k|v rows (row stride qkv_stride); query heads are
  * head-normalized and rotated, the key of position positions[row] is

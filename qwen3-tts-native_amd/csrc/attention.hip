@@ -247,6 +247,90 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     a.scores[(static_cast<size_t>(row) * a.query_heads + head) * a.capacity + p] = score;
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Prompt rows against one shared, complete key cache (the prefill's exact
+// attention for long prompts: queries already normalized and rotated):
+// grid (position blocks, kv heads, tiles of kRows rows), one wave, lane =
+// position.  The key row is loaded once for the kRows rows and kG query
+// heads of the tile (the per-row kernel loads it once per row and head).
+// Each score is exact_score's arithmetic: leaf t = q[t] k[t] + q[t+64]
+// k[t+64], here one bf16 dot2 on the pairs (q[t], q[t+64]) and (k[t],
+// k[t+64]) -- both products of bf16 values are exact in fp32, so the sum
+// rounds once, as the two fmas and the add do -- then the same tree
+// (s[t] += s[t + w], w = 32..1), evaluated as a stack over the leaves in
+// post-order (bit-reversed index order), so at most six partial sums are
+// live.  Scores are bit-identical to attention_scores_kernel's.
+template <int kG, int kRows>
+__global__ __launch_bounds__(kScoreLanes) void attention_scores_rows_kernel(AttnArgs a, int rows) {
+    const int r0 = blockIdx.z * kRows;
+    const int kvh = blockIdx.y;
+    const int p0 = blockIdx.x * kScoreLanes;
+    const int last = min(r0 + kRows, rows) - 1;
+    int longest = 0;
+    for (int r = r0; r <= last; ++r) longest = max(longest, row_length(a, r));
+    if (p0 >= longest) return;
+    __shared__ uint32_t q_pairs[kRows][kG][kDim / 2];  // (q[t], q[t + 64]) bf16 pairs
+    const int lane = threadIdx.x;
+    const int p = p0 + lane;
+    const int kv_width = a.key_value_heads * kDim;
+    const int prow = p < longest ? p : longest - 1;
+    const uint4* k4 = reinterpret_cast<const uint4*>(a.key_cache + static_cast<size_t>(prow) * kv_width +
+                                                     static_cast<size_t>(kvh) * kDim);
+    uint32_t kw[64];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const uint4 t = load_global16(k4 + v);
+        kw[4 * v + 0] = t.x;
+        kw[4 * v + 1] = t.y;
+        kw[4 * v + 2] = t.z;
+        kw[4 * v + 3] = t.w;
+    }
+    for (int i = lane; i < kRows * kG * (kDim / 2); i += kScoreLanes) {
+        const int r = i / (kG * (kDim / 2));
+        const int h = (i / (kDim / 2)) % kG;
+        const int t = i % (kDim / 2);
+        const int row = min(r0 + r, last);
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(a.query) + static_cast<size_t>(row) * a.query_stride +
+                            static_cast<size_t>(kvh * kG + h) * kDim;
+        q_pairs[r][h][t] = static_cast<uint32_t>(q[t]) | (static_cast<uint32_t>(q[t + 64]) << 16);
+    }
+    // key pairs (k[t], k[t + 64])
+    uint32_t kp[64];
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+        const uint32_t lo = kw[t >> 1], hi = kw[32 + (t >> 1)];
+        kp[t] = (t & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+    __syncthreads();
+    for (int r = 0; r < kRows && r0 + r <= last; ++r) {
+        const int row = r0 + r;
+        if (p >= row_length(a, row)) continue;
+#pragma unroll 1
+        for (int h = 0; h < kG; ++h) {
+            const uint32_t* qp = q_pairs[r][h];
+            float stack[6];
+#pragma unroll
+            for (int i = 0; i < 64; ++i) {
+                const int t = static_cast<int>(__builtin_bitreverse32(static_cast<unsigned>(i)) >> 26);
+                float v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp[t]),
+                                                          __builtin_bit_cast(bf16x2_t, kp[t]), 0.0f, false);
+#pragma unroll
+                for (int b = 0; b < 6; ++b) {
+                    if (((i >> b) & 1) == 0) break;
+                    v = stack[b] + v;  // earlier (left) subtree + this one
+                }
+                stack[__builtin_ctz(~static_cast<unsigned>(i)) < 6 ? __builtin_ctz(~static_cast<unsigned>(i)) : 0] = v;
+            }
+            a.scores[(static_cast<size_t>(row) * a.query_heads + kvh * kG + h) * a.capacity + p] =
+                round_bf(round_bf(stack[0]) * a.scale);
+        }
+    }
+}
+
+// Prompt rows per tile of attention_scores_rows_kernel.
+constexpr int kPromptTileRows = 8;
+
 // Row stride of the probability table in LDS: whole 64-position blocks plus
 // one (the exact normalizer's look-ahead block), 16-byte aligned, and offset
 // by four banks between query heads.
@@ -294,7 +378,6 @@ __device__ __forceinline__ float chain8(float acc, const uint4& w, const float* 
 // 8 positions of a group as a bf16 dot2 whose other product is 0 * (the
 // neighbouring value).  A product of two bf16 values is exact in fp32, so
 // the dot2 rounds once, like the fma (values past `live` are masked to 0).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, const float* p, int live) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -880,8 +963,15 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         attention_small_kernel<kExact, kG><<<dim3(a.key_value_heads, rows), kG * kDim, 0, stream>>>(a);
         return hipGetLastError();
     }
-    const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.query_heads, rows);
-    attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
+    if (kExact && a.key_bases == nullptr && a.q_norm == nullptr && rows >= 2 * kPromptTileRows) {
+        // many prompt rows on one complete cache: the key rows are shared
+        const dim3 grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.key_value_heads,
+                        (rows + kPromptTileRows - 1) / kPromptTileRows);
+        attention_scores_rows_kernel<kG, kPromptTileRows><<<grid, kScoreLanes, 0, stream>>>(a, rows);
+    } else {
+        const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.query_heads, rows);
+        attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
+    }
     attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
 }

@@ -454,6 +454,31 @@ hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride
                                     max_sequence_length, stream);
 }
 
+hipError_t launch_prompt_attention_op(bool exact, const bf16_t* query, int query_stride, const bf16_t* key_cache,
+                                      const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
+                                      int query_heads, int key_value_heads, int head_dimension, int capacity,
+                                      hipStream_t stream) {
+    if (key_cache == nullptr || value_cache == nullptr || positions == nullptr || rows <= 0 || query_heads <= 0 ||
+        key_value_heads <= 0 || capacity <= 0) {
+        return hipErrorInvalidValue;
+    }
+    void* workspace = nullptr;
+    hipError_t st = hipMallocAsync(&workspace, attention_workspace_bytes(rows, query_heads, capacity), stream);
+    if (st != hipSuccess) return st;
+    // the one shared cache, all of its positions, dimension-major
+    ValueTemporary values;
+    st = make_value_temporary(values, nullptr, value_cache, nullptr, capacity, 1, key_value_heads * head_dimension,
+                              capacity, stream);
+    if (st == hipSuccess) {
+        st = launch_attention(exact, query, query_stride, nullptr, nullptr, key_cache, values.values, positions, 0,
+                              output, rows, query_heads, key_value_heads, head_dimension, capacity,
+                              static_cast<float*>(workspace), nullptr, stream);
+    }
+    st = free_value_temporary(values, stream, st);
+    const hipError_t freed = hipFreeAsync(workspace, stream);
+    return st != hipSuccess ? st : freed;
+}
+
 // File-scope scratch of the allocation-free decode attention entry point:
 // each device holds its own copy for the life of the process.  In host code
 // the name is only a stand-in; the device address comes from

@@ -257,6 +257,12 @@ hipError_t launch_attention_op(bool exact, const bf16_t* query, int query_stride
                                bf16_t* const* value_bases, const int* positions, bf16_t* output, int rows,
                                int query_heads, int key_value_heads, int head_dimension, int max_sequence_length,
                                hipStream_t stream);
+// Prompt rows against one shared key/value cache ([capacity][kv_width] each,
+// complete): row r attends to positions 0..positions[r].
+hipError_t launch_prompt_attention_op(bool exact, const bf16_t* query, int query_stride, const bf16_t* key_cache,
+                                      const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
+                                      int query_heads, int key_value_heads, int head_dimension, int capacity,
+                                      hipStream_t stream);
 hipError_t launch_causal_gqa_attention(const bf16_t* query, const bf16_t* key_cache,
                                        const bf16_t* value_cache, bf16_t* output, int query_heads,
                                        int key_value_heads, int head_dimension,

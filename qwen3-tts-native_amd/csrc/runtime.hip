@@ -675,6 +675,16 @@ QWEN3_TTS_API int32_t qwen3_tts_op_attention(int32_t exact, const uint16_t* quer
                          "attention", error, cap);
 }
 
+QWEN3_TTS_API int32_t qwen3_tts_op_prompt_attention_v1(int32_t exact, const uint16_t* query, int32_t query_stride,
+                                                      const uint16_t* key_cache, const uint16_t* value_cache,
+                                                      const int32_t* positions, uint16_t* output, int32_t rows,
+                                                      int32_t qh, int32_t kvh, int32_t hd, int32_t capacity,
+                                                      void* stream, char* error, size_t cap) {
+    return launch_status(launch_prompt_attention_op(exact != 0, query, query_stride, key_cache, value_cache, positions,
+                                                    output, rows, qh, kvh, hd, capacity, as_stream(stream)),
+                         "prompt attention", error, cap);
+}
+
 QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention(int32_t exact, const uint16_t* qkv, int32_t qkv_stride,
                                                     const uint16_t* q_norm, const uint16_t* k_norm,
                                                     const uint16_t* rope_table, float epsilon,

@@ -202,6 +202,7 @@ SIGNATURES = {
     "qwen3_tts_rope_table_v1": (I32, [I32, I32, C.c_float, P] + ERR),
     "qwen3_tts_op_qk_norm_rope_kv_append": (I32, [P, P, P, P, P, P, P, I32, I32, I32, I32, C.c_float, P] + ERR),
     "qwen3_tts_op_attention": (I32, [I32, P, I32, P, P, P, P, I32, I32, I32, I32, I32, P] + ERR),
+    "qwen3_tts_op_prompt_attention_v1": (I32, [I32, P, I32, P, P, P, P, I32, I32, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_decode_attention": (I32, [I32, P, I32, P, P, P, C.c_float, P, P, P, P, I32, I32, I32, I32, I32, P]
                                       + ERR),
     "qwen3_tts_op_decode_attention_noalloc_v1": (I32, [I32, P, I32, P, P, P, C.c_float, P, P, P, P, I32, I32, I32,

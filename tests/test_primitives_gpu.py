@@ -179,6 +179,30 @@ def test_decode_attention_fused_matches_separate_ops(hip, orc, exact, qh, kvh, p
         assert np.array_equal(out_f[r], ref)
 
 
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("qh,kvh", [(16, 8), (8, 8), (16, 4)])
+@pytest.mark.parametrize("first,rows,capacity", [(0, 40, 64), (500, 24, 600), (0, 17, 17), (700, 101, 801)])
+def test_prompt_attention_shared_cache(hip, orc, exact, qh, kvh, first, rows, capacity):
+    """The prefill's exact attention for long prompts: consecutive prompt rows
+    against one complete cache (row r attends to positions 0..first + r), in
+    tiles of rows that share each key row; every row's output equals the
+    oracle's causal_gqa_attention of its prefix."""
+    rng = np.random.default_rng(first + rows + qh + kvh + exact)
+    d = 128
+    q = gen.activations(rng, rows, qh * d)
+    k = gen.bf16(rng.standard_normal((capacity, kvh * d)).astype(np.float32) * 0.5)
+    v = gen.activations(rng, capacity, kvh * d)
+    pos = np.arange(first, first + rows, dtype=np.int32)
+    out = hip.DeviceArray((rows, qh * d), np.uint16)
+    hip.call("qwen3_tts_op_prompt_attention_v1", exact, dev(hip, q).ptr, qh * d, dev(hip, k).ptr, dev(hip, v).ptr,
+             dev(hip, pos).ptr, out.ptr, rows, qh, kvh, d, capacity, None)
+    got = out.numpy()
+    for r in range(rows):
+        n = first + r + 1
+        ref = orc.attention(q[r], k[:n], v[:n], qh, kvh, d, n, exact=bool(exact))
+        assert np.array_equal(got[r], ref), r
+
+
 def test_attention_rows_with_own_caches(hip, orc):
     rng = np.random.default_rng(9)
     qh, kvh, d, max_seq, rows = 16, 8, 128, 64, 3
