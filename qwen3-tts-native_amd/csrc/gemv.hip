@@ -170,6 +170,77 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Exact-order rows 2..8 without the RMSNorm prologue, K = 512 * kVpl known at
+// compile time (the prompt's text projection, exact batched mode): the
+// batch-1 kernel's layout -- one unit per half-wave, its weights (the lane's
+// vectors lane + 32 i) requested first and held in registers -- against every
+// input row, staged once per block in LDS.  Per row the sum is the generic
+// kernel's: acc += chain16(vector i) for i in order, then fold32.
+// ---------------------------------------------------------------------------
+template <int kVpl, int kEpi>
+__global__ __launch_bounds__(kThreads) void gemv_exact_rows_fixed(GemvArgs a) {
+    constexpr bool kSilu = (kEpi == kEpiSiluFused || kEpi == kEpiSiluRounded);
+    constexpr int kTiles = kSilu ? 2 : 1;
+    constexpr int kIn = kVpl * 512;
+    constexpr int kChunks = kIn * 2 / 16;  // 16-byte chunks of one bf16 row
+    extern __shared__ __align__(16) uint4 rows_lds[];  // [rows][kChunks]
+    const int lane = threadIdx.x & 31;
+    const int rows = a.rows;
+    const int units = a.out_features;
+    const int unit = blockIdx.x * kHalfWaves + (threadIdx.x >> 5);
+    const int first = unit < units ? unit : units - 1;  // clamped: see gemv_exact_fixed
+    int4 w[kTiles][kVpl];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int row = t == 0 ? first : a.out_features + first;
+        const int4* base = reinterpret_cast<const int4*>(a.weight + static_cast<size_t>(row) * kIn);
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) w[t][i] = stream_load(base + lane + 32 * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the weight stream first, then the rows
+    const uint4* xin = reinterpret_cast<const uint4*>(a.input);
+    for (int c = threadIdx.x; c < rows * kChunks; c += kThreads) rows_lds[c] = xin[c];
+    __syncthreads();
+    for (int r = 0; r < rows; ++r) {
+        const bf16_t* xs = reinterpret_cast<const bf16_t*>(rows_lds + r * kChunks);
+        float acc[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kVpl; ++i) {
+            float xv[16];
+            load_x16<false>(xs, nullptr, lane + 32 * i, 1.0f, xv);
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) acc[t] += chain16(w[t][i], xv);
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = fold32(acc[t]);
+        if (lane == 0 && unit < units) {
+            GemvArgs row = a;
+            row.out16 = a.out16 ? a.out16 + static_cast<size_t>(r) * a.out_features : nullptr;
+            row.out32 = a.out32 ? a.out32 + static_cast<size_t>(r) * a.out_features : nullptr;
+            if constexpr (kSilu) {
+                store_gate_up<kEpi>(row, unit, acc[0], acc[kTiles - 1]);
+            } else {
+                store_channel<kEpi>(row, unit, acc[0]);
+            }
+        }
+    }
+}
+
+template <int kVpl, int kEpi>
+hipError_t launch_exact_rows_fixed(const GemvArgs& a, hipStream_t s) {
+    constexpr int kIn = kVpl * 512;
+    static std::atomic<unsigned long long> configured{0};
+    const hipError_t st = set_dynamic_lds_once(configured, reinterpret_cast<const void*>(gemv_exact_rows_fixed<kVpl, kEpi>),
+                                               static_cast<int>(8 * kIn * sizeof(bf16_t)));
+    if (st != hipSuccess) return st;
+    const size_t lds = static_cast<size_t>(a.rows) * kIn * sizeof(bf16_t);
+    gemv_exact_rows_fixed<kVpl, kEpi><<<(a.out_features + kHalfWaves - 1) / kHalfWaves, kThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Exact-order GEMV/GEMM for any in_features % 16 == 0 and rows 1..8.  The
 // activation vectors are re-read per weight vector (they stay in L1/L2).
 // ---------------------------------------------------------------------------
@@ -798,6 +869,18 @@ hipError_t dispatch(const GemvArgs& a, hipStream_t s) {
         if (vpl == 2 || vpl == 4 || vpl == 6 || vpl == 12) {
             const int grid = (a.out_features + kHalfWaves - 1) / kHalfWaves;
             return dispatch_fixed<kEpi, kNorm>(a, vpl, grid, s);
+        }
+    }
+    if constexpr (!kNorm) {
+        // several exact rows on a production width: weights once per unit
+        if (a.rows > 1 && a.input_row_index == nullptr) {
+            switch (a.in_features) {
+                case 1024: return launch_exact_rows_fixed<2, kEpi>(a, s);
+                case 2048: return launch_exact_rows_fixed<4, kEpi>(a, s);
+                case 3072: return launch_exact_rows_fixed<6, kEpi>(a, s);
+                case 6144: return launch_exact_rows_fixed<12, kEpi>(a, s);
+                default: break;
+            }
         }
     }
     const int generic_units = a.out_features;

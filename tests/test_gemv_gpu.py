@@ -42,8 +42,9 @@ def test_exact_rows1_bit_identical(hip, orc, out_f, in_f):
     assert np.array_equal(y16.numpy(), ref16)
 
 
+# toy widths take the generic kernel; 1024/2048/3072/6144 the fixed-K rows kernel
 @pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
-@pytest.mark.parametrize("out_f,in_f", [(64, 256), (130, 512), (2048, 6144)])
+@pytest.mark.parametrize("out_f,in_f", [(64, 256), (130, 512), (1000, 1024), (2048, 2048), (301, 3072), (2048, 6144)])
 def test_exact_rows_bit_identical(hip, orc, rows, out_f, in_f):
     rng = np.random.default_rng(rows * 1000 + out_f)
     w, s, x = gen.weights(rng, out_f, in_f), gen.scales(rng, out_f), gen.activations(rng, rows, in_f)
