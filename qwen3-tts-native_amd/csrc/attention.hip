@@ -306,7 +306,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_rows_kernel(Attn
     for (int r = 0; r < kRows && r0 + r <= last; ++r) {
         const int row = r0 + r;
         if (p >= row_length(a, row)) continue;
-#pragma unroll 1
+#pragma unroll
         for (int h = 0; h < kG; ++h) {
             const uint32_t* qp = q_pairs[r][h];
             float stack[6];
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_rows_kernel(Attn
 }
 
 // Prompt rows per tile of attention_scores_rows_kernel.
-constexpr int kPromptTileRows = 8;
+constexpr int kPromptTileRows = 4;
 
 // Row stride of the probability table in LDS: whole 64-position blocks plus
 // one (the exact normalizer's look-ahead block), 16-byte aligned, and offset
