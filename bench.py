@@ -224,6 +224,10 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
     then `frames` codec frames with top-k 50 / T 0.9 from a fixed seed.  The
     prompt fills the KV cache so that the timed frames run at context
     max_seq - frames .. max_seq (attention reads up to 1024 positions).
+    An end token sampled on the way (random weights) ends the session: it is
+    reset and prefilled again outside the timing, so every run times the same
+    number of frames (each frame is timed on the host: the call returns its
+    codes).
     Before the timed frames, `greedy` frames run the code predictor with
     greedy argmax (config 3: the 15-step predictor chain); its GPU time per
     frame is reported separately (it covers 16 passes through the 5 layers:
@@ -257,29 +261,38 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
             pred_ms = talk_ms = 0.0
             greedy_ms = []
             eos = 0
-            t_start = None
             greedy_ps = hip.sampling(0, 0, 1.0, 1.0, 1.0)
+            timed = 0.0
+            seeds = iter(range(100, 1000))
+
+            def restart():
+                # random weights: the end token can come up and end the
+                # session; it is reset and prefilled again outside the timing
+                hip.call("qwen3_tts_session_reset", session, next(seeds))
+                again = hip.PrefillResult()
+                hip.call("qwen3_tts_session_prefill", session, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                         codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(again))
+                hip.synchronize()
+                return C.c_uint16(again.first_semantic_token)
+
             for f in range(frames + warm + greedy):
-                if f == warm + greedy:
-                    hip.synchronize()
-                    t_start = time.perf_counter()
-                if semantic.value == cfg.codec_eos_token:
+                while semantic.value == cfg.codec_eos_token:
                     eos += 1
-                    break
+                    semantic = restart()
                 chain = warm <= f < warm + greedy
+                t0 = time.perf_counter()
                 hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts,
                          greedy_ps if chain else ps, codes, 16, C.byref(nxt), C.byref(info))
+                dt = time.perf_counter() - t0  # the frame returns its codes on the host: synchronous
                 semantic = C.c_uint16(nxt.value)
                 if chain:
                     greedy_ms.append(info.predictor_gpu_milliseconds)
                 if f >= warm + greedy:
+                    timed += dt
                     done += 1
                     pred_ms += info.predictor_gpu_milliseconds
                     talk_ms += info.talker_gpu_milliseconds
-            if t_start is None:
-                raise RuntimeError("the session sampled the end token before the timed frames")
-            wall = time.perf_counter() - t_start
-            frame_ms = wall * 1000.0 / max(done, 1)
+            frame_ms = timed * 1000.0 / max(done, 1)
             return {
                 "frames": done, "prompt_tokens": prompt, "max_sequence_length": max_seq,
                 "frames_per_second": round(1000.0 / frame_ms, 2),
@@ -288,7 +301,7 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
                 "predictor_gpu_ms_per_frame": round(pred_ms / max(done, 1), 3),
                 "talker_gpu_ms_per_frame": round(talk_ms / max(done, 1), 3),
                 "prefill_seconds": round(prefill_s, 3),
-                "ended_by_eos_early": bool(eos),
+                "sessions_restarted_after_end_token": eos,
                 "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9; seed 42",
                 "predictor_chain_config3": predictor_chain_entry(greedy_ms),
             }
