@@ -47,7 +47,11 @@ __device__ __forceinline__ uint4 load_chunk(const bf16_t* base, int ld, int row,
 // (kBM/32) x (kBN/32) 16x16 MFMA tiles.
 // gridDim.z = batch * splits: slice `split` covers K steps
 // [split * steps_per_split, ...) and writes fp32 partial sums when splits > 1.
-template <int kBM, int kBN, int kBK>
+// kDeep: two register sets of global loads, so the loads of steps s + 1 and
+// s + 2 are in flight while step s runs its MFMAs (each step otherwise waits
+// one memory latency); beyond the slice the loads still issue (masked past
+// the matrix, unused) so that every wait counts the same loads.
+template <int kBM, int kBN, int kBK, bool kDeep = false>
 __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g, int splits, int steps_per_split) {
     constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row: 16-byte pad against bank conflicts
     constexpr int kRowChunks = kBK / 8;  // 16-byte chunks per row and K step
@@ -55,6 +59,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
     constexpr int kTN = kBN / 32;                 // and along N
     constexpr int kChunksA = kBM * kRowChunks / kGemmThreads;  // 16-byte chunks per thread per K step
     constexpr int kChunksB = kBN * kRowChunks / kGemmThreads;
+    constexpr int kSets = kDeep ? 2 : 1;
     __shared__ __align__(16) bf16_t as[2][kBM * kLdsRow];
     __shared__ __align__(16) bf16_t bs[2][kBN * kLdsRow];
     const int tid = threadIdx.x;
@@ -68,29 +73,31 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
     const bf16_t* b = g.b + static_cast<size_t>(z / g.b_group) * g.b_batch;
     bf16_t* c = g.c + static_cast<size_t>(z) * g.c_batch;
 
-    uint4 ra[kChunksA], rb[kChunksB];
-    auto fetch = [&](int k0) {
+    uint4 ra[kSets][kChunksA], rb[kSets][kChunksB];
+    auto fetch = [&](int set, int k0) {
 #pragma unroll
         for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            ra[i] = load_chunk(a, g.lda, m0 + chunk / kRowChunks, g.m, k0 + (chunk % kRowChunks) * 8, g.k);
+            ra[set][i] = load_chunk(a, g.lda, m0 + chunk / kRowChunks, g.m, k0 + (chunk % kRowChunks) * 8, g.k);
         }
 #pragma unroll
         for (int i = 0; i < kChunksB; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            rb[i] = load_chunk(b, g.ldb, n0 + chunk / kRowChunks, g.n, k0 + (chunk % kRowChunks) * 8, g.k);
+            rb[set][i] = load_chunk(b, g.ldb, n0 + chunk / kRowChunks, g.n, k0 + (chunk % kRowChunks) * 8, g.k);
         }
     };
-    auto stage = [&](int buffer) {
+    auto stage = [&](int set, int buffer) {
 #pragma unroll
         for (int i = 0; i < kChunksA; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            *reinterpret_cast<uint4*>(&as[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) = ra[i];
+            *reinterpret_cast<uint4*>(&as[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) =
+                ra[set][i];
         }
 #pragma unroll
         for (int i = 0; i < kChunksB; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            *reinterpret_cast<uint4*>(&bs[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) = rb[i];
+            *reinterpret_cast<uint4*>(&bs[buffer][(chunk / kRowChunks) * kLdsRow + (chunk % kRowChunks) * 8]) =
+                rb[set][i];
         }
     };
 
@@ -103,16 +110,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
     for (int i = 0; i < kTM; ++i)
 #pragma unroll
         for (int j = 0; j < kTN; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-
-    const int first = split * steps_per_split;
-    const int steps = min((g.k + kBK - 1) / kBK - first, steps_per_split);
-    const int k_base = first * kBK;
-    fetch(k_base);
-    stage(0);
-    __syncthreads();
-    for (int s = 0; s < steps; ++s) {
-        const int buffer = s & 1;
-        if (s + 1 < steps) fetch(k_base + (s + 1) * kBK);  // in flight under the MFMAs
+    auto compute = [&](int buffer) {
 #pragma unroll
         for (int kk = 0; kk < kBK; kk += 32) {
             bf16x8_t af[kTM], bfr[kTN];
@@ -129,9 +127,43 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
 #pragma unroll
                 for (int j = 0; j < kTN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < steps) {
-            stage(buffer ^ 1);
+    };
+
+    const int first = split * steps_per_split;
+    const int steps = min((g.k + kBK - 1) / kBK - first, steps_per_split);
+    const int k_base = first * kBK;
+    if constexpr (kDeep) {
+        // step j's loads live in set (j + 1) % 2 after the prologue: step 0
+        // staged from set 0, then step 1 in set 1 and step 2 in set 0
+        fetch(0, k_base);
+        stage(0, 0);
+        fetch(1, k_base + kBK);
+        fetch(0, k_base + 2 * kBK);
+        __syncthreads();
+        for (int s = 0; s < steps; s += 2) {
+            compute(0);  // step s
+            if (s + 1 >= steps) break;
+            stage(1, 1);  // step s + 1
+            fetch(1, k_base + (s + 3) * kBK);
             __syncthreads();
+            compute(1);  // step s + 1
+            if (s + 2 >= steps) break;
+            stage(0, 0);  // step s + 2
+            fetch(0, k_base + (s + 4) * kBK);
+            __syncthreads();
+        }
+    } else {
+        fetch(0, k_base);
+        stage(0, 0);
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            const int buffer = s & 1;
+            if (s + 1 < steps) fetch(0, k_base + (s + 1) * kBK);  // in flight under the MFMAs
+            compute(buffer);
+            if (s + 1 < steps) {
+                stage(0, buffer ^ 1);
+                __syncthreads();
+            }
         }
     }
     // acc[i][j][r] = C[wm + 16 i + 4 group + r][wn + 16 j + m]
@@ -306,18 +338,27 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);
     if ((align & 15u) != 0 || (g.a_batch % 8) != 0 || (g.b_batch % 8) != 0) return hipErrorInvalidValue;
-    // Tiles and K steps (measured on MI355X over the prefill's shapes, 16..801
-    // rows): 128-square only where it still gives two workgroups per CU,
-    // else 64-square for more than 128 rows and 32-square below; K steps of
-    // 256 / 128 / 64 -- each step waits one memory latency, so short prompts
-    // want long steps, but a 256-step 32-square tile holds 66 KB of LDS (two
-    // workgroups per CU), which costs more than it saves from 65 rows on.
+    // Tiles, K steps and K slices, measured on MI355X over the prefill's
+    // shapes (prompts of 16..801 rows, N 1024..6144, K 2048 / 6144): 128-square
+    // only where it still gives two workgroups per CU; else 32-square up to
+    // 256 rows (K steps of 256 up to 64 rows, else 128: the 256-step tile's
+    // 66 KB of LDS halves occupancy), 64-square above (K steps of 128 up to
+    // 2048 columns, else 64).  Each K step waits one memory latency, so deep
+    // products (K >= 4096) split K into slices (4 for the 32-square tile, 8
+    // for the 64-square one up to 256 rows, 2 above while the grid has under
+    // 384 workgroups), and a 32-square grid of
+    // under 128 workgroups spreads to about 512 (two steps a slice at least).
     auto blocks = [&](int t) { return static_cast<long long>((g.n + t - 1) / t) * ((g.m + t - 1) / t) * g.batch; };
+    const bool deep = g.k >= 4096;
     int tile = g.force_tile;
-    if (tile == 0) tile = blocks(128) >= 512 ? 128 : g.m > 128 ? 64 : 32;
+    if (tile == 0) tile = blocks(128) >= 512 ? 128 : (g.m <= 128 || (g.m <= 256 && !deep)) ? 32 : 64;
     if (tile != 32 && tile != 64 && tile != 128) return hipErrorInvalidValue;
     int bk = g.force_k_step;
-    if (bk == 0) bk = tile == 32 ? (g.m <= 64 ? 256 : 128) : tile == 64 ? 128 : 64;
+    if (bk == 0) {
+        if (tile == 32) bk = g.m <= 64 ? 256 : 128;
+        else if (tile == 64) bk = (g.n >= 3072 || (deep && g.m <= 256)) ? 64 : 128;
+        else bk = 64;
+    }
     if (!((tile == 32 && (bk == 64 || bk == 128 || bk == 256)) || (tile == 64 && (bk == 64 || bk == 128)) ||
           (tile == 128 && bk == 64))) {
         return hipErrorInvalidValue;
@@ -325,19 +366,14 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     const int steps = (g.k + bk - 1) / bk;
     int splits = g.force_splits;
     if (splits == 0) {
-        // K slices (with a workspace): the 32-square tile keeps a slice to
-        // 2048 K and spreads a grid of under 128 workgroups to about 512 (two
-        // steps a slice at least); the larger tiles split a grid of under 384
-        // workgroups toward 512, a slice keeping 12 steps at least
         const long long tiles = blocks(tile);
         if (tile == 32) {
-            splits = (g.k + 2047) / 2048;
+            splits = deep ? 4 : 1;
             if (tiles < 128) {
                 splits = std::max<long long>(splits, std::min<long long>((512 + tiles - 1) / tiles, steps / 2));
             }
         } else {
-            splits = tiles < 384 ? static_cast<int>(std::min<long long>((512 + tiles - 1) / tiles, (steps + 11) / 12))
-                                 : 1;
+            splits = deep ? (g.m <= 256 ? 8 : tiles < 384 ? 2 : 1) : 1;
         }
     }
     splits = std::max(1, std::min(splits, steps));
@@ -354,12 +390,12 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     if (tile == 128) {
         gemm_bf16_kernel<128, 128, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
     } else if (tile == 64) {
-        if (bk == 128) gemm_bf16_kernel<64, 64, 128><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
-        else gemm_bf16_kernel<64, 64, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        if (bk == 128) gemm_bf16_kernel<64, 64, 128, true><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else gemm_bf16_kernel<64, 64, 64, true><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
     } else {
-        if (bk == 256) gemm_bf16_kernel<32, 32, 256><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
-        else if (bk == 128) gemm_bf16_kernel<32, 32, 128><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
-        else gemm_bf16_kernel<32, 32, 64><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        if (bk == 256) gemm_bf16_kernel<32, 32, 256, true><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else if (bk == 128) gemm_bf16_kernel<32, 32, 128, true><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
+        else gemm_bf16_kernel<32, 32, 64, true><<<grid, kGemmThreads, 0, stream>>>(g, splits, per);
     }
     if (splits > 1) {
         const hipError_t e = hipGetLastError();
