@@ -459,12 +459,15 @@ QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_v1(
  * (planned) or 64/128/256 (32 tile), 64/128 (64 tile), 64 (128 tile), and
  * splits 0 (planned) or a K slice count,
  * bounded by the workspace (splits * batch * m * n floats).  The slices' sums
- * are added in slice order.  The prefill uses the planned form. */
+ * are added in slice order.  epilogue 0 stores bf16(sum); 1 adds it into C
+ * as add_in_place does after a GEMM (C = bf16(C + bf16(sum))); 2 applies
+ * silu_gate with C holding the gate product (C = bf16(bf16(silu(C)) *
+ * bf16(sum))).  The prefill uses the planned form. */
 QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_split_v1(
     const uint16_t* a, const uint16_t* b, uint16_t* c, int32_t m, int32_t n, int32_t k, int32_t lda,
     int32_t ldb, int32_t ldc, int32_t batch, int32_t b_group, int64_t a_batch, int64_t b_batch,
     int64_t c_batch, float* partial, uint64_t partial_floats, int32_t tile, int32_t k_step, int32_t splits,
-    void* stream, char* error, size_t error_capacity);
+    int32_t epilogue, void* stream, char* error, size_t error_capacity);
 /* causal_softmax_kernel (talker_kernels.cu:232-260) on bf16 scores
  * [heads][rows][stride], in place; keys past the query (up to stride) are set
  * to 0.  rows <= 512. */

@@ -43,6 +43,23 @@ __device__ __forceinline__ uint4 load_chunk(const bf16_t* base, int ld, int row,
     return v;
 }
 
+// The product's bf16 value v = bf16(sum) into C, as the epilogue says: kept
+// (store), added into C as the reference's add_in_place after the GEMM
+// (C = bf16(C + v)), or as its silu_gate with C holding the gate GEMM's
+// output and v the up GEMM's (C = bf16(bf16(g / (1 + exp(-g))) * v)).
+__device__ __forceinline__ void gemm_store(bf16_t* out, float sum, int epilogue) {
+    const bf16_t v = f2bf(sum);
+    if (epilogue == kGemmAddInto) {
+        *out = f2bf(bf2f(*out) + bf2f(v));
+    } else if (epilogue == kGemmSiluGateInto) {
+        const float g = bf2f(*out);
+        const float activated = round_bf(g / (1.0f + q3_expf(-g)));
+        *out = f2bf(activated * bf2f(v));
+    } else {
+        *out = v;
+    }
+}
+
 // Block tile kBM x kBN, four waves in 2 x 2, each (kBM/2) x (kBN/2) as
 // (kBM/32) x (kBN/32) 16x16 MFMA tiles.
 // gridDim.z = batch * splits: slice `split` covers K steps
@@ -193,7 +210,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
 #pragma unroll
             for (int j = 0; j < kTN; ++j) {
                 const int col = n0 + wn + 16 * j + m;
-                if (col < g.n) c[static_cast<size_t>(row) * g.ldc + col] = f2bf(acc[i][j][r]);
+                if (col < g.n) gemm_store(c + static_cast<size_t>(row) * g.ldc + col, acc[i][j][r], g.epilogue);
             }
         }
     }
@@ -211,7 +228,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_reduce_kernel(Bf16GemmArgs g, i
     const float* p = g.partial + (static_cast<size_t>(z) * g.m + row) * g.n + col;
     float sum = p[0];
     for (int s = 1; s < splits; ++s) sum += p[s * slice];
-    g.c[static_cast<size_t>(z) * g.c_batch + static_cast<size_t>(row) * g.ldc + col] = f2bf(sum);
+    gemm_store(g.c + static_cast<size_t>(z) * g.c_batch + static_cast<size_t>(row) * g.ldc + col, sum, g.epilogue);
 }
 
 // causal_softmax_kernel (talker_kernels.cu:232-260) on bf16 scores
@@ -334,6 +351,9 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
     if (g.a == nullptr || g.b == nullptr || g.c == nullptr || g.m <= 0 || g.n <= 0 || g.k <= 0 || g.batch <= 0 ||
         g.b_group <= 0 || g.k % 8 != 0 || g.lda % 8 != 0 || g.ldb % 8 != 0 || g.lda < g.k || g.ldb < g.k ||
         g.ldc < g.n) {
+        return hipErrorInvalidValue;
+    }
+    if (g.epilogue != kGemmStore && g.epilogue != kGemmAddInto && g.epilogue != kGemmSiluGateInto) {
         return hipErrorInvalidValue;
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);

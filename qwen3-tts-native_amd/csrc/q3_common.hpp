@@ -356,6 +356,11 @@ hipError_t launch_sum_embeddings(const bf16_t* const* tables, int count, int voc
 // row-major with leading dimensions lda, ldb, ldc (elements).  Batch z uses
 // A + z * a_batch, B + (z / b_group) * b_batch, C + z * c_batch.  K, lda,
 // ldb, a_batch and b_batch must be multiples of 8 and A, B 16-byte aligned.
+// Epilogues of the bf16 GEMM: C = bf16(sum); C = bf16(C + bf16(sum)) (the
+// residual add_in_place); C = bf16(bf16(silu(C)) * bf16(sum)) (silu_gate with
+// C holding the gate product).
+enum Bf16GemmEpilogue : int { kGemmStore = 0, kGemmAddInto = 1, kGemmSiluGateInto = 2 };
+
 struct Bf16GemmArgs {
     const bf16_t* a = nullptr;
     const bf16_t* b = nullptr;
@@ -373,6 +378,7 @@ struct Bf16GemmArgs {
     int force_tile = 0;    // 0: planned; else 32, 64 or 128
     int force_k_step = 0;  // 0: planned; else K per pipeline step (32 tile: 64/128/256; 64: 64/128; 128: 64)
     int force_splits = 0;  // 0: planned; else the K slices (bounded by the workspace)
+    int epilogue = kGemmStore;
 };
 hipError_t launch_bf16_gemm(const Bf16GemmArgs& args, hipStream_t stream);
 // Prompts of at most this many positions run the reference's GEMM attention

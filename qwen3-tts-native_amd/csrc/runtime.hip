@@ -746,8 +746,8 @@ QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_split_v1(const uint16_t* a, const u
                                                       int32_t n, int32_t k, int32_t lda, int32_t ldb, int32_t ldc,
                                                       int32_t batch, int32_t b_group, int64_t a_batch, int64_t b_batch,
                                                       int64_t c_batch, float* partial, uint64_t partial_floats,
-                                                      int32_t tile, int32_t k_step, int32_t splits, void* stream,
-                                                      char* error, size_t cap) {
+                                                      int32_t tile, int32_t k_step, int32_t splits, int32_t epilogue,
+                                                      void* stream, char* error, size_t cap) {
     if (tile < 0 || k_step < 0 || splits < 0 || (partial == nullptr && partial_floats != 0)) {
         write_error(error, cap, "bf16 GEMM: negative tile, K step or split count, or a workspace size without a workspace");
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
@@ -772,6 +772,7 @@ QWEN3_TTS_API int32_t qwen3_tts_op_bf16_gemm_split_v1(const uint16_t* a, const u
     g.force_tile = tile;
     g.force_k_step = k_step;
     g.force_splits = splits;
+    g.epilogue = epilogue;
     return launch_status(launch_bf16_gemm(g, as_stream(stream)), "bf16 GEMM (split)", error, cap);
 }
 

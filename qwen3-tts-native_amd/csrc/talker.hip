@@ -733,8 +733,9 @@ public:
         check_hip(launch_prompt_rows(hidden, text_ids, codec_ids, m_.codec_embedding_, cfg_.talker_vocab, rows, H, stream_),
                   "prompt rows");
         auto gemm = [&](const bf16_t* a, int lda, const bf16_t* weight, bf16_t* c, int ldc, int n, int k,
-                        const char* what) {
+                        const char* what, int epilogue = kGemmStore) {
             Bf16GemmArgs g;
+            g.epilogue = epilogue;
             g.a = a;
             g.b = weight;
             g.c = c;
@@ -751,9 +752,7 @@ public:
         bf16_t* xn = w.normalized.as<bf16_t>();
         bf16_t* qkv = w.qkv.as<bf16_t>();
         bf16_t* attn = w.attn.as<bf16_t>();
-        bf16_t* proj = w.proj.as<bf16_t>();
         bf16_t* gate = w.gate.as<bf16_t>();
-        bf16_t* up = w.up.as<bf16_t>();
         const int vstride = value_cache_stride(max_seq_);
         for (int l = 0; l < T.layers; ++l) {
             const Layer& L = m_.talker_layers_[l];
@@ -820,14 +819,13 @@ public:
                               "prefill exact attention");
                 }
             }
-            gemm(attn, qw, L.o16, proj, H, H, qw, "prefill O GEMM");
-            check_hip(launch_add_in_place(hidden, proj, rows * H, stream_), "prefill attention residual");
+            // O GEMM with the residual add (add_in_place) as its epilogue
+            gemm(attn, qw, L.o16, hidden, H, H, qw, "prefill O GEMM + residual", kGemmAddInto);
             check_hip(launch_rms_norm_rows(hidden, L.post_norm, xn, rows, H, cfg_.eps, stream_), "prefill post norm");
             gemm(xn, H, L.gate16, gate, I, I, H, "prefill gate GEMM");
-            gemm(xn, H, L.up16, up, I, I, H, "prefill up GEMM");
-            check_hip(launch_silu_gate(gate, up, rows * I, stream_), "prefill SiLU gate");
-            gemm(gate, I, L.down16, proj, H, H, I, "prefill down GEMM");
-            check_hip(launch_add_in_place(hidden, proj, rows * H, stream_), "prefill MLP residual");
+            // up GEMM with silu_gate as its epilogue (gate holds the gate product)
+            gemm(xn, H, L.up16, gate, I, I, H, "prefill up GEMM + SiLU gate", kGemmSiluGateInto);
+            gemm(gate, I, L.down16, hidden, H, H, I, "prefill down GEMM + residual", kGemmAddInto);
         }
     }
 
@@ -1051,7 +1049,7 @@ private:
     // split-K partial sums of the prefill GEMMs (short prompts), 16 MB
     static constexpr size_t kPrefillPartialFloats = size_t{4} << 20;
     struct PrefillBuffers {
-        DeviceBuffer hidden, normalized, qkv, attn, proj, gate, up, scores, values_t, positions, workspace, partial;
+        DeviceBuffer hidden, normalized, qkv, attn, proj, gate, scores, values_t, positions, workspace, partial;
         int rows = 0, score_stride = 0, capacity = 0;
         void ensure(int r, int H, int I, int qkvw, int qw, int query_heads, int kv_heads, int rp, int exact_capacity) {
             const size_t b = sizeof(bf16_t);
@@ -1063,7 +1061,6 @@ private:
                 attn = DeviceBuffer(static_cast<size_t>(r) * qw * b);
                 proj = DeviceBuffer(static_cast<size_t>(r) * H * b);
                 gate = DeviceBuffer(static_cast<size_t>(r) * I * b);
-                up = DeviceBuffer(static_cast<size_t>(r) * I * b);
                 rows = r;
             }
             if (rp > score_stride) {  // GEMM attention: scores, transposed values

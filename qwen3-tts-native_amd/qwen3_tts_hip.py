@@ -210,7 +210,7 @@ SIGNATURES = {
     "qwen3_tts_op_bf16_gemm_v1": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, I32, I32, C.c_int64, C.c_int64,
                                         C.c_int64, P] + ERR),
     "qwen3_tts_op_bf16_gemm_split_v1": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, I32, I32, C.c_int64,
-                                              C.c_int64, C.c_int64, P, C.c_uint64, I32, I32, I32, P] + ERR),
+                                              C.c_int64, C.c_int64, P, C.c_uint64, I32, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_causal_softmax_v1": (I32, [P, I32, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_kv_scatter_rows": (I32, [P, P, P, I32, I32, I32, P] + ERR),
     "qwen3_tts_op_elementwise": (I32, [I32, P, P, I32, I32, P] + ERR),

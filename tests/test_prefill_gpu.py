@@ -88,13 +88,13 @@ def test_bf16_gemm_batched_gqa_strides(hip, orc):
 
 
 def gemm_split(hip, a, b, m, n, k, tile, k_step, splits, workspace_floats=4 << 20, batch=1, b_group=1, a_batch=0,
-               b_batch=0, c_batch=0, lda=None, ldb=None, ldc=None, c_shape=None):
+               b_batch=0, c_batch=0, lda=None, ldb=None, ldc=None, c_shape=None, epilogue=0, c_init=None):
     c_shape = c_shape or (m, n)
     c = hip.DeviceArray(c_shape, np.uint16)
-    c.upload(np.zeros(c_shape, np.uint16))
+    c.upload(np.zeros(c_shape, np.uint16) if c_init is None else c_init)
     part = hip.DeviceArray(max(workspace_floats, 1), np.float32)
     hip.call("qwen3_tts_op_bf16_gemm_split_v1", a.ptr, b.ptr, c.ptr, m, n, k, lda or k, ldb or k, ldc or n, batch,
-             b_group, a_batch, b_batch, c_batch, part.ptr, workspace_floats, tile, k_step, splits, None)
+             b_group, a_batch, b_batch, c_batch, part.ptr, workspace_floats, tile, k_step, splits, epilogue, None)
     return c.numpy()
 
 
@@ -147,6 +147,24 @@ def test_bf16_gemm_split_batched_gqa(hip, orc):
         assert within_bound(got[h], p[h], vt[h // 2]).all(), h
 
 
+@pytest.mark.parametrize("splits", [1, 4])
+def test_bf16_gemm_epilogues_match_separate_ops(hip, orc, splits):
+    """The fused residual add and SiLU gate equal the GEMM followed by the
+    reference's add_in_place / silu_gate (oracle), bit for bit, with and
+    without K slices."""
+    rng = np.random.default_rng(40 + splits)
+    m, n, k = 24, 320, 2048
+    a = gen.activations(rng, m, k)
+    b = gen.bf16(0.05 * rng.standard_normal((n, k)).astype(np.float32))
+    other = gen.activations(rng, m, n)
+    da, db = dev(hip, a), dev(hip, b)
+    plain = gemm_split(hip, da, db, m, n, k, 32, 128, splits)
+    added = gemm_split(hip, da, db, m, n, k, 32, 128, splits, epilogue=1, c_init=other)
+    assert np.array_equal(added, orc.add_in_place(other.ravel(), plain.ravel()).reshape(m, n))
+    gated = gemm_split(hip, da, db, m, n, k, 32, 128, splits, epilogue=2, c_init=other)
+    assert np.array_equal(gated, orc.silu_gate(other.ravel(), plain.ravel()).reshape(m, n))
+
+
 def test_bf16_gemm_split_rejects_bad_arguments(hip):
     a = hip.DeviceArray(64 * 64, np.uint16)
     with pytest.raises(hip.Qwen3TtsError):
@@ -155,6 +173,8 @@ def test_bf16_gemm_split_rejects_bad_arguments(hip):
         gemm_split(hip, a, a, 8, 8, 64, 64, 256, 0)  # no such K step for the tile
     with pytest.raises(hip.Qwen3TtsError):
         gemm_split(hip, a, a, 8, 8, 64, 0, 0, -1)
+    with pytest.raises(hip.Qwen3TtsError):
+        gemm_split(hip, a, a, 8, 8, 64, 0, 0, 0, epilogue=3)
 
 
 @pytest.mark.parametrize("rows,stride", [(1, 8), (9, 16), (70, 72), (512, 512)])
