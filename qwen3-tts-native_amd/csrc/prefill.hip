@@ -100,7 +100,19 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(Bf16GemmArgs g,
 #pragma unroll
         for (int i = 0; i < kChunksB; ++i) {
             const int chunk = tid + i * kGemmThreads;
-            rb[set][i] = load_chunk(b, g.ldb, n0 + chunk / kRowChunks, g.n, k0 + (chunk % kRowChunks) * 8, g.k);
+            const int row = n0 + chunk / kRowChunks;
+            // B may come in up to three row segments (the q, k and v weights)
+            const bf16_t* bseg = b;
+            int brow = row;
+            if (g.b3 != nullptr && row >= g.b3_row) {
+                bseg = g.b3;
+                brow = row - g.b3_row;
+            } else if (g.b2 != nullptr && row >= g.b2_row) {
+                bseg = g.b2;
+                brow = row - g.b2_row;
+            }
+            rb[set][i] = row < g.n ? load_chunk(bseg, g.ldb, brow, g.n, k0 + (chunk % kRowChunks) * 8, g.k)
+                                   : uint4{0u, 0u, 0u, 0u};
         }
     };
     auto stage = [&](int set, int buffer) {
@@ -354,6 +366,12 @@ hipError_t launch_bf16_gemm(const Bf16GemmArgs& g, hipStream_t stream) {
         return hipErrorInvalidValue;
     }
     if (g.epilogue != kGemmStore && g.epilogue != kGemmAddInto && g.epilogue != kGemmSiluGateInto) {
+        return hipErrorInvalidValue;
+    }
+    if ((g.b2 != nullptr || g.b3 != nullptr) &&
+        (g.batch != 1 || (g.b2 != nullptr && (g.b2_row <= 0 || g.b2_row >= g.n)) ||
+         (g.b3 != nullptr && (g.b3_row <= (g.b2 != nullptr ? g.b2_row : 0) || g.b3_row >= g.n)) ||
+         ((reinterpret_cast<uintptr_t>(g.b2) | reinterpret_cast<uintptr_t>(g.b3)) & 15u) != 0)) {
         return hipErrorInvalidValue;
     }
     const uintptr_t align = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b);

@@ -379,6 +379,11 @@ struct Bf16GemmArgs {
     int force_k_step = 0;  // 0: planned; else K per pipeline step (32 tile: 64/128/256; 64: 64/128; 128: 64)
     int force_splits = 0;  // 0: planned; else the K slices (bounded by the workspace)
     int epilogue = kGemmStore;
+    // B in row segments (batch 1): rows from b2_row on come from b2, rows
+    // from b3_row on from b3 (each segment row-major with stride ldb).
+    const bf16_t* b2 = nullptr;
+    const bf16_t* b3 = nullptr;
+    int b2_row = 0, b3_row = 0;
 };
 hipError_t launch_bf16_gemm(const Bf16GemmArgs& args, hipStream_t stream);
 // Prompts of at most this many positions run the reference's GEMM attention

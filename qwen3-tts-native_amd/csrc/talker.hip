@@ -759,9 +759,25 @@ public:
             bf16_t* kc = host_bases_[l];
             bf16_t* vc = host_bases_[T.layers + l];
             check_hip(launch_rms_norm_rows(hidden, L.input_norm, xn, rows, H, cfg_.eps, stream_), "prefill input norm");
-            gemm(xn, H, L.q16, qkv, qkvw, qw, H, "prefill q GEMM");
-            gemm(xn, H, L.k16, qkv + qw, qkvw, kvw, H, "prefill k GEMM");
-            gemm(xn, H, L.v16, qkv + qw + kvw, qkvw, kvw, H, "prefill v GEMM");
+            {  // q, k and v: one GEMM over the three weights as row segments of B
+                Bf16GemmArgs g;
+                g.a = xn;
+                g.b = L.q16;
+                g.b2 = L.k16;
+                g.b2_row = qw;
+                g.b3 = L.v16;
+                g.b3_row = qw + kvw;
+                g.c = qkv;
+                g.m = rows;
+                g.n = qkvw;
+                g.k = H;
+                g.lda = H;
+                g.ldb = H;
+                g.ldc = qkvw;
+                g.partial = w.partial.as<float>();
+                g.partial_floats = kPrefillPartialFloats;
+                check_hip(launch_bf16_gemm(g, stream_), "prefill q/k/v GEMM");
+            }
             check_hip(launch_prefill_qkv_epilogue(qkv, L.q_norm, L.k_norm, m_.rope_table_.as<bf16_t>(), kc, vc, vstride, 0,
                                                   rows, T.query_heads, T.key_value_heads, cfg_.eps, stream_),
                       "prefill q/k norm + RoPE + cache");
