@@ -170,8 +170,9 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_fixed(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Exact-order rows 2..8 without the RMSNorm prologue, K = 512 * kVpl known at
-// compile time (the prompt's text projection, exact batched mode): the
+// Exact-order rows without the RMSNorm prologue -- 2..8 (exact batched mode)
+// or a whole prompt's (its text projection) -- K = 512 * kVpl known at
+// compile time: the
 // batch-1 kernel's layout -- one unit per half-wave, its weights (the lane's
 // vectors lane + 32 i) requested first and held in registers -- against every
 // input row, staged once per block in LDS.  Per row the sum is the generic
@@ -199,30 +200,39 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_rows_fixed(GemvArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);  // the weight stream first, then the rows
     const uint4* xin = reinterpret_cast<const uint4*>(a.input);
-    for (int c = threadIdx.x; c < rows * kChunks; c += kThreads) rows_lds[c] = xin[c];
-    __syncthreads();
-    for (int r = 0; r < rows; ++r) {
-        const bf16_t* xs = reinterpret_cast<const bf16_t*>(rows_lds + r * kChunks);
-        float acc[kTiles];
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kVpl; ++i) {
-            float xv[16];
-            load_x16<false>(xs, nullptr, lane + 32 * i, 1.0f, xv);
-#pragma unroll
-            for (int t = 0; t < kTiles; ++t) acc[t] += chain16(w[t][i], xv);
+    // rows in chunks of up to 8 through LDS (more than 8 only for a prompt's
+    // rows: the weights stay in registers for all of them)
+    for (int r0 = 0; r0 < rows; r0 += 8) {
+        const int count = min(8, rows - r0);
+        if (r0 > 0) __syncthreads();  // the previous chunk is read
+        for (int c = threadIdx.x; c < count * kChunks; c += kThreads) {
+            rows_lds[c] = xin[static_cast<size_t>(r0) * kChunks + c];
         }
+        __syncthreads();
+        for (int rr = 0; rr < count; ++rr) {
+            const int r = r0 + rr;
+            const bf16_t* xs = reinterpret_cast<const bf16_t*>(rows_lds + rr * kChunks);
+            float acc[kTiles];
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = fold32(acc[t]);
-        if (lane == 0 && unit < units) {
-            GemvArgs row = a;
-            row.out16 = a.out16 ? a.out16 + static_cast<size_t>(r) * a.out_features : nullptr;
-            row.out32 = a.out32 ? a.out32 + static_cast<size_t>(r) * a.out_features : nullptr;
-            if constexpr (kSilu) {
-                store_gate_up<kEpi>(row, unit, acc[0], acc[kTiles - 1]);
-            } else {
-                store_channel<kEpi>(row, unit, acc[0]);
+            for (int t = 0; t < kTiles; ++t) acc[t] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kVpl; ++i) {
+                float xv[16];
+                load_x16<false>(xs, nullptr, lane + 32 * i, 1.0f, xv);
+#pragma unroll
+                for (int t = 0; t < kTiles; ++t) acc[t] += chain16(w[t][i], xv);
+            }
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) acc[t] = fold32(acc[t]);
+            if (lane == 0 && unit < units) {
+                GemvArgs row = a;
+                row.out16 = a.out16 ? a.out16 + static_cast<size_t>(r) * a.out_features : nullptr;
+                row.out32 = a.out32 ? a.out32 + static_cast<size_t>(r) * a.out_features : nullptr;
+                if constexpr (kSilu) {
+                    store_gate_up<kEpi>(row, unit, acc[0], acc[kTiles - 1]);
+                } else {
+                    store_channel<kEpi>(row, unit, acc[0]);
+                }
             }
         }
     }
@@ -235,7 +245,7 @@ hipError_t launch_exact_rows_fixed(const GemvArgs& a, hipStream_t s) {
     const hipError_t st = set_dynamic_lds_once(configured, reinterpret_cast<const void*>(gemv_exact_rows_fixed<kVpl, kEpi>),
                                                static_cast<int>(8 * kIn * sizeof(bf16_t)));
     if (st != hipSuccess) return st;
-    const size_t lds = static_cast<size_t>(a.rows) * kIn * sizeof(bf16_t);
+    const size_t lds = static_cast<size_t>(std::min(a.rows, 8)) * kIn * sizeof(bf16_t);
     gemv_exact_rows_fixed<kVpl, kEpi><<<(a.out_features + kHalfWaves - 1) / kHalfWaves, kThreads, lds, s>>>(a);
     return hipGetLastError();
 }
@@ -914,6 +924,47 @@ hipError_t launch_int8_gemv(const GemvArgs& a, hipStream_t stream) {
         case kEpiBias: return norm ? dispatch<kEpiBias, true>(a, stream) : dispatch<kEpiBias, false>(a, stream);
         case kEpiBiasSilu: return norm ? dispatch<kEpiBiasSilu, true>(a, stream) : dispatch<kEpiBiasSilu, false>(a, stream);
         case kEpiBiasAdd: return norm ? dispatch<kEpiBiasAdd, true>(a, stream) : dispatch<kEpiBiasAdd, false>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// A prompt's rows (any count) in exact order through one launch, each row's
+// result the same as through launch_int8_gemv in launches of up to 8 rows
+// (the per-row sum does not depend on the rows beside it).  No RMSNorm
+// prologue; store and bias epilogues; K outside {1024, 2048, 3072, 6144} runs
+// as launches of up to 8 rows.
+hipError_t launch_int8_gemv_prompt_rows(const GemvArgs& a, hipStream_t stream) {
+    if (a.weight == nullptr || a.scales == nullptr || a.input == nullptr || a.out16 == nullptr || a.rows < 1 ||
+        a.out_features <= 0 || a.norm_weight != nullptr || a.input_row_index != nullptr || a.out32 != nullptr ||
+        !aligned16(a.weight) || !aligned16(a.input)) {
+        return hipErrorInvalidValue;
+    }
+    if (a.epilogue >= kEpiBias && a.bias == nullptr) return hipErrorInvalidValue;
+    auto by_k = [&](auto epi) -> hipError_t {
+        constexpr int kE = decltype(epi)::value;
+        switch (a.in_features) {
+            case 1024: return launch_exact_rows_fixed<2, kE>(a, stream);
+            case 2048: return launch_exact_rows_fixed<4, kE>(a, stream);
+            case 3072: return launch_exact_rows_fixed<6, kE>(a, stream);
+            case 6144: return launch_exact_rows_fixed<12, kE>(a, stream);
+            default: break;
+        }
+        // other widths: launches of up to 8 rows
+        for (int r0 = 0; r0 < a.rows; r0 += 8) {
+            GemvArgs part = a;
+            part.rows = std::min(8, a.rows - r0);
+            part.mode = kModeExact;
+            part.input = a.input + static_cast<size_t>(r0) * a.in_features;
+            part.out16 = a.out16 + static_cast<size_t>(r0) * a.out_features;
+            const hipError_t st = launch_int8_gemv(part, stream);
+            if (st != hipSuccess) return st;
+        }
+        return hipSuccess;
+    };
+    switch (a.epilogue) {
+        case kEpiStore: return by_k(std::integral_constant<int, kEpiStore>{});
+        case kEpiBias: return by_k(std::integral_constant<int, kEpiBias>{});
+        case kEpiBiasSilu: return by_k(std::integral_constant<int, kEpiBiasSilu>{});
         default: return hipErrorInvalidValue;
     }
 }

@@ -174,6 +174,8 @@ struct GemvArgs {
 };
 
 hipError_t launch_int8_gemv(const GemvArgs& args, hipStream_t stream);
+// Exact-order rows of a prompt (any count, no RMSNorm) in one launch.
+hipError_t launch_int8_gemv_prompt_rows(const GemvArgs& a, hipStream_t stream);
 
 hipError_t launch_quantize_weight_rows(const bf16_t* weight, int8_t* quantized, float* scales,
                                        int in_features, int out_features, hipStream_t stream);

@@ -508,6 +508,7 @@ struct Gemv {
         return *this;
     }
     void run(hipStream_t s, const char* what) { check_hip(launch_int8_gemv(a, s), what); }
+    void run_prompt_rows(hipStream_t s, const char* what) { check_hip(launch_int8_gemv_prompt_rows(a, s), what); }
 };
 
 struct SamplingParams {
@@ -721,15 +722,12 @@ public:
         check_hip(launch_gather_text_rows(m_.text_embedding_, text_ids, cfg_.text_vocab, rows, H, w.normalized.as<bf16_t>(),
                                           stream_),
                   "gather prompt text embeddings");
-        for (int r0 = 0; r0 < rows; r0 += 8) {
-            const int n = std::min(8, rows - r0);
-            Gemv(m_.text_fc1_, w.normalized.as<bf16_t>() + static_cast<size_t>(r0) * H, H, H, kEpiBiasSilu)
-                .bias(m_.text_fc1_bias_).rows(n, kModeExact).to(w.proj.as<bf16_t>() + static_cast<size_t>(r0) * H)
-                .run(stream_, "prompt text fc1");
-            Gemv(m_.text_fc2_, w.proj.as<bf16_t>() + static_cast<size_t>(r0) * H, H, H, kEpiBias)
-                .bias(m_.text_fc2_bias_).rows(n, kModeExact).to(hidden + static_cast<size_t>(r0) * H)
-                .run(stream_, "prompt text fc2");
-        }
+        // (the reference runs 8 rows a launch; each row's exact-order sum is
+        // the same whatever rows share its launch, so all rows run in one)
+        Gemv(m_.text_fc1_, w.normalized.as<bf16_t>(), H, H, kEpiBiasSilu).bias(m_.text_fc1_bias_)
+            .rows(rows, kModeExact).to(w.proj.as<bf16_t>()).run_prompt_rows(stream_, "prompt text fc1");
+        Gemv(m_.text_fc2_, w.proj.as<bf16_t>(), H, H, kEpiBias).bias(m_.text_fc2_bias_)
+            .rows(rows, kModeExact).to(hidden).run_prompt_rows(stream_, "prompt text fc2");
         check_hip(launch_prompt_rows(hidden, text_ids, codec_ids, m_.codec_embedding_, cfg_.talker_vocab, rows, H, stream_),
                   "prompt rows");
         auto gemm = [&](const bf16_t* a, int lda, const bf16_t* weight, bf16_t* c, int ldc, int n, int k,
