@@ -202,8 +202,11 @@ __global__ __launch_bounds__(kThreads) void gemv_exact_rows_fixed(GemvArgs a) {
     const uint4* xin = reinterpret_cast<const uint4*>(a.input);
     // rows in chunks of up to 8 through LDS (more than 8 only for a prompt's
     // rows: the weights stay in registers for all of them)
-    for (int r0 = 0; r0 < rows; r0 += 8) {
-        const int count = min(8, rows - r0);
+    // gridDim.y groups of rows (a long prompt's rows over more workgroups)
+    const int per_group = (rows + gridDim.y - 1) / gridDim.y;
+    const int r_end = min(rows, static_cast<int>(blockIdx.y + 1) * per_group);
+    for (int r0 = blockIdx.y * per_group; r0 < r_end; r0 += 8) {
+        const int count = min(8, r_end - r0);
         if (r0 > 0) __syncthreads();  // the previous chunk is read
         for (int c = threadIdx.x; c < count * kChunks; c += kThreads) {
             rows_lds[c] = xin[static_cast<size_t>(r0) * kChunks + c];
@@ -246,7 +249,12 @@ hipError_t launch_exact_rows_fixed(const GemvArgs& a, hipStream_t s) {
                                                static_cast<int>(8 * kIn * sizeof(bf16_t)));
     if (st != hipSuccess) return st;
     const size_t lds = static_cast<size_t>(std::min(a.rows, 8)) * kIn * sizeof(bf16_t);
-    gemv_exact_rows_fixed<kVpl, kEpi><<<(a.out_features + kHalfWaves - 1) / kHalfWaves, kThreads, lds, s>>>(a);
+    // more than 8 rows: up to 4 groups of rows on their own workgroups, each
+    // reading the weights again (measured: one workgroup per CU leaves the
+    // per-row arithmetic's latency exposed)
+    const int groups = std::min(4, (a.rows + 7) / 8);
+    const dim3 grid((a.out_features + kHalfWaves - 1) / kHalfWaves, groups);
+    gemv_exact_rows_fixed<kVpl, kEpi><<<grid, kThreads, lds, s>>>(a);
     return hipGetLastError();
 }
 
