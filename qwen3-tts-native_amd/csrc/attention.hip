@@ -76,6 +76,12 @@ struct AttnArgs {
     // of 8; per row from value_strides when that is set.
     int value_stride;
     const int* value_strides;
+    // Batched (non-exact) value chains split over position_splits segments
+    // (tolerance semantics only): unnormalized partial chains in `partials`
+    // [rows][query_heads][splits][128], added in segment order by a second
+    // launch, which applies the inverse (`inverse`).
+    int position_splits;
+    float* partials;
 };
 
 __device__ __forceinline__ int row_length(const AttnArgs& a, int row) {
@@ -391,7 +397,7 @@ __device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, const f
     return acc;
 }
 
-template <bool kExact, int kG>
+template <bool kExact, int kG, bool kSplit = false>
 __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float p_lds[];  // scores, then exponentials, then probabilities
     const int row = blockIdx.y;
@@ -400,6 +406,14 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     const int kvh = head / kG;
     const int lane = threadIdx.x;
     const int length = row_length(a, row);
+    // kSplit: this workgroup's segment of the value chain (whole ring rounds)
+    constexpr int kRound = kRing * 8;
+    int chain_begin = 0, chain_end = length;
+    if constexpr (kSplit) {
+        const int per = ((length + gridDim.z - 1) / gridDim.z + kRound - 1) / kRound * kRound;
+        chain_begin = min(length, static_cast<int>(blockIdx.z) * per);
+        chain_end = min(length, chain_begin + per);
+    }
 
     // 1. value ring
     const bf16_t* vrun = value_run(a, row, kvh, half * 64 + lane);
@@ -407,7 +421,7 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     auto load = [&](int i) { return load_global16(vrun + kGroupStep * (i < last_group ? i : last_group)); };
     uint4 ring[kRing];
 #pragma unroll
-    for (int k = 0; k < kRing; ++k) ring[k] = load(k);
+    for (int k = 0; k < kRing; ++k) ring[k] = load(chain_begin / 8 + k);
     asm volatile("" ::: "memory");  // in flight before the scores are requested
 
     // 2. this head's scores into LDS, 16 loads in flight per lane
@@ -540,11 +554,28 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
             ring[k + 1] = load(i + 1 + kRing);
         }
     };
-    int base = 0;
-    for (; base + kRing * 8 <= length; base += kRing * 8) round(base, kRing * 8);
-    if (base < length) round(base, length - base);
+    int base = chain_begin;
+    for (; base + kRing * 8 <= chain_end; base += kRing * 8) round(base, kRing * 8);
+    if (base < chain_end) round(base, chain_end - base);
+    if constexpr (kSplit) {
+        const size_t slot = (static_cast<size_t>(row) * a.query_heads + head) * gridDim.z + blockIdx.z;
+        a.partials[slot * kDim + half * 64 + lane] = acc;
+        if (blockIdx.z == 0 && half == 0 && lane == 0) a.inverse[static_cast<size_t>(row) * a.query_heads + head] = inverse;
+        return;
+    }
     const float y = kExact ? acc : acc * inverse;
     a.output[(static_cast<size_t>(row) * a.query_heads + head) * kDim + half * 64 + lane] = f2bf(y);
+}
+
+// The split value chains: out = bf16((partial_0 + .. + partial_{S-1}) * inverse),
+// segments added in order.  One workgroup per (row, query head), lane =
+// dimension.
+__global__ __launch_bounds__(kDim) void attention_combine_kernel(AttnArgs a, int splits) {
+    const size_t rh = blockIdx.x;
+    const float* p = a.partials + rh * splits * kDim + threadIdx.x;
+    float acc = p[0];
+    for (int s = 1; s < splits; ++s) acc += p[static_cast<size_t>(s) * kDim];
+    a.output[rh * kDim + threadIdx.x] = f2bf(acc * a.inverse[rh]);
 }
 
 // ---------------------------------------------------------------------------
@@ -972,6 +1003,19 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.query_heads, rows);
         attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
     }
+    if (!kExact && a.position_splits > 1 && a.partials != nullptr) {
+        static std::atomic<unsigned long long> configured_split{0};
+        const hipError_t sst = set_dynamic_lds_once(
+            configured_split, reinterpret_cast<const void*>(attention_head_kernel<kExact, kG, true>),
+            static_cast<int>(kLdsLimit));
+        if (sst != hipSuccess) return sst;
+        attention_head_kernel<kExact, kG, true>
+            <<<dim3(a.query_heads * 2, rows, a.position_splits), 64, head_lds, stream>>>(a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attention_combine_kernel<<<rows * a.query_heads, kDim, 0, stream>>>(a, a.position_splits);
+        return hipGetLastError();
+    }
     attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
 }
@@ -983,6 +1027,11 @@ int value_cache_stride(int capacity) { return (capacity + 7) / 8 * 8; }
 
 size_t attention_workspace_bytes(int rows, int query_heads, int capacity) {
     return static_cast<size_t>(rows) * query_heads * (static_cast<size_t>(capacity) + 1) * sizeof(float);
+}
+
+size_t attention_split_workspace_bytes(int rows, int query_heads, int capacity, int splits) {
+    return attention_workspace_bytes(rows, query_heads, capacity) +
+           static_cast<size_t>(rows) * query_heads * splits * kDim * sizeof(float);
 }
 
 namespace {
@@ -1054,7 +1103,9 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
                                    bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
                                    const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
                                    int query_heads, int key_value_heads, int head_dimension, int capacity,
-                                   float* workspace, const int* value_strides, hipStream_t stream) {
+                                   float* workspace, const int* value_strides, hipStream_t stream,
+                                   int position_splits) {
+    if (position_splits < 1 || position_splits > 8) return hipErrorInvalidValue;
     if (!valid_shape(rows, query_heads, key_value_heads, head_dimension, capacity, workspace) || qkv == nullptr ||
         output == nullptr || q_norm == nullptr || k_norm == nullptr || rope_table == nullptr ||
         positions == nullptr) {
@@ -1068,6 +1119,10 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
     a.k_norm = k_norm;
     a.rope_table = rope_table;
     a.epsilon = epsilon;
+    if (position_splits > 1) {
+        a.position_splits = position_splits;
+        a.partials = workspace + static_cast<size_t>(rows) * query_heads * (static_cast<size_t>(capacity) + 1);
+    }
     return dispatch(exact, a, rows, stream);
 }
 

@@ -237,7 +237,13 @@ hipError_t launch_decode_attention(bool exact, const bf16_t* qkv, int qkv_stride
                                    bf16_t* const* key_bases, bf16_t* const* value_bases, const bf16_t* key_cache,
                                    const bf16_t* value_cache, const int* positions, bf16_t* output, int rows,
                                    int query_heads, int key_value_heads, int head_dimension, int capacity,
-                                   float* workspace, const int* value_strides, hipStream_t stream);
+                                   float* workspace, const int* value_strides, hipStream_t stream,
+                                   int position_splits = 1);
+// Workspace of launch_decode_attention with position_splits > 1 (the
+// batched, non-exact semantics only: the value chains of each row and head
+// run as `splits` segments whose sums are added afterwards -- tolerance, not
+// the reference's single chain).
+size_t attention_split_workspace_bytes(int rows, int query_heads, int capacity, int splits);
 hipError_t launch_decode_attention_op(bool exact, const bf16_t* qkv, int qkv_stride, const bf16_t* q_norm,
                                       const bf16_t* k_norm, const bf16_t* rope_table, float epsilon,
                                       bf16_t* const* key_bases, bf16_t* const* value_bases, const int* positions,

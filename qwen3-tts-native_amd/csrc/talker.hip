@@ -50,6 +50,10 @@ constexpr int kCodebooks = 16;
 constexpr int kResidualCodebooks = 15;
 constexpr int kMaxBatch = QWEN3_TTS_MAX_BATCH_SESSIONS;
 constexpr int kAttentionCapacity = 8192;  // largest session max_sequence_length
+// MFMA (tolerance) batch mode: each talker row's value chains run as this many
+// position segments, for more workgroups on long caches (the exact mode keeps
+// the reference's one chain)
+constexpr int kAttentionSplits = 2;
 
 void write_error(char* destination, size_t capacity, const char* message) {
     if (destination != nullptr && capacity != 0) {
@@ -1384,8 +1388,9 @@ public:
         proj_ = DeviceBuffer(R * T.hidden * b);
         qkv_ = DeviceBuffer(R * std::max(T.qkv_width(), P.qkv_width()) * b);
         attn_ = DeviceBuffer(R * std::max(T.query_width(), P.query_width()) * b);
-        attn_scratch_ = DeviceBuffer(attention_workspace_bytes(static_cast<int>(R), std::max(T.query_heads, P.query_heads),
-                                                               kAttentionCapacity));
+        attn_scratch_ = DeviceBuffer(attention_split_workspace_bytes(static_cast<int>(R),
+                                                                     std::max(T.query_heads, P.query_heads),
+                                                                     kAttentionCapacity, kAttentionSplits));
         act_ = DeviceBuffer(R * std::max(T.intermediate, P.intermediate) * b);
         logits_ = DeviceBuffer(R * std::max(cfg_.talker_vocab, cfg_.predictor_vocab) * b);
         layers_ = T.layers + P.layers;
@@ -1669,7 +1674,8 @@ private:
                                               m_.rope_table_.as<bf16_t>(), cfg_.eps, kv_table(slot0 + l, false),
                                               kv_table(slot0 + l, true), nullptr, nullptr, pos, attn_.as<bf16_t>(), n,
                                               d.query_heads, d.key_value_heads, d.head_dimension, capacity,
-                                              attn_scratch_.as<float>(), predictor ? nullptr : value_strides(), stream_),
+                                              attn_scratch_.as<float>(), predictor ? nullptr : value_strides(), stream_,
+                                              (mode == kModeMfma || (mode == kModeAuto && n >= 2)) ? kAttentionSplits : 1),
                       "batch q/k norm + RoPE + KV append + attention");
             Gemv(L.o, attn_.as<bf16_t>(), d.query_width(), d.hidden, kEpiAddFma).rows(n, mode).to(hidden)
                 .run(stream_, "batch O GEMV");
