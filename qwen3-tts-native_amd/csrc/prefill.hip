@@ -9,11 +9,13 @@
 // queries x keys^T, probabilities x values^T), batched over heads through
 // gridDim.z with a grouped B index for GQA.  A 128x128 (or, when that leaves
 // CUs idle, 64x64 or 32x32) block tile of 256 threads (4 waves in 2x2, each a grid of
-// v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 (128, 256 for the smaller
-// tiles) staged through double-buffered LDS (padded rows), the next step's
-// global loads issued before the current step's MFMAs.  Short prompts, whose
-// grids leave CUs idle and whose steps each wait one memory latency, split K
-// into slices (fp32 partial sums, added in slice order by a second launch).
+// v_mfma_f32_16x16x32_bf16 tiles), K in steps of 64 to 256 (by tile and
+// prompt length) staged through double-buffered LDS (padded rows), the
+// global loads of the next one or two steps in flight under each step's
+// MFMAs.  Deep products and under-filled grids split K into slices (fp32
+// partial sums, added in slice order by a second launch).  Epilogues fold
+// the reference's residual add_in_place and silu_gate into the products, and
+// B may come in three row segments (the q, k and v weights as one GEMM).
 //
 // The summation order of an fp32 GEMM is not the reference's (cuBLAS leaves
 // it unspecified), so this path is compared with tolerances; everything
