@@ -1,4 +1,4 @@
-// Decode attention over a bf16 KV cache, head dimension 128.  Four kernels:
+// Decode attention over a bf16 KV cache, head dimension 128.  Four main kernels:
 //
 //   scores  (caches > 64 positions) one wave per (64 positions, query head,
 //           row), lane = position: the query head and the new key are
@@ -15,6 +15,10 @@
 //           append, scores, softmax and values fused, with the QKV epilogue.
 //   small   (other caches <= 64 positions) one block of G*128 threads per
 //           (kv head, row), the phases in one kernel.
+// and two for particular callers: prompt-row score tiles (many prompt rows on
+// one shared, complete cache: each key row loaded once for a tile of rows and
+// the heads of its group), and the combine of the batched (non-exact) value
+// chains when they run as position segments (tolerance mode only).
 //
 // Two arithmetic variants, each the reference's own operation order:
 //   exact  causal_gqa_attention_kernel (talker_kernels.cu:287-357):
