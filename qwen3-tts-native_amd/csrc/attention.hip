@@ -179,6 +179,40 @@ __device__ __forceinline__ float exact_score(const float* qg, const uint32_t (&k
     return round_bf(round_bf(s[0]) * scale);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// The key pair (k[t], k[t + 64]) of a key row held as 64 packed bf16 pairs
+// (kw[j] = (k[2j], k[2j + 1]), kw[32 + j] = (k[64 + 2j], k[65 + 2j])).
+__device__ __forceinline__ uint32_t key_pair(const uint32_t (&kw)[64], int t) {
+    const uint32_t lo = kw[t >> 1], hi = kw[32 + (t >> 1)];
+    return (t & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+}
+
+// exact_score's arithmetic on bf16 pairs: leaf t = q[t] k[t] + q[t+64] k[t+64]
+// as one bf16 dot2 on (q[t], q[t+64]) x (k[t], k[t+64]) -- both products of
+// bf16 values are exact in fp32, so the sum rounds once, as the two fmas and
+// the add do -- then the same tree (s[t] += s[t + w], w = 32..1) evaluated
+// as a stack over the leaves in post-order (bit-reversed index order): at
+// most six partial sums live.  Bit-identical to exact_score.  kp(t): the
+// key pair of leaf t.
+template <typename KeyPair>
+__device__ __forceinline__ float exact_score_pairs(const uint32_t* qp, KeyPair kp, float scale) {
+    float stack[6];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+        const int t = static_cast<int>(__builtin_bitreverse32(static_cast<unsigned>(i)) >> 26);
+        float v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp[t]), __builtin_bit_cast(bf16x2_t, kp(t)),
+                                                  0.0f, false);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            if (((i >> b) & 1) == 0) break;
+            v = stack[b] + v;  // earlier (left) subtree + this one
+        }
+        stack[__builtin_ctz(~static_cast<unsigned>(i)) < 6 ? __builtin_ctz(~static_cast<unsigned>(i)) : 0] = v;
+    }
+    return round_bf(round_bf(stack[0]) * scale);
+}
+
 // ---------------------------------------------------------------------------
 // scores: grid (position blocks, kv heads, rows), 64 threads, lane = position
 // ---------------------------------------------------------------------------
@@ -192,6 +226,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     const int p0 = blockIdx.x * kScoreLanes;
     if (p0 >= length) return;
     __shared__ float q_lds[kDim];
+    __shared__ uint32_t q_pairs[kDim / 2];  // (q[t], q[t + 64]) bf16 pairs for the exact score
     __shared__ uint32_t knew_lds[kDim / 2];
     const int lane = threadIdx.x;
     const int position = length - 1;
@@ -218,6 +253,8 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
         head_detail::norm_rope_head(q, a.q_norm, cs, a.epsilon, q0, q1);
         q_lds[lane] = bf2f(q0);
         q_lds[lane + 64] = bf2f(q1);
+        q_pairs[lane] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, q0)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, q1)) << 16);
         if (position >= p0 && position < p0 + kScoreLanes) {
             // the current key; the group's first query head appends it (and
             // the value) to the caches
@@ -235,6 +272,8 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     } else {
         q_lds[lane] = bf2f(q[lane]);
         q_lds[lane + 64] = bf2f(q[lane + 64]);
+        q_pairs[lane] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, q[lane])) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, q[lane + 64])) << 16);
     }
     __syncthreads();
     if (p >= length) return;
@@ -244,7 +283,7 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     }
     float score;
     if constexpr (kExact) {
-        score = exact_score(q_lds, kw, a.scale);
+        score = exact_score_pairs(q_pairs, [&](int t) { return key_pair(kw, t); }, a.scale);
     } else {
         float dot = 0.0f;
 #pragma unroll
@@ -257,7 +296,6 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_kernel(AttnArgs 
     a.scores[(static_cast<size_t>(row) * a.query_heads + head) * a.capacity + p] = score;
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Prompt rows against one shared, complete key cache (the prefill's exact
 // attention for long prompts: queries already normalized and rotated):
@@ -305,35 +343,18 @@ __global__ __launch_bounds__(kScoreLanes) void attention_scores_rows_kernel(Attn
                             static_cast<size_t>(kvh * kG + h) * kDim;
         q_pairs[r][h][t] = static_cast<uint32_t>(q[t]) | (static_cast<uint32_t>(q[t + 64]) << 16);
     }
-    // key pairs (k[t], k[t + 64])
+    // key pairs (k[t], k[t + 64]), once for the tile's rows and heads
     uint32_t kp[64];
 #pragma unroll
-    for (int t = 0; t < 64; ++t) {
-        const uint32_t lo = kw[t >> 1], hi = kw[32 + (t >> 1)];
-        kp[t] = (t & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-    }
+    for (int t = 0; t < 64; ++t) kp[t] = key_pair(kw, t);
     __syncthreads();
     for (int r = 0; r < kRows && r0 + r <= last; ++r) {
         const int row = r0 + r;
         if (p >= row_length(a, row)) continue;
 #pragma unroll
         for (int h = 0; h < kG; ++h) {
-            const uint32_t* qp = q_pairs[r][h];
-            float stack[6];
-#pragma unroll
-            for (int i = 0; i < 64; ++i) {
-                const int t = static_cast<int>(__builtin_bitreverse32(static_cast<unsigned>(i)) >> 26);
-                float v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qp[t]),
-                                                          __builtin_bit_cast(bf16x2_t, kp[t]), 0.0f, false);
-#pragma unroll
-                for (int b = 0; b < 6; ++b) {
-                    if (((i >> b) & 1) == 0) break;
-                    v = stack[b] + v;  // earlier (left) subtree + this one
-                }
-                stack[__builtin_ctz(~static_cast<unsigned>(i)) < 6 ? __builtin_ctz(~static_cast<unsigned>(i)) : 0] = v;
-            }
             a.scores[(static_cast<size_t>(row) * a.query_heads + kvh * kG + h) * a.capacity + p] =
-                round_bf(round_bf(stack[0]) * a.scale);
+                exact_score_pairs(q_pairs[r][h], [&](int t) { return kp[t]; }, a.scale);
         }
     }
 }
