@@ -58,7 +58,8 @@ def test_exact_rows_bit_identical(hip, orc, rows, out_f, in_f):
 
 
 @pytest.mark.parametrize("rows", [2, 4, 8])
-@pytest.mark.parametrize("out_f,in_f", [(12288, 2048), (2048, 6144), (1028, 2048), (1024, 3072), (2052, 1024), (64, 256), (130, 512)])
+@pytest.mark.parametrize("out_f,in_f", [(12288, 2048), (2048, 6144), (1028, 2048), (1024, 3072), (2052, 1024), (4096, 2048),
+                                        (3072, 1024), (64, 256), (130, 512)])
 def test_mfma_rows_within_tolerance(hip, orc, rows, out_f, in_f):
     rng = np.random.default_rng(rows + out_f + in_f)
     w, s, x = gen.weights(rng, out_f, in_f), gen.scales(rng, out_f), gen.activations(rng, rows, in_f)

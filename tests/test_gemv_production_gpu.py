@@ -142,3 +142,40 @@ def test_talker_step_chain_two_layers(hip, orc):
         assert np.array_equal(got, ref), f"layer {layer}: {np.count_nonzero(got != ref)} of {H} differ"
         assert np.array_equal(qkv.numpy(), q16)
         assert np.array_equal(act.numpy(), a16)
+
+
+# MFMA mode (rows 2..8) at the production widths.  The launcher packs 1, 2 or
+# 3 groups of 8 channels per block by width (talker gate/up 3, QKV 2, O and
+# down 1; predictor QKV and gate/up 2), so these shapes run every group count
+# with the norm prologue and the SiLU / residual epilogues.  The summation
+# order is MFMA's: bf16 outputs within one bf16 rounding step (2^-7 of the
+# value, the result of the sum rounding either way) plus ATOL of the oracle's
+# exact-order result; fp32 outputs within the north-star bar 1e-2 + 1e-3|y|.
+MFMA_SHAPES = [  # (kernel output width, in_features, epilogue, norm)
+    (4096, 2048, "store", True), (2048, 2048, "add_fma", False), (6144, 2048, "silu_fused", True),
+    (2048, 6144, "add_fma", False), (4096, 1024, "store", True), (1024, 2048, "add_fma", False),
+    (3072, 1024, "silu_fused", True), (1024, 3072, "add_fma", False)]
+
+
+@pytest.mark.parametrize("rows", [2, 8])
+@pytest.mark.parametrize("out_f,in_f,epilogue,norm", MFMA_SHAPES)
+def test_mfma_production_widths(hip, orc, rows, out_f, in_f, epilogue, norm):
+    silu = epilogue.startswith("silu")
+    rng = np.random.default_rng(out_f + 3 * in_f + rows)
+    w_rows = 2 * out_f if silu else out_f
+    w, s = gen.weights(rng, w_rows, in_f), gen.scales(rng, w_rows)
+    x, g = gen.activations(rng, rows, in_f), gen.gains(rng, in_f)
+    base = gen.activations(rng, rows, out_f)
+    xn = orc.rms_norm_rows(x, g) if norm else x
+    ref = oracle_epilogue(orc, epilogue, w, s, xn, base, None)
+    y = dev(hip, base) if epilogue == "add_fma" else hip.DeviceArray((rows, out_f), np.uint16)
+    y32 = hip.DeviceArray((rows, out_f), np.float32) if epilogue == "store" else None
+    hip.int8_gemv(dev(hip, w), dev(hip, s), dev(hip, x), in_f, out_f, rows, out16=y, out32=y32,
+                  epilogue=getattr(hip, "EPI_" + epilogue.upper()), norm_weight=dev(hip, g) if norm else None,
+                  mode=hip.MODE_MFMA)
+    got, want = gen.f32(y.numpy()), gen.f32(ref)
+    assert np.all(np.abs(got - want) <= 1e-2 + 2.0 ** -7 * np.abs(want)), np.max(np.abs(got - want))
+    if y32 is not None:
+        ref32 = orc.int8_gemm_rows(w, s, xn)[0]
+        err = np.abs(y32.numpy() - ref32)
+        assert np.all(err <= 1e-2 + 1e-3 * np.abs(ref32)), err.max()
