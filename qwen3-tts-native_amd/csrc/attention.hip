@@ -1028,18 +1028,20 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
         const dim3 score_grid((a.capacity + kScoreLanes - 1) / kScoreLanes, a.query_heads, rows);
         attention_scores_kernel<kExact, kG><<<score_grid, kScoreLanes, 0, stream>>>(a);
     }
-    if (!kExact && a.position_splits > 1 && a.partials != nullptr) {
-        static std::atomic<unsigned long long> configured_split{0};
-        const hipError_t sst = set_dynamic_lds_once(
-            configured_split, reinterpret_cast<const void*>(attention_head_kernel<kExact, kG, true>),
-            static_cast<int>(kLdsLimit));
-        if (sst != hipSuccess) return sst;
-        attention_head_kernel<kExact, kG, true>
-            <<<dim3(a.query_heads * 2, rows, a.position_splits), 64, head_lds, stream>>>(a);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        attention_combine_kernel<<<rows * a.query_heads, kDim, 0, stream>>>(a, a.position_splits);
-        return hipGetLastError();
+    if constexpr (!kExact) {
+        if (a.position_splits > 1 && a.partials != nullptr) {
+            static std::atomic<unsigned long long> configured_split{0};
+            const hipError_t sst = set_dynamic_lds_once(
+                configured_split, reinterpret_cast<const void*>(attention_head_kernel<kExact, kG, true>),
+                static_cast<int>(kLdsLimit));
+            if (sst != hipSuccess) return sst;
+            attention_head_kernel<kExact, kG, true>
+                <<<dim3(a.query_heads * 2, rows, a.position_splits), 64, head_lds, stream>>>(a);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            attention_combine_kernel<<<rows * a.query_heads, kDim, 0, stream>>>(a, a.position_splits);
+            return hipGetLastError();
+        }
     }
     attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
