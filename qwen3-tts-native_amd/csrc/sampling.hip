@@ -10,9 +10,11 @@
 //
 // Design: one 1024-thread block.  The repetition penalty uses an LDS mark
 // table built from the history in one pass (O(history + vocabulary)).  The
-// k-th largest logit is found by a 4-pass 8-bit radix select over monotone
-// 32-bit keys; the survivors (ties included) are ordered by rank counting, a
-// single barrier-free pass that yields the exact total order.  The sampled
+// top `selections` logits are found by an 8-bit radix select over monotone
+// 32-bit keys that stops after the first pass leaving at most 128 keys at or
+// above the chosen bin (bf16 logits: after two passes, up to ties); the
+// survivors are ordered by rank counting (eight lanes per survivor when
+// there are at most 128), which yields the exact total order.  The sampled
 // token can be stored straight into the frame token array and the semantic
 // history (device-resident counters), so a frame needs no host round trip.
 #include "q3_common.hpp"
@@ -23,6 +25,8 @@ namespace {
 constexpr int kSampleThreads = 1024;
 constexpr int kMaxVocabulary = 4096;
 constexpr int kCandidateCap = 1024;
+// survivors ranked by eight lanes each (all 1024 threads)
+constexpr int kRankParallelCap = kSampleThreads / 8;
 
 __device__ __forceinline__ bool before(float av, int ai, float bv, int bi) {
     return (av > bv) || (av == bv && ai < bi);
@@ -84,6 +88,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
     __shared__ int red_i[kSampleThreads / 64];
     __shared__ uint32_t s_prefix;
     __shared__ int s_above;
+    __shared__ int s_total;
     __shared__ int s_count;
     __shared__ int s_best;
     __shared__ double s_target;
@@ -194,9 +199,13 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
             selected = s_best;
         }
     } else {
-        // Threshold key of the selections-th largest value (radix select).
-        // Two histogram buffers: the next pass's is cleared while this
-        // pass's is scanned, two barriers per pass.
+        // Radix select, most significant byte first.  After each pass the
+        // count of keys at or above the chosen bin is known; once it is at
+        // most kRankParallelCap the remaining passes are skipped: every key
+        // whose leading bits reach the bin is a candidate, and the exact
+        // rank counting below orders them (ranks past `selections` are not
+        // used).  Two histogram buffers: the next pass's is cleared while
+        // this pass's is scanned, two barriers per pass.
         if (tid == 0) {
             s_prefix = 0u;
             s_above = 0;
@@ -246,16 +255,21 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
                     if (lane == 63) {  // no bin reaches the count: chosen 0, all bins above
                         s_above = before;
                         s_prefix = prefix;
+                        s_total = before;
                     }
                 } else if (lane == first) {
                     s_above = found_before;
+                    s_total = found_before + h[found];
                     s_prefix = prefix | (static_cast<uint32_t>(255 - 4 * lane - found) << shift);
                 }
             } else if (tid >= 256 && tid < 512) {
                 hist2[256 * (buffer ^ 1) + (tid - 256)] = 0u;  // next pass's buffer
             }
             __syncthreads();
+            if (s_total <= kRankParallelCap) break;  // block-uniform
         }
+        // keys >= threshold: the chosen bin's prefix with the unresolved
+        // low bits zero
         const uint32_t threshold = s_prefix;
         if (tid == 0) s_count = 0;
         __syncthreads();
@@ -272,11 +286,30 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
         }
         __syncthreads();
         const int n = s_count;
-        if (n <= kCandidateCap) {
-            // Rank counting over the survivors: exact total order.  The
-            // packed key compares like (value desc, index asc) (order_key
-            // is monotone, -0 == +0); a 0 pad (below every key) makes the
-            // count even, two keys per LDS read.
+        // Rank counting over the survivors: exact total order.  The packed
+        // key compares like (value desc, index asc) (order_key is monotone,
+        // -0 == +0).
+        if (n <= kRankParallelCap) {
+            // eight lanes per survivor, each over every eighth key; the
+            // integer partial ranks are added by lane swaps
+            const int c = tid >> 3;
+            const int part = tid & 7;
+            int rank = 0;
+            if (c < n) {
+                const unsigned long long mine = cand_key[c];
+#pragma unroll 4
+                for (int j = part; j < n; j += 8) rank += static_cast<int>(cand_key[j] > mine);
+            }
+            rank += __shfl_xor(rank, 1, 64);
+            rank += __shfl_xor(rank, 2, 64);
+            rank += __shfl_xor(rank, 4, 64);
+            if (c < n && part == 0) {
+                sorted_v[rank] = cand_v[c];
+                sorted_i[rank] = cand_i[c];
+            }
+        } else if (n <= kCandidateCap) {
+            // a 0 pad (below every key) makes the count even, two keys per
+            // LDS read
             if (tid == 0) cand_key[n] = 0ull;
             __syncthreads();
             for (int c = tid; c < n; c += kSampleThreads) {
