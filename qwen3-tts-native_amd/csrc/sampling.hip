@@ -28,15 +28,19 @@ constexpr int kCandidateCap = 1024;
 // survivors ranked by eight lanes each (all 1024 threads)
 constexpr int kRankParallelCap = kSampleThreads / 8;
 
-__device__ __forceinline__ bool before(float av, int ai, float bv, int bi) {
-    return (av > bv) || (av == bv && ai < bi);
-}
-
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v);
     if (u == 0x80000000u) u = 0u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// (order key, ~index): a larger packed key ranks earlier -- (value desc,
+// index asc) for ordered values, and a total order for every bit pattern
+// (NaN included), so the ranks are distinct and every token index stays in
+// range.
+__device__ __forceinline__ unsigned long long rank_key(float v, int index) {
+    return (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(~index);
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
@@ -279,8 +283,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
                 if (slot < kCandidateCap) {
                     cand_v[slot] = values[t];
                     cand_i[slot] = t;
-                    cand_key[slot] = (static_cast<unsigned long long>(order_key(values[t])) << 32) |
-                                     static_cast<uint32_t>(~t);
+                    cand_key[slot] = rank_key(values[t], t);
                 }
             }
         }
@@ -326,8 +329,9 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
         } else {
             for (int t = tid; t < V; t += kSampleThreads) {
                 const float v = values[t];
+                const unsigned long long mine = rank_key(v, t);
                 int rank = 0;
-                for (int j = 0; j < V; ++j) rank += before(values[j], j, v, t) ? 1 : 0;
+                for (int j = 0; j < V; ++j) rank += static_cast<int>(rank_key(values[j], j) > mine);
                 sorted_v[rank] = v;
                 sorted_i[rank] = t;
             }

@@ -317,6 +317,31 @@ def test_sampler_topk_matches_oracle(hip, orc, top_k, top_p, vocab, suppress, pe
         state = rstate
 
 
+@pytest.mark.parametrize("pattern", ["all_nan", "half_nan", "nan_and_inf"])
+def test_sampler_nan_logits_select_in_range(hip, pattern):
+    """Logits with NaNs (a diverged model) still yield a token inside the
+    vocabulary, the same one on a repeat, under every selection path: greedy,
+    the direct draw, top-k (the early-stopping radix select) and top-p over
+    the whole vocabulary (the all-keys rank count)."""
+    vocab = 2048
+    raw = np.random.default_rng(3).standard_normal(vocab).astype(np.float32)
+    if pattern == "all_nan":
+        raw[:] = np.nan
+    elif pattern == "half_nan":
+        raw[::2] = np.nan
+    else:
+        raw[::3] = np.nan
+        raw[1::7] = np.inf
+        raw[2::11] = -np.inf
+    logits = gen.bf16(raw)
+    for cfg in (hip.sampling(0, 0, 1.0, 1.0, 1.0), hip.sampling(1, 0, 1.0, 0.9, 1.0),
+                hip.sampling(1, 50, 1.0, 0.9, 1.0), hip.sampling(1, 0, 0.9, 0.9, 1.0),
+                hip.sampling(1, 700, 0.95, 0.9, 1.0)):
+        first, _ = sample_gpu(hip, logits, False, [], cfg, 77)
+        again, _ = sample_gpu(hip, logits, False, [], cfg, 77)
+        assert 0 <= first < vocab and first == again
+
+
 def test_argmax_benchmark_known_answer(hip):
     for vocab in (2048, 3072):
         out = hip.ArgmaxBenchmark()
