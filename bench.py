@@ -675,6 +675,9 @@ def main() -> int:
     ap.add_argument("--only-batched-frames", action="store_true",
                     help="run only the batched-frame workload (N = 8 sessions through the batch entry point); "
                          "for rocprofv3 kernel statistics")
+    ap.add_argument("--only-frames", action="store_true",
+                    help="run only config 5's frame step (prompt, greedy predictor-chain frames, timed top-k "
+                         "frames; no decoder); for rocprofv3 kernel statistics")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the decode path on a single MI355X "
@@ -707,6 +710,9 @@ def main() -> int:
         return 0
     if args.only_streaming:
         print(json.dumps({"streaming": streaming_benchmark(hip)}), flush=True)
+        return 0
+    if args.only_frames:
+        print(json.dumps({"frame_step": frame_benchmark(hip, frames=args.frames)}), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
