@@ -772,6 +772,18 @@ def main() -> int:
                               "weight_gbs": round(ceiling_gbs, 1),
                               "gemv_weight_gbs": round(gemv_weight_gbs, 1),
                               "gemv_fraction_of_ceiling": round(gemv_weight_gbs / ceiling_gbs, 4)}
+    # The same chain as one persistent launch per step (step_chain.hip): the
+    # GEMVs hand their outputs over through tagged words instead of kernel
+    # boundaries; bit-identical outputs on the same inputs.
+    try:
+        chain = step_benchmark(hip, args.steps, args.warmup, use_graph=3)
+        line["persistent_chain"] = {
+            "what": "the step's 112 GEMVs in one persistent launch (tagged-word hand-off between GEMVs)",
+            "ms_per_step": round(chain.milliseconds_per_step, 4),
+            "achieved_gbs": round(chain.algorithmic_bytes_per_step / (chain.milliseconds_per_step * 1e-3) / 1e9, 1),
+            "bit_identical_to_graph": bool(chain.output_checksum == main_run.output_checksum)}
+    except Exception as e:  # report, never hide
+        line["persistent_chain"] = {"error": str(e)}
     line["single_gemv_config1"] = single_gemv(hip)
     line["batched_config4"] = batched(hip, max(args.steps // 4, 5), max(args.warmup // 2, 2))
     if not args.no_frames:

@@ -528,7 +528,9 @@ typedef struct Qwen3TtsStepBenchmarkV1 {
     int32_t steps;
     int32_t use_graph;     /* 0 eager launches, 1 hipGraph per step, 2 the same launches as plain
                               16-byte reads of the weights in one hipGraph (the launch-shape
-                              ceiling; no GEMV arithmetic, rows must be 1) */
+                              ceiling; no GEMV arithmetic, rows must be 1), 3 the whole step as
+                              one persistent launch (rows 1, exact mode, whole chain, hidden
+                              2048 / intermediate 6144 / query 2048 / key-value 1024 only) */
     int32_t kernel_filter; /* 0 whole chain; 1 QKV, 2 O, 3 gate/up, 4 down GEMVs only */
     uint64_t weight_bytes;
     uint64_t algorithmic_bytes_per_step;

@@ -164,7 +164,8 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
     if (b == nullptr || b->struct_size != sizeof(Qwen3TtsStepBenchmarkV1) || b->layers <= 0 || b->hidden <= 0 ||
         b->intermediate <= 0 || b->query_width <= 0 || b->key_value_width <= 0 || b->rows < 1 || b->rows > 8 ||
         b->steps <= 0 || b->warmup < 0 || b->kernel_filter < 0 || b->kernel_filter > 4 || b->use_graph < 0 ||
-        b->use_graph > 2 || (b->use_graph == 2 && b->rows != 1)) {
+        b->use_graph > 3 || (b->use_graph == 2 && b->rows != 1) ||
+        (b->use_graph == 3 && (b->rows != 1 || b->kernel_filter != 0 || b->mode == kModeMfma))) {
         write_error(error, cap, "invalid step benchmark arguments");
         return QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT;
     }
@@ -252,7 +253,38 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
                 }
             }
         };
-        if (b->use_graph >= 1) {
+        // use_graph 3: the whole step as one persistent launch (step_chain.hip).
+        StepChainArgs chain;
+        if (b->use_graph == 3) {
+            bool supported = false;
+            check_hip(talker_step_chain_supported(device_index, &supported), "persistent chain support query");
+            if (!supported) throw DeviceFailure("persistent step chain: the device cannot hold all 256 workgroups at once");
+            chain.weights = w;
+            chain.scales = s;
+            chain.weight_layer_stride = per_layer;
+            chain.scale_layer_stride = scales_per_layer;
+            chain.gain_qkv = gains;
+            chain.gain_gu = gains + H;
+            chain.hidden = hidden;
+            chain.qkv = qkv;
+            chain.act = act;
+            chain.words = mem.get<unsigned long long>(talker_step_chain_words());
+            chain.epoch = mem.get<unsigned>(1);
+            chain.status = mem.get<int>(1);
+            chain.hidden_size = H;
+            chain.intermediate = I;
+            chain.qkv_rows = static_cast<int>(qkv_rows);
+            chain.query_width = QW;
+            chain.layers = L;
+            chain.epsilon = 1.0e-6f;
+            check_hip(hipMemsetAsync(chain.words, 0, talker_step_chain_words() * sizeof(unsigned long long), stream),
+                      "clear chain words");
+            const unsigned one = 1;
+            check_hip(hipMemcpyAsync(chain.epoch, &one, sizeof(one), hipMemcpyHostToDevice, stream), "chain epoch");
+            check_hip(hipMemsetAsync(chain.status, 0, sizeof(int), stream), "chain status");
+            check_hip(hipStreamSynchronize(stream), "chain workspace");
+        }
+        if (b->use_graph == 1 || b->use_graph == 2) {
             check_hip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
             enqueue_step();
             hipGraph_t graph = nullptr;
@@ -262,7 +294,9 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
             check_hip(st, "hipGraphInstantiate");
         }
         auto run = [&] {
-            if (exec) {
+            if (b->use_graph == 3) {
+                check_hip(launch_talker_step_chain(chain, stream), "persistent step chain");
+            } else if (exec) {
                 check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch");
             } else {
                 enqueue_step();
@@ -278,6 +312,11 @@ QWEN3_TTS_API int32_t qwen3_tts_benchmark_talker_step_gemvs(int32_t device_index
         check_hip(hipEventSynchronize(stop), "hipEventSynchronize");
         float ms = 0.0f;
         check_hip(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+        if (b->use_graph == 3) {
+            int status = 0;
+            check_hip(hipMemcpy(&status, chain.status, sizeof(int), hipMemcpyDeviceToHost), "chain status");
+            if (status != 0) throw DeviceFailure("persistent step chain: a wait between GEMVs timed out");
+        }
         // Algorithmic bytes of the filtered chain.
         uint64_t bytes = 0;
         auto gemv_bytes = [&](uint64_t out_rows, uint64_t in, uint64_t out, bool norm, bool rmw) {

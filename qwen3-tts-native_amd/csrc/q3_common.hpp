@@ -174,6 +174,34 @@ struct GemvArgs {
 };
 
 hipError_t launch_int8_gemv(const GemvArgs& args, hipStream_t stream);
+
+// Persistent batch-1 talker-step GEMV chain (step_chain.hip): every layer's
+// QKV (+RMSNorm), O (+residual), gate/up (+RMSNorm, SiLU) and down
+// (+residual) GEMV in one launch, bit-identical to the per-GEMV exact
+// kernels.  Fixed geometry: hidden 2048, intermediate 6144, 4096 fused QKV
+// rows, O input 2048; one launch must finish before the next starts on the
+// same workspace (words / epoch / status).
+struct StepChainArgs {
+    const int8_t* weights = nullptr;   // per layer: qkv, o, gate/up, down (row-major int8)
+    const float* scales = nullptr;     // per layer: 4096 + 2048 + 12288 + 2048
+    size_t weight_layer_stride = 0;    // bytes between layers
+    size_t scale_layer_stride = 0;     // floats between layers
+    const bf16_t* gain_qkv = nullptr;  // [2048] RMSNorm gain before QKV
+    const bf16_t* gain_gu = nullptr;   // [2048] before gate/up
+    size_t gain_layer_stride = 0;      // elements between layers (0: shared)
+    bf16_t* hidden = nullptr;          // [2048] in / out
+    bf16_t* qkv = nullptr;             // [4096] out (last layer)
+    bf16_t* act = nullptr;             // [6144] out (last layer)
+    unsigned long long* words = nullptr;  // talker_step_chain_words() zeroed words
+    unsigned* epoch = nullptr;         // one word, initialized to 1
+    int* status = nullptr;             // one word, 0; set to 1 if a wait timed out
+    int hidden_size = 0, intermediate = 0, qkv_rows = 0, query_width = 0, layers = 0;
+    float epsilon = 1.0e-6f;
+};
+size_t talker_step_chain_words();
+hipError_t launch_talker_step_chain(const StepChainArgs& args, hipStream_t stream);
+// True when every workgroup of the chain can be resident at once on `device`.
+hipError_t talker_step_chain_supported(int device, bool* supported);
 // Exact-order rows of a prompt (any count, no RMSNorm) in one launch.
 hipError_t launch_int8_gemv_prompt_rows(const GemvArgs& a, hipStream_t stream);
 
