@@ -678,6 +678,9 @@ def main() -> int:
     ap.add_argument("--only-frames", action="store_true",
                     help="run only config 5's frame step (prompt, greedy predictor-chain frames, timed top-k "
                          "frames; no decoder); for rocprofv3 kernel statistics")
+    ap.add_argument("--only-chain", action="store_true",
+                    help="run only config 2's chain three ways (the per-GEMV hipGraph, the launch-shape ceiling "
+                         "of plain reads, the persistent launch); for rocprofv3 kernel traces")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the decode path on a single MI355X "
@@ -713,6 +716,15 @@ def main() -> int:
         return 0
     if args.only_frames:
         print(json.dumps({"frame_step": frame_benchmark(hip, frames=args.frames)}), flush=True)
+        return 0
+    if args.only_chain:
+        out = {}
+        for name, graph in (("graph", 1), ("ceiling", 2), ("persistent", 3)):
+            b = step_benchmark(hip, args.steps, args.warmup, use_graph=graph)
+            out[name] = {"ms_per_step": round(b.milliseconds_per_step, 4),
+                         "weight_gbs": round(b.weight_bytes / (b.milliseconds_per_step * 1e-3) / 1e9, 1),
+                         "checksum": f"{b.output_checksum:016x}"}
+        print(json.dumps(out), flush=True)
         return 0
     if args.only_batched_frames:
         print(json.dumps({"batched_frames": batched_frames(hip, ns=(8,))}), flush=True)
