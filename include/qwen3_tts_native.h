@@ -434,9 +434,13 @@ QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention(
  * scratch of 32 MiB held until the process ends; calls needing more (roughly
  * rows * (4 * query_heads + 2 * key_value_heads * 128) * max_sequence_length
  * bytes) fail with QWEN3_TTS_TALKER_STATUS_INVALID_ARGUMENT.  Every call on a
- * device shares that device's scratch: calls that overlap on one device
- * (different streams, or different threads) race and must be serialized by
- * the caller.  Results are identical to qwen3_tts_op_decode_attention. */
+ * device shares that device's scratch, which keeps the last call's contents.
+ * Eager calls are serialized in stream order: a call on another stream (or
+ * thread) than the previous call on the device first makes its stream wait
+ * for that call's kernels.  A call made while its stream is being captured
+ * is ordered by the graph instead: replays of such graphs must not overlap
+ * each other, or eager calls, on one device.  Results are identical to
+ * qwen3_tts_op_decode_attention. */
 QWEN3_TTS_API int32_t qwen3_tts_op_decode_attention_noalloc_v1(
     int32_t exact, const uint16_t* qkv, int32_t qkv_stride, const uint16_t* q_norm,
     const uint16_t* k_norm, const uint16_t* rope_table, float epsilon, uint16_t* const* key_bases,

@@ -528,6 +528,14 @@ hipError_t decode_attention_in(void* scratch, bool exact, const bf16_t* qkv, int
 constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
 void* scratch_address[kMaxDevices] = {};
+// Stream-order guard of each device's scratch: the last eager call's stream
+// and an event recorded after its kernels.
+struct ScratchUse {
+    hipEvent_t done = nullptr;
+    hipStream_t stream = nullptr;
+    bool recorded = false;
+};
+ScratchUse scratch_use[kMaxDevices];
 
 hipError_t scratch_for_current_device(void** out) {
     int device = 0;
@@ -591,11 +599,44 @@ hipError_t launch_decode_attention_op_noalloc(bool exact, const bf16_t* qkv, int
         return hipErrorInvalidValue;
     }
     void* memory = nullptr;
-    const hipError_t st = scratch_for_current_device(&memory);
+    hipError_t st = scratch_for_current_device(&memory);
     if (st != hipSuccess) return st;
-    return decode_attention_in(memory, exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
-                               value_bases, positions, output, rows, query_heads, key_value_heads, head_dimension,
-                               max_sequence_length, stream);
+    auto enqueue = [&] {
+        return decode_attention_in(memory, exact, qkv, qkv_stride, q_norm, k_norm, rope_table, epsilon, key_bases,
+                                   value_bases, positions, output, rows, query_heads, key_value_heads,
+                                   head_dimension, max_sequence_length, stream);
+    };
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    st = hipStreamIsCapturing(stream, &capture);
+    if (st != hipSuccess) return st;
+    if (capture != hipStreamCaptureStatusNone) {
+        // Under capture the graph orders the call; replays of graphs that hold
+        // it must not overlap on one device (documented in the header).
+        return enqueue();
+    }
+    // Eager calls share the device's scratch in stream order: a call on
+    // another stream than the previous one first waits for the previous
+    // call's kernels, then marks its own end.
+    int device = 0;
+    st = hipGetDevice(&device);
+    if (st != hipSuccess) return st;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    ScratchUse& use = scratch_use[device];
+    if (use.done == nullptr) {
+        st = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+        if (st != hipSuccess) return st;
+    }
+    if (use.recorded && use.stream != stream) {
+        st = hipStreamWaitEvent(stream, use.done, 0);
+        if (st != hipSuccess) return st;
+    }
+    st = enqueue();
+    if (st != hipSuccess) return st;
+    st = hipEventRecord(use.done, stream);
+    if (st != hipSuccess) return st;
+    use.stream = stream;
+    use.recorded = true;
+    return hipSuccess;
 }
 
 hipError_t launch_kv_scatter_rows(const bf16_t* rows_data, bf16_t* const* cache_bases,
