@@ -333,3 +333,70 @@ def test_xorshift_zero_state_reseeds(orc):
     x ^= (x << 25) & 0xFFFFFFFFFFFFFFFF
     x ^= x >> 27
     assert s0.value == x
+
+
+def _xorshift64star(state):
+    """Published xorshift64* step (Vigna 2016) with the reference's zero-state
+    reseed (sampling_kernels.cu:53-63): returns (output, next state)."""
+    m = (1 << 64) - 1
+    x = state or 0x9E3779B97F4A7C15
+    x ^= x >> 12
+    x ^= (x << 25) & m
+    x ^= x >> 27
+    return (x * 0x2545F4914F6CDD1D) & m, x
+
+
+def _uniform(state):
+    out, nxt = _xorshift64star(state)
+    return float(np.float32((out >> 11) * 2.0 ** -53)), nxt
+
+
+TOPK_CASE_TOKENS = [400, 100, 300, 200]          # descending logit order
+TOPK_CASE_LOGITS = [2.0, 1.25, 0.5, -0.75]       # exact in bf16
+
+
+def topk_case_boundaries(temperature=1.0):
+    """Cumulative weights of the retained candidates in descending order,
+    normalized: the u values where the draw moves to the next candidate
+    (target = u * total; candidate r is the first with cumulative >= target,
+    sampling_kernels.cu:374-386)."""
+    w = [math.exp(v / temperature - TOPK_CASE_LOGITS[0] / temperature) for v in TOPK_CASE_LOGITS]
+    c = np.cumsum(w)
+    return list(c[:-1] / c[-1])
+
+
+def states_around(boundaries, margin=2e-3, count=1):
+    """RNG states whose draw u lies just below / just above each boundary."""
+    want = {(i, side): [] for i in range(len(boundaries)) for side in (0, 1)}
+    seed = 1
+    while any(len(v) < count for v in want.values()):
+        u, _ = _uniform(seed)
+        for i, b in enumerate(boundaries):
+            if b - margin < u < b and len(want[(i, 0)]) < count:
+                want[(i, 0)].append(seed)
+            if b < u < b + margin and len(want[(i, 1)]) < count:
+                want[(i, 1)].append(seed)
+        seed += 1
+    return want
+
+
+def topk_case_logits():
+    lg = np.full(2048, -8.0, np.float32)
+    lg[TOPK_CASE_TOKENS] = TOPK_CASE_LOGITS
+    return gen.bf16(lg)
+
+
+def test_topk_draw_maps_u_through_the_descending_cumulative_order(orc):
+    """Closed form: four candidates with known weights exp(v - max), a draw
+    u from a known xorshift64* state, and the token is the first candidate
+    in DESCENDING logit order whose cumulative weight reaches u * total --
+    checked just below and just above every boundary (a reversed or
+    ascending order, or an off-by-one at the boundary, fails here)."""
+    bounds = topk_case_boundaries()
+    logits = topk_case_logits()
+    for (i, side), seeds in states_around(bounds).items():
+        for st in seeds:
+            u, nxt = _uniform(st)
+            expected = TOPK_CASE_TOKENS[i + side]
+            tok, state = orc.sample_logits(logits, False, 2150, [], 1, 4, 1.0, 1.0, 1.0, st)
+            assert (tok, state) == (expected, nxt), (i, side, u)

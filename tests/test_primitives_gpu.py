@@ -388,3 +388,17 @@ def test_device_buffer_sequential_upload(hip):
     finally:
         lib.qwen3_tts_device_buffer_destroy(buf)
 
+
+
+def test_sampler_topk_draw_closed_form(hip):
+    """The device sampler on the closed-form top-k case of the oracle tests:
+    draws just below and just above every cumulative boundary pick the
+    candidate the descending cumulative order gives (sampling_kernels.cu:374-386)."""
+    from test_oracle import TOPK_CASE_TOKENS, _uniform, states_around, topk_case_boundaries, topk_case_logits
+
+    logits = topk_case_logits()
+    cfg = hip.sampling(1, 4, 1.0, 1.0, 1.0)
+    for (i, side), seeds in states_around(topk_case_boundaries()).items():
+        for st in seeds:
+            _, nxt = _uniform(st)
+            assert sample_gpu(hip, logits, False, [], cfg, st) == (TOPK_CASE_TOKENS[i + side], nxt), (i, side)
