@@ -194,8 +194,19 @@ void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
  * l, l+32, ...; each vector is a fresh 16-term fmaf chain from 0 that is then
  * added to the lane accumulator; lanes are folded by shuffle-down with
  * offsets 16, 8, 4, 2, 1; lane 0 holds the dot product. */
+/* Test switch (not a reference semantics): every int8 GEMV sums in double
+ * and rounds once -- a second valid summation order, used to measure how far
+ * two valid orders drift apart through a whole model. */
+static int g_double_sum = 0;
+void orc_set_gemv_double_sum(int on) { g_double_sum = on; }
+
 __attribute__((target_clones("fma", "default")))
 static float dot_channel_exact(const int8_t* w, const float* x, int in_features) {
+    if (g_double_sum) {
+        double sum = 0.0;
+        for (int k = 0; k < in_features; ++k) sum += (double)w[k] * (double)x[k];
+        return (float)sum;
+    }
     float acc[32];
     for (int l = 0; l < 32; ++l) acc[l] = 0.0f;
     const int vectors = in_features / 16;

@@ -41,6 +41,8 @@ void orc_quantize_weight_rows(const uint16_t* weight, int8_t* quantized,
 /* Threads used by the GEMV restatements for large matrices (default 1);
  * results do not depend on it. */
 void orc_set_threads(int threads);
+/* Test switch: int8 GEMVs sum in double, rounded once (a second valid order). */
+void orc_set_gemv_double_sum(int on);
 /* Runs fn(ctx, c0, c1) over [0, channels) split across the oracle's threads
  * (one call on the calling thread when work is small). */
 typedef void (*OrcRangeFn)(void* ctx, int c0, int c1);

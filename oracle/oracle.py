@@ -207,6 +207,13 @@ def set_threads(threads: int) -> None:
     lib().orc_set_threads(int(threads))
 
 
+def set_gemv_double_sum(on: bool) -> None:
+    """Test switch: every int8 GEMV sums in double and rounds once -- a
+    second valid summation order (not the reference's), for measuring the
+    drift between two valid orders."""
+    lib().orc_set_gemv_double_sum(int(bool(on)))
+
+
 def bf16_gemm(a_bits, b_bits):
     """c = bf16(a @ b^T) with the oracle's fp32 accumulation (k order)."""
     a = _c(np.atleast_2d(a_bits), np.uint16)
