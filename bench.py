@@ -225,9 +225,11 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
     prompt fills the KV cache so that the timed frames run at context
     max_seq - frames .. max_seq (attention reads up to 1024 positions).
     An end token sampled on the way (random weights) ends the session: it is
-    reset and prefilled again outside the timing, so every run times the same
-    number of frames (each frame is timed on the host: the call returns its
-    codes).
+    reset and prefilled again outside the timing with as many prompt tokens
+    as the session had positions when it ended, so the frames after it run at
+    the same context as without the restart and every run times the same
+    number of frames over the same context range (each frame is timed on the
+    host: the call returns its codes).
     Before the timed frames, `greedy` frames run the code predictor with
     greedy argmax (config 3: the 15-step predictor chain); its GPU time per
     frame is reported separately (it covers 16 passes through the 5 layers:
@@ -243,8 +245,10 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
         hip.call("qwen3_tts_session_create", model, max_seq, 42, C.byref(session), C.byref(smem))
         try:
             rng = np.random.default_rng(1)
-            text = rng.integers(0, cfg.text_vocabulary, prompt).astype(np.int32)
-            codec = rng.integers(0, 2048, prompt).astype(np.int32)
+            # prompt tokens for the longest re-prefill (a restart just before
+            # the last frame); the first prefill takes the first `prompt`
+            text = rng.integers(0, cfg.text_vocabulary, max_seq).astype(np.int32)
+            codec = rng.integers(0, 2048, max_seq).astype(np.int32)
             ts = hip.sampling(1, 50, 1.0, 0.9, 1.05)
             ps = hip.sampling(1, 50, 1.0, 0.9, 1.0)
             pre = hip.PrefillResult()
@@ -265,20 +269,25 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
             timed = 0.0
             seeds = iter(range(100, 1000))
 
-            def restart():
+            def restart(context):
                 # random weights: the end token can come up and end the
                 # session; it is reset and prefilled again outside the timing
+                # up to the context the ended session had reached
                 hip.call("qwen3_tts_session_reset", session, next(seeds))
                 again = hip.PrefillResult()
                 hip.call("qwen3_tts_session_prefill", session, text.ctypes.data_as(C.POINTER(C.c_int32)),
-                         codec.ctypes.data_as(C.POINTER(C.c_int32)), prompt, ts, C.byref(again))
+                         codec.ctypes.data_as(C.POINTER(C.c_int32)), context, ts, C.byref(again))
                 hip.synchronize()
                 return C.c_uint16(again.first_semantic_token)
 
+            context_range = [None, None]
             for f in range(frames + warm + greedy):
                 while semantic.value == cfg.codec_eos_token:
                     eos += 1
-                    semantic = restart()
+                    semantic = restart(prompt + f)
+                if f == warm + greedy:
+                    context_range[0] = prompt + f
+                context_range[1] = prompt + f + 1
                 chain = warm <= f < warm + greedy
                 t0 = time.perf_counter()
                 hip.call("qwen3_tts_session_next_frame", session, semantic, int(trailing[f]), ts,
@@ -302,6 +311,7 @@ def frame_benchmark(hip, frames: int = 200, max_seq: int = 1024, warm: int = 3, 
                 "talker_gpu_ms_per_frame": round(talk_ms / max(done, 1), 3),
                 "prefill_seconds": round(prefill_s, 3),
                 "sessions_restarted_after_end_token": eos,
+                "timed_context_positions": context_range,
                 "sampling": "talker top-k 50 T 0.9 rep 1.05; predictor top-k 50 T 0.9; seed 42",
                 "predictor_chain_config3": predictor_chain_entry(greedy_ms),
             }

@@ -275,6 +275,11 @@ QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_packet_v1(Qwen3TtsCodecConte
                                                               size_t pcm_capacity_samples,
                                                               Qwen3TtsCodecPacketResultV1* result, char* error,
                                                               size_t error_capacity);
+/* Items are validated and queued in array order; the first failure ends the
+ * batch and is returned, and the items before it still complete.  Every
+ * item's result is cleared on entry, so after an error the items whose packet
+ * completed (and advanced their stream) are exactly those with a nonzero
+ * result->frame_count. */
 QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_batch_v1(Qwen3TtsCodecBatchItemV1* items, uint32_t item_count,
                                                              char* error, size_t error_capacity);
 

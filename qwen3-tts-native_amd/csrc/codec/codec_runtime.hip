@@ -1406,6 +1406,11 @@ QWEN3_TTS_CODEC_API int32_t qwen3_tts_codec_process_batch_v1(Qwen3TtsCodecBatchI
     // Every stream's packet is queued on its own HIP stream before any is
     // waited for, so the streams decode concurrently; items complete in
     // order and the first failure ends the batch (earlier items are done).
+    // Results are cleared first: after a failed batch, an item whose packet
+    // completed (and advanced its stream) is the one whose result has a
+    // nonzero frame_count.
+    for (uint32_t i = 0; i < item_count; ++i)
+        if (items[i].result) *items[i].result = Qwen3TtsCodecPacketResultV1{};
     const auto start = std::chrono::steady_clock::now();
     uint32_t slots[QWEN3_TTS_CODEC_MAX_BATCH_STREAMS] = {};
     uint32_t queued = 0;

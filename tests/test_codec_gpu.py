@@ -177,6 +177,38 @@ def test_batch_matches_single_sessions(codec, model):
             assert got[i][1].first_frame_position == a
 
 
+def test_batch_with_an_invalid_item_reports_which_items_completed(codec, model):
+    """An invalid item in the middle ends the batch with an error; the item
+    before it completes and advances its stream (nonzero result frame_count),
+    the invalid one and the one after it do not (cleared results, streams
+    still at frame 0), and the completed item's PCM equals a single session's.
+    Reference semantics: codec_state.cu:4474-4516 processes items in order and
+    returns the first failure."""
+    print("codec batch with invalid middle item", flush=True)
+    streams = [M.random_codes(2, 40 + i) for i in range(3)]
+    sessions = [model.session() for _ in range(3)]
+    codes = [np.ascontiguousarray(c, np.uint16) for c in streams]
+    pcms = [np.zeros(codec.MAX_PACKET_SAMPLES, np.int16) for _ in range(3)]
+    results = [codec.PacketResult() for _ in range(3)]
+    for r in results:
+        r.frame_count = 99  # stale values from an earlier call
+    items = (codec.BatchItem * 3)()
+    for i in range(3):
+        capacity = 0 if i == 1 else codec.MAX_PACKET_SAMPLES  # item 1: PCM capacity too small
+        items[i] = codec.BatchItem(sessions[i].handle, codes[i].ctypes.data, 2, 0, pcms[i].ctypes.data, capacity,
+                                   C.pointer(results[i]))
+    with pytest.raises(codec.CodecError) as e:
+        codec.call("qwen3_tts_codec_session_process_batch_v1", items, 3)
+    assert e.value.status == -1
+    assert [r.frame_count for r in results] == [2, 0, 0]
+    assert [s.state().frame_position for s in sessions] == [2, 0, 0]
+    want, _ = model.session().packet(streams[0])
+    np.testing.assert_array_equal(pcms[0][: results[0].sample_count], want)
+    # the streams that did not consume their packet continue from frame 0
+    again = codec.process_batch(sessions[1:], streams[1:])
+    assert [r.first_frame_position for _, r in again] == [0, 0]
+
+
 def test_reset_restores_a_fresh_stream(model, codes):
     s = model.session()
     first, _ = s.packet(codes[:4])

@@ -400,3 +400,18 @@ def test_topk_draw_maps_u_through_the_descending_cumulative_order(orc):
             expected = TOPK_CASE_TOKENS[i + side]
             tok, state = orc.sample_logits(logits, False, 2150, [], 1, 4, 1.0, 1.0, 1.0, st)
             assert (tok, state) == (expected, nxt), (i, side, u)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_scale_is_correctly_rounded(d):
+    """The attention scale 1.0f/sqrtf(d) (oracle, decode attention and the
+    prefill's causal softmax; the reference's rsqrtf at talker_kernels.cu:136,
+    247, 303, 443, 527) is the float32 nearest to 1/sqrt(d): the exact squares
+    of the midpoints to its neighbours bracket 1/d."""
+    f = np.float32(1.0) / np.sqrt(np.float32(d))
+    lo = Fraction(float(np.nextafter(f, np.float32(0))))
+    hi = Fraction(float(np.nextafter(f, np.float32(1))))
+    x = Fraction(float(f))
+    assert ((lo + x) / 2) ** 2 * d < 1 < ((x + hi) / 2) ** 2 * d
+    if d == 128:
+        assert float(f).hex() == "0x1.6a09e60000000p-4"
