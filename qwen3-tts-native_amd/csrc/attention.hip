@@ -34,6 +34,8 @@
 // The max is order independent, and every exponential is q3_expf of the same
 // operands as the oracle's, so splitting the phases over kernels changes no
 // bit of the result.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "q3_common.hpp"
@@ -86,6 +88,10 @@ struct AttnArgs {
     // launch, which applies the inverse (`inverse`).
     int position_splits;
     float* partials;
+    // Factor on the exact kernel's provisional normalizer (1 in production;
+    // QWEN3_TTS_ATTENTION_SKEW_PROVISIONAL=1 sets 1 + 2^-7 so that the
+    // provisional probabilities differ and the rerun path runs).
+    float provisional_scale;
 };
 
 __device__ __forceinline__ int row_length(const AttnArgs& a, int row) {
@@ -422,6 +428,79 @@ __device__ __forceinline__ float chain8_pairs(float acc, const uint4& w, const f
     return acc;
 }
 
+// The head's scores (fp32, `length` of them) into LDS, 16 loads in flight
+// per lane; returns their maximum in every lane.
+__device__ __forceinline__ float scores_to_lds(const float* src, int length, float* p_lds, int lane) {
+    float m = -INFINITY;
+    for (int base = 0; base < length; base += 16 * 64) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int p = base + u * 64 + lane;
+            t[u] = src[p < length ? p : length - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int p = base + u * 64 + lane;
+            if (p < length) {
+                p_lds[p] = t[u];
+                m = fmaxf(m, t[u]);
+            }
+        }
+    }
+    return wave_max(m);
+}
+
+// Exact softmax over the scores in p_lds (one wave): thread 0 of the
+// reference's block takes one sequential sum (every lane runs the same
+// additions on the same values).  Blocks of 64 positions: the sum over block
+// b is interleaved with the exponentials of block b+1; exponentials past the
+// length are 0 (x + 0 == x for the non-negative running sum).  Then the
+// probabilities bf16(e * (1/sum)), each stored as one half of a bf16 pair
+// (the half of the position's parity, the other 0) up to `padded` (a
+// multiple of 128 >= length); p_lds holds at least ceil(length / 128) * 128
+// + 64 floats (the look-ahead block's exponentials are written as zeros).
+__device__ __forceinline__ void exact_probabilities(float* p_lds, int length, int padded, float maximum, int lane) {
+    auto exps = [&](int block) {
+        const int p = block * 64 + lane;
+        const float t = p_lds[p < length ? p : length - 1];
+        p_lds[p] = p < length ? q3_expf(t - maximum) : 0.0f;
+    };
+    const int blocks = (length + 63) / 64;
+    const float4* all = reinterpret_cast<const float4*>(p_lds);
+    float denominator = 0.0f;
+    exps(0);
+    for (int b = 0; b < blocks; ++b) {
+        float4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = all[b * 16 + u];  // block b, requested first
+        exps(b + 1);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            denominator += v[u].x;
+            denominator += v[u].y;
+            denominator += v[u].z;
+            denominator += v[u].w;
+        }
+    }
+    const float inverse = 1.0f / denominator;
+    // reads first, then the conversions
+    auto convert = [&](int base, auto count) {
+        constexpr int kCount = decltype(count)::value;
+        float t[kCount];
+#pragma unroll
+        for (int u = 0; u < kCount; ++u) t[u] = p_lds[base + u * 64 + lane];
+#pragma unroll
+        for (int u = 0; u < kCount; ++u) {
+            const uint32_t bits = __float_as_uint(round_bf(t[u] * inverse));
+            p_lds[base + u * 64 + lane] = __uint_as_float((lane & 1) ? (bits & 0xffff0000u) : (bits >> 16));
+        }
+    };
+    int base = 0;
+    for (; base + 512 <= padded; base += 512) convert(base, std::integral_constant<int, 8>());
+    for (; base < padded; base += 128) convert(base, std::integral_constant<int, 2>());
+}
+
 template <bool kExact, int kG, bool kSplit = false>
 __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float p_lds[];  // scores, then exponentials, then probabilities
@@ -451,74 +530,13 @@ __global__ __launch_bounds__(64) void attention_head_kernel(AttnArgs a) {
 
     // 2. this head's scores into LDS, 16 loads in flight per lane
     const float* src = a.scores + (static_cast<size_t>(row) * a.query_heads + head) * a.capacity;
-    float m = -INFINITY;
-    for (int base = 0; base < length; base += 16 * 64) {
-        float t[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int p = base + u * 64 + lane;
-            t[u] = src[p < length ? p : length - 1];
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int p = base + u * 64 + lane;
-            if (p < length) {
-                p_lds[p] = t[u];
-                m = fmaxf(m, t[u]);
-            }
-        }
-    }
-    const float maximum = wave_max(m);
+    const float maximum = scores_to_lds(src, length, p_lds, lane);
     const int padded = (length + kRing * 8 - 1) / (kRing * 8) * (kRing * 8);  // end of the last ring round
 
     // 3. exponentials, normalizer, probabilities
     float inverse = 1.0f;
     if constexpr (kExact) {
-        // thread 0 of the reference's block: one sequential sum (every lane
-        // runs the same additions on the same values).  Blocks of 64
-        // positions: the sum over block b is interleaved with the
-        // exponentials of block b+1; exponentials past the length are 0
-        // (x + 0 == x for the non-negative running sum).
-        auto exps = [&](int block) {
-            const int p = block * 64 + lane;
-            const float t = p_lds[p < length ? p : length - 1];
-            p_lds[p] = p < length ? q3_expf(t - maximum) : 0.0f;
-        };
-        const int blocks = (length + 63) / 64;
-        const float4* all = reinterpret_cast<const float4*>(p_lds);
-        float denominator = 0.0f;
-        exps(0);
-        for (int b = 0; b < blocks; ++b) {
-            float4 v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = all[b * 16 + u];  // block b, requested first
-            exps(b + 1);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                denominator += v[u].x;
-                denominator += v[u].y;
-                denominator += v[u].z;
-                denominator += v[u].w;
-            }
-        }
-        inverse = 1.0f / denominator;
-        // probabilities bf16(e * inverse), each stored as one half of a bf16
-        // pair (the half of the position's parity, the other 0); reads first,
-        // then the conversions (padded is a multiple of 128)
-        auto convert = [&](int base, auto count) {
-            constexpr int kCount = decltype(count)::value;
-            float t[kCount];
-#pragma unroll
-            for (int u = 0; u < kCount; ++u) t[u] = p_lds[base + u * 64 + lane];
-#pragma unroll
-            for (int u = 0; u < kCount; ++u) {
-                const uint32_t bits = __float_as_uint(round_bf(t[u] * inverse));
-                p_lds[base + u * 64 + lane] = __uint_as_float((lane & 1) ? (bits & 0xffff0000u) : (bits >> 16));
-            }
-        };
-        int base = 0;
-        for (; base + 512 <= padded; base += 512) convert(base, std::integral_constant<int, 8>());
-        for (; base < padded; base += 128) convert(base, std::integral_constant<int, 2>());
+        exact_probabilities(p_lds, length, padded, maximum, lane);
     } else {
         // 256 strided partials: lane l holds those of threads l, l+64,
         // l+128, l+192; the block_sum tree's levels 128 and 64 are lane
@@ -601,6 +619,356 @@ __global__ __launch_bounds__(kDim) void attention_combine_kernel(AttnArgs a, int
     float acc = p[0];
     for (int s = 1; s < splits; ++s) acc += p[static_cast<size_t>(s) * kDim];
     a.output[rh * kDim + threadIdx.x] = f2bf(acc * a.inverse[rh]);
+}
+
+// ---------------------------------------------------------------------------
+// Exact softmax + values with the value slice staged in LDS (caches whose
+// slice fits): grid (kv heads * 2G slices, rows), 8 waves.
+// Workgroup (kv head, slice, row) covers the kD = 64 / G dimensions
+// [slice * kD, slice * kD + kD) of the kv head for all G query heads of its
+// group; the chain wave (wave G) runs the chain of query head h, dimension
+// slice * kD + j in lane h * kD + j.
+//   1. waves G .. 7 request the slice's values from the blocked cache; wave
+//      h < G brings the scores of query head h into LDS and takes their
+//      maximum;
+//   2. all waves: every exponential of the G heads and a provisional sum of
+//      them (any order);
+//   3. in parallel: wave h < G takes the reference's sequential normalizer
+//      of head h (thread 0's sum in position order, every lane on LDS
+//      broadcast reads kept 48 positions ahead), the exact probabilities
+//      bf16(e * (1/sum)) (once the staging waves are done with the
+//      exponentials) and the first position where one differs from the
+//      provisional one; waves G .. 7 write the provisional probabilities,
+//      store the values (zeros past the length) and stage the rest, each
+//      then adding itself to an LDS count; the chain wave, once the count
+//      is complete, runs the sequential chains with the provisional
+//      probabilities (one bf16 dot2 per position, as in
+//      attention_head_kernel, 32 positions read ahead), keeping the chain's
+//      value at the start of every 64-position block;
+//   4. the chain wave: lanes of a head with a differing position rerun their
+//      chain from the start of its 64-position block with the exact
+//      probabilities.
+// The probabilities are rounded to bf16, so the provisional ones almost
+// always equal the exact ones and the sequential sum and the chain (the
+// kernel's two long dependent sequences, about 4.6 cycles per step) run
+// side by side.  Every output is the chain over the exact probabilities:
+// bit-identical to attention_head_kernel<true, G> (positions past the length
+// add +0).
+// ---------------------------------------------------------------------------
+// Waves per workgroup: G softmax waves, the others (the first of them the
+// chain wave) stage values.
+constexpr int kGroupWaves = 8;
+
+// Positions held per head: whole 128-position blocks (the chain and the sum
+// run over whole 64-position blocks) plus the reads ahead.
+__host__ __device__ constexpr int group_p_stride(int capacity) { return (capacity + 127) / 128 * 128 + 64; }
+
+// LDS: exponentials / exact probabilities [G][p_stride]; provisional
+// probabilities [G][p_stride]; chain checkpoints [64-position blocks][64];
+// the staged value slice [groups of 8 positions + 4 read ahead][kD] x 16 B.
+template <int kG>
+constexpr size_t group_lds_bytes(int capacity) {
+    return 2 * static_cast<size_t>(kG) * group_p_stride(capacity) * sizeof(float) +
+           static_cast<size_t>((capacity + 63) / 64) * 64 * sizeof(float) +
+           static_cast<size_t>((capacity + 127) / 128 * 16 + 4) * (64 / kG) * 16;
+}
+
+#ifdef Q3_ATT_TRACE
+__device__ unsigned long long q3_att_trace[64];
+#define ATT_STAMP(i) \
+    do { \
+        if (blockIdx.x == 0 && blockIdx.y == 0 && (threadIdx.x & 63) == 0 && threadIdx.x < 256) { \
+            q3_att_trace[(i) + 8 * (threadIdx.x >> 6)] = wall_clock64(); \
+            if (threadIdx.x == 128) q3_att_trace[32 + (i)] = clock64(); \
+        } \
+    } while (0)
+#else
+#define ATT_STAMP(i) \
+    do { \
+    } while (0)
+#endif
+
+// Sequential fp32 sum of e[0 .. count) (count a multiple of 64) in index
+// order, every lane the same; LDS broadcast reads of 8 positions per
+// buffer, six buffers (48 positions, 12 reads) ahead of the additions.  e
+// holds at least count + 64 floats (the reads ahead stay inside).
+__device__ __forceinline__ float sequential_sum(const float* e, int count) {
+    const float4* all = static_cast<const float4*>(__builtin_assume_aligned(e, 16));
+    float4 buf[8][2];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        buf[k][0] = all[2 * k];
+        buf[k][1] = all[2 * k + 1];
+    }
+    float s = 0.0f;
+    for (int b4 = 0; b4 < count / 4; b4 += 16) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            buf[(k + 6) & 7][0] = all[b4 + 2 * (k + 6)];
+            buf[(k + 6) & 7][1] = all[b4 + 2 * (k + 6) + 1];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                s += buf[k][r].x;
+                s += buf[k][r].y;
+                s += buf[k][r].z;
+                s += buf[k][r].w;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    return s;
+}
+
+// Waits until `count` (LDS) reaches `target` (bounded: the staging waves
+// always add themselves).
+__device__ __forceinline__ void wait_for_staging(int& count, int target) {
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(&count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Minimum over the wave (every lane active), in every lane.
+__device__ __forceinline__ int wave_min_int(int v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+// One bf16 dot2 step per position of an 8-position group: the position's
+// probability word (p, 0) or (0, p) against the value pair holding it.
+__device__ __forceinline__ float chain_group8(float acc, const uint4& w, const float4& pa, const float4& pb) {
+    const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, __float_as_uint(pv[e])),
+                                              __builtin_bit_cast(bf16x2_t, words[e >> 1]), acc, false);
+    return acc;
+}
+
+// bf16(e * inverse) as the half of a bf16 pair of position p's parity.
+__device__ __forceinline__ float probability_word(float e, float inverse, int p) {
+    const uint32_t bits = __float_as_uint(round_bf(e * inverse));
+    return __uint_as_float((p & 1) ? (bits & 0xffff0000u) : (bits >> 16));
+}
+
+template <int kG>
+__global__ __launch_bounds__(64 * kGroupWaves) void attention_group_kernel(AttnArgs a) {
+    constexpr int kD = 64 / kG;
+    constexpr int kThreads = 64 * kGroupWaves;
+    constexpr int kChainWave = kG;
+    extern __shared__ __align__(16) float lds[];
+    __shared__ float head_max[kG];
+    __shared__ int first_mismatch[kG];
+    __shared__ float provisional_sum[kG];
+    __shared__ int staged_waves;
+    const int row = blockIdx.y;
+    const int kvh = blockIdx.x / (2 * kG);
+    const int d0 = (blockIdx.x % (2 * kG)) * kD;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int length = row_length(a, row);
+    const int p_stride = group_p_stride(a.capacity);
+    float* provisional = lds + kG * p_stride;
+    float* checkpoints = provisional + kG * p_stride;
+    uint4* staged = reinterpret_cast<uint4*>(checkpoints + (a.capacity + 63) / 64 * 64);
+    const int blocks = (length + 63) / 64;  // 64-position blocks of the sum and the chain
+    const int padded = (length + 127) / 128 * 128;
+    const int units = blocks * 8 * kD;  // staged units, zeros past the length
+    const int live_units = (length + 7) / 8 * kD;
+    const bf16_t* vbase = value_run(a, row, kvh, d0);
+    constexpr int kStride = 64 * (kGroupWaves - kG);
+    const int stager = tid - 64 * kG;
+    ATT_STAMP(0);
+    if (tid < kG) provisional_sum[tid] = 0.0f;
+    if (tid == 0) staged_waves = 0;
+
+    // 1. value requests; scores and maxima
+    uint4 t[16];
+    auto request = [&](int first) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int u = min(min(first + j * kStride, units - 1), live_units - 1);
+            t[j] = load_global16(vbase + static_cast<size_t>(u / kD) * kGroupStep + (u % kD) * 8);
+        }
+    };
+    auto store = [&](int first) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int u = first + j * kStride;
+            if (u < units) {
+                const int live = length - (u / kD) * 8;  // positions of the group inside the length
+                uint4 w = t[j];
+                if (live < 8) {
+                    uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        words[k] = 2 * k + 1 < live ? words[k] : (2 * k < live ? (words[k] & 0xffffu) : 0u);
+                    w = make_uint4(words[0], words[1], words[2], words[3]);
+                }
+                staged[u] = w;
+            }
+        }
+    };
+    if (wave < kG) {
+        const int head = kvh * kG + wave;
+        const float* src = a.scores + (static_cast<size_t>(row) * a.query_heads + head) * a.capacity;
+        const float m = scores_to_lds(src, length, lds + wave * p_stride, lane);
+        if (lane == 0) head_max[wave] = m;
+    } else {
+        request(stager);
+    }
+    __syncthreads();
+    ATT_STAMP(1);
+
+    // 2. exponentials (zeros past the length, up to `padded`) and their
+    //    provisional sums (any order); values
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+        float* e = lds + h * p_stride;
+        const float m = head_max[h];
+        constexpr int kPer = 4;
+        float part = 0.0f;
+        for (int first = tid; first < padded; first += kPer * kThreads) {
+            float x[kPer];
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) x[k] = e[min(first + k * kThreads, length - 1)];
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int p = first + k * kThreads;
+                if (p < padded) {
+                    const float ex = p < length ? q3_expf(x[k] - m) : 0.0f;
+                    e[p] = ex;
+                    part += ex;
+                }
+            }
+        }
+        part = wave_sum_down<64>(part);
+        if (lane == 0) atomicAdd(&provisional_sum[h], part);
+    }
+    ATT_STAMP(6);
+    __syncthreads();
+    ATT_STAMP(2);
+    // 3. exact normalizers || provisional probabilities and chains
+    const int h = lane / kD;
+    const int j = lane % kD;
+    const int groups = blocks * 8;
+    float acc = 0.0f;
+    if (wave < kG) {
+        // the exact probabilities of head `wave` and the first position
+        // where one differs from the provisional one
+        float* e = lds + wave * p_stride;
+        const float* q = provisional + wave * p_stride;
+        const float inverse = 1.0f / sequential_sum(e, blocks * 64);
+        // the staging waves have read the exponentials and written the
+        // provisional probabilities before they are overwritten / compared
+        wait_for_staging(staged_waves, kGroupWaves - kG);
+        int mismatch = 0x7fffffff;
+        for (int base = 0; base < padded; base += 4 * 64) {
+            float x[4], y[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int p = min(base + k * 64 + lane, padded - 1);
+                x[k] = e[p];
+                y[k] = q[p];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int p = base + k * 64 + lane;
+                if (p < padded) {
+                    const float word = probability_word(x[k], inverse, p);
+                    e[p] = word;
+                    if (__float_as_uint(word) != __float_as_uint(y[k])) mismatch = min(mismatch, p);
+                }
+            }
+        }
+        mismatch = wave_min_int(mismatch);
+        if (lane == 0) first_mismatch[wave] = mismatch;
+    } else {
+        // provisional probabilities; the values; then the chain wave waits
+        // for every staging wave (an LDS count, bounded)
+#pragma unroll
+        for (int hh = 0; hh < kG; ++hh) {
+            const float* e = lds + hh * p_stride;
+            float* q = provisional + hh * p_stride;
+            const float inverse = a.provisional_scale / provisional_sum[hh];
+            constexpr int kPer = 4;
+            for (int first = stager; first < padded; first += kPer * kStride) {
+                float x[kPer];
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) x[k] = e[min(first + k * kStride, padded - 1)];
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int p = first + k * kStride;
+                    if (p < padded) q[p] = probability_word(x[k], inverse, p);
+                }
+            }
+        }
+        store(stager);
+        for (int first = stager + 16 * kStride; first < units; first += 16 * kStride) {
+            request(first);
+            store(first);
+        }
+        __threadfence_block();  // this wave's LDS writes before its count
+        if (lane == 0) atomicAdd(&staged_waves, 1);
+    }
+    if (wave == kChainWave) {
+        wait_for_staging(staged_waves, kGroupWaves - kG);
+        ATT_STAMP(4);
+        // the chains: one 8-position group per buffer, four buffers (12
+        // reads) ahead; the reads ahead stay inside the slice and the rows
+        const float4* p4 = static_cast<const float4*>(__builtin_assume_aligned(provisional + h * p_stride, 16));
+        const uint4* v = staged + j;
+        uint4 w[8];
+        float4 pa[8], pb[8];
+        auto issue = [&](int slot, int g) {
+            w[slot] = v[g * kD];
+            pa[slot] = p4[2 * g];
+            pb[slot] = p4[2 * g + 1];
+        };
+#pragma unroll
+        for (int k = 0; k < 4; ++k) issue(k, k);
+        for (int g0 = 0; g0 < groups; g0 += 8) {
+            checkpoints[g0 * 8 + lane] = acc;  // the chain before block g0 / 8
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                issue((k + 4) & 7, g0 + k + 4);
+                __builtin_amdgcn_sched_barrier(0);
+                acc = chain_group8(acc, w[k], pa[k], pb[k]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    __syncthreads();
+    ATT_STAMP(3);
+
+    if (wave != kChainWave) return;
+
+    // 4. rerun from the block of the first mismatch with the exact
+    //    probabilities (lanes of heads without one keep their chain)
+    const int bad = first_mismatch[h];
+    const int start = bad < length ? bad / 64 : blocks;
+    int earliest = blocks;
+#pragma unroll
+    for (int hh = 0; hh < kG; ++hh) {
+        const int m = first_mismatch[hh];
+        earliest = min(earliest, m < length ? m / 64 : blocks);
+    }
+    if (earliest < blocks) {
+        const float4* p4 = reinterpret_cast<const float4*>(lds + h * p_stride);
+        const uint4* v = staged + j;
+        for (int b = earliest; b < blocks; ++b) {
+            if (b == start) acc = checkpoints[b * 64 + lane];
+            if (b >= start) {
+                for (int g = b * 8; g < b * 8 + 8; ++g) acc = chain_group8(acc, v[g * kD], p4[2 * g], p4[2 * g + 1]);
+            }
+        }
+    }
+    a.output[(static_cast<size_t>(row) * a.query_heads + kvh * kG + h) * kDim + d0 + j] = f2bf(acc);
+    ATT_STAMP(5);
 }
 
 // ---------------------------------------------------------------------------
@@ -1043,6 +1411,19 @@ hipError_t launch_variant(const AttnArgs& a, int rows, hipStream_t stream) {
             return hipGetLastError();
         }
     }
+    if constexpr (kExact) {
+        const size_t group_lds = group_lds_bytes<kG>(a.capacity);
+        if (group_lds + 256 <= kLdsLimit) {  // + the static maxima and normalizers
+            static std::atomic<unsigned long long> configured_group{0};
+            const hipError_t gst = set_dynamic_lds_once(
+                configured_group, reinterpret_cast<const void*>(attention_group_kernel<kG>),
+                static_cast<int>(kLdsLimit - 256));
+            if (gst != hipSuccess) return gst;
+            attention_group_kernel<kG>
+                <<<dim3(a.key_value_heads * 2 * kG, rows), 64 * kGroupWaves, group_lds, stream>>>(a);
+            return hipGetLastError();
+        }
+    }
     attention_head_kernel<kExact, kG><<<dim3(a.query_heads * 2, rows), 64, head_lds, stream>>>(a);
     return hipGetLastError();
 }
@@ -1078,6 +1459,14 @@ bool valid_shape(int rows, int query_heads, int key_value_heads, int head_dimens
            capacity > 0 && capacity <= kMaxCapacity && workspace != nullptr;
 }
 
+float provisional_scale() {
+    static const float scale = [] {
+        const char* v = std::getenv("QWEN3_TTS_ATTENTION_SKEW_PROVISIONAL");
+        return v != nullptr && std::strcmp(v, "1") == 0 ? 1.0f + 0.0078125f : 1.0f;
+    }();
+    return scale;
+}
+
 AttnArgs base_args(const bf16_t* query, int query_stride, bf16_t* const* key_bases, bf16_t* const* value_bases,
                    const bf16_t* key_cache, const bf16_t* value_cache, const int* positions, int fixed_length,
                    bf16_t* output, int rows, int query_heads, int key_value_heads, int capacity, float* workspace,
@@ -1100,6 +1489,7 @@ AttnArgs base_args(const bf16_t* query, int query_stride, bf16_t* const* key_bas
     a.inverse = workspace + static_cast<size_t>(rows) * query_heads * capacity;
     a.value_stride = value_cache_stride(capacity);
     a.value_strides = value_strides;
+    a.provisional_scale = provisional_scale();
     return a;
 }
 
