@@ -202,6 +202,39 @@ size_t talker_step_chain_words();
 hipError_t launch_talker_step_chain(const StepChainArgs& args, hipStream_t stream);
 // True when every workgroup of the chain can be resident at once on `device`.
 hipError_t talker_step_chain_supported(int device, bool* supported);
+// One code-predictor pass in one persistent launch (pred_chain.hip):
+// small_to_mtp + bias, 5 decoder layers with the exact 16-position
+// attention, and (head_w non-null) the final RMSNorm + codebook head.
+struct PredLayerArgs {
+    const int8_t *qkv_w = nullptr, *o_w = nullptr, *gu_w = nullptr, *d_w = nullptr;
+    const float *qkv_s = nullptr, *o_s = nullptr, *gu_s = nullptr, *d_s = nullptr;
+    const bf16_t *input_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    bf16_t* key_cache = nullptr;    // [16][kv heads * 128]
+    bf16_t* value_cache = nullptr;  // blocked dimension-major, stride 16
+};
+struct PredictorPassArgs {
+    const int8_t* s2m_w = nullptr;
+    const float* s2m_s = nullptr;
+    const bf16_t* s2m_bias = nullptr;
+    const bf16_t* input = nullptr;  // [rows][input_width]
+    const int* input_row = nullptr;  // device row index (nullable: row 0)
+    PredLayerArgs layer[5];
+    const int8_t* head_w = nullptr;  // null: no head
+    const float* head_s = nullptr;
+    const bf16_t* final_norm = nullptr;
+    bf16_t* logits = nullptr;
+    const bf16_t* rope_table = nullptr;
+    const int* position = nullptr;  // device
+    unsigned long long* words = nullptr;  // predictor_pass_words() zeroed words
+    unsigned* epoch = nullptr;            // one word, initialized to 1
+    int* status = nullptr;                // one word, 0; set to 1 if a wait timed out
+    int hidden = 0, intermediate = 0, query_heads = 0, key_value_heads = 0, input_width = 0, vocabulary = 0;
+    int layers = 0, capacity = 0;
+    float epsilon = 1.0e-6f;
+};
+size_t predictor_pass_words();
+hipError_t launch_predictor_pass(const PredictorPassArgs& args, hipStream_t stream);
+hipError_t predictor_pass_supported(int device, bool* supported);
 // Exact-order rows of a prompt (any count, no RMSNorm) in one launch.
 hipError_t launch_int8_gemv_prompt_rows(const GemvArgs& a, hipStream_t stream);
 

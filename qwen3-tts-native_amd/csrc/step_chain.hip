@@ -31,7 +31,7 @@
 //     SiLU gate) in the reference's rounding order.
 // Every wait is bounded: a poll that sees no progress for ~0.1 s sets the
 // status word and every later poll gives up, so the grid always drains.
-#include "gemv_device.hpp"
+#include "chain_device.hpp"
 
 // Build-time diagnostic: -DQ3_CHAIN_TRACE records per-GEMV timestamps of
 // workgroup 0 (poll start / poll done / dot products start / done / outputs
@@ -61,7 +61,6 @@ constexpr int kWordsH = kH / 2, kWordsQkv = kQkv / 2, kWordsAct = kI / 2;
 constexpr int kOffH = 0, kOffQkv = kOffH + kWordsH, kOffH2 = kOffQkv + kWordsQkv, kOffAct = kOffH2 + kWordsH;
 constexpr int kWordsTotal = kOffAct + kWordsAct;
 
-constexpr unsigned long long kPollLimit = 10000000ull;  // 0.1 s of the 100 MHz clock
 
 struct ChainArgs {
     const int8_t* weights;       // per layer: qkv [4096][2048], o [2048][2048], gate/up [12288][2048], down [2048][6144]
@@ -84,87 +83,17 @@ struct ChainArgs {
 
 // ----------------------------------------------------------------- helpers
 
-__device__ __forceinline__ unsigned long long pack_word(unsigned lo, unsigned hi, unsigned tag) {
-    return (static_cast<unsigned long long>(tag) << 32) | (hi << 16) | (lo & 0xffffu);
-}
-
-__device__ __forceinline__ void publish(unsigned long long* dst, unsigned long long word) {
-    __hip_atomic_store(dst, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Poll kWords tagged words (this poller thread's share: words pt + 256 i)
-// until all carry `tag`, then store their payloads to LDS.  All loads of a
-// round are in flight together; only stale words are re-read.
-// LDS layout of a stage input of K values as fp32: element k of vector
-// v = k / 16 sits in quarter q = (k % 16) / 4 at [q][v][k % 4], so the
-// 16-byte reads of one quarter by consecutive lanes (consecutive vectors)
-// are contiguous: no bank conflicts.
-template <int kK>
-__device__ __forceinline__ int x_index(int k) {
-    return ((k & 15) >> 2) * (kK / 4) + (k >> 4) * 4 + (k & 3);
-}
+using chain_detail::chain_at;
+using chain_detail::from_upper_half;
+using chain_detail::pack_word;
+using chain_detail::publish;
+using chain_detail::x_index;
 
 template <int kWords>
 __device__ __forceinline__ void poll_words(const unsigned long long* src, unsigned tag, float* x, int pt,
                                            int* status) {
     CHAIN_TRACE(if (chain_nosync) return;)
-    constexpr int kPer = kWords / (64 * kPollWaves);
-    static_assert(kPer * 64 * kPollWaves == kWords, "whole rounds");
-    unsigned long long v[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-        v[i] = __hip_atomic_load(src + pt + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long t0 = 0;
-    int spins = 0;
-    while (true) {
-        bool stale = false;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) stale |= static_cast<unsigned>(v[i] >> 32) != tag;
-        if (!stale) break;
-        if (t0 == 0) t0 = wall_clock64();
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (static_cast<unsigned>(v[i] >> 32) != tag)
-                v[i] = __hip_atomic_load(src + pt + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((++spins & 63) == 0) {
-            if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-            if (wall_clock64() - t0 > kPollLimit) {
-                __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const uint32_t pair = static_cast<uint32_t>(v[i]);
-        *reinterpret_cast<float2*>(x + x_index<2 * kWords>(2 * (pt + 256 * i))) =
-            make_float2(__uint_as_float(pair << 16), __uint_as_float(pair & 0xffff0000u));
-    }
-}
-
-// One 16-byte weight vector against its 16 activations (fp32 in LDS, the
-// exact values of the bf16 inputs): the reference's fresh 16-term fmaf chain
-// (chain16, int8_gemv.cu:99-112).  Staging the input as fp32 takes the bf16
-// -> fp32 conversion off the dot products: per weight byte one int8 -> fp32
-// conversion and one fma.
-template <int kK>
-__device__ __forceinline__ float chain_at(const int4& w, const float* x, int vec) {
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 q = reinterpret_cast<const float4*>(x + i * (kK / 4))[vec];
-        v[4 * i] = q.x;
-        v[4 * i + 1] = q.y;
-        v[4 * i + 2] = q.z;
-        v[4 * i + 3] = q.w;
-    }
-    return chain16(w, v);
-}
-
-// Lanes 0-31 receive lanes 32-63's value.
-__device__ __forceinline__ float from_upper_half(float v) {
-    const unsigned bits = __float_as_uint(v);
-    return __uint_as_float(__builtin_amdgcn_permlane32_swap(bits, bits, false, false)[1]);
+    chain_detail::poll_words<kWords>(src, tag, x, pt, status);
 }
 
 // ------------------------------------------------------------ compute waves

@@ -593,6 +593,8 @@ public:
             host_bases_ = bases;
             std::vector<int> init(64, 0);
             for (int p = 0; p < kCodebooks; ++p) init[20 + p] = p;
+            init[41] = 1;  // predictor pass epoch
+            setup_predictor_chain();
             check_hip(hipMemcpy(ints_.as<void>(), init.data(), init.size() * sizeof(int), hipMemcpyHostToDevice), "init session ints");
             check_hip(hipHostMalloc(reinterpret_cast<void**>(&pinned_), 256, hipHostMallocDefault), "hipHostMalloc(session)");
             reset(seed);
@@ -894,6 +896,10 @@ public:
             check_hip(hipEventRecord(predictor_start_, stream_), "hipEventRecord(predictor start)");
             launch_graph(predictor_graph_, ps, [&] { enqueue_predictor(ps); });
             check_hip(hipEventRecord(predictor_stop_, stream_), "hipEventRecord(predictor stop)");
+            if (pred_chain_) {
+                check_hip(hipMemcpyAsync(pinned_ + 20, ints_.as<int>() + 40, sizeof(int), hipMemcpyDeviceToHost, stream_),
+                          "copy predictor pass status");
+            }
             check_hip(hipEventRecord(codes_ready_, stream_), "hipEventRecord(codes ready)");
             if (copy_codes) {
                 check_hip(hipMemcpyAsync(pinned_codes(), codes_.as<void>(), kCodebooks * sizeof(uint16_t), hipMemcpyDeviceToHost, stream_), "copy codec frame");
@@ -928,6 +934,10 @@ public:
         }
         check_hip(hipEventSynchronize(semantic_ready_), "hipEventSynchronize(semantic ready)");
         ++host_syncs_;
+        if (pred_chain_ && pinned_[20] != 0) {
+            poisoned_ = true;
+            throw DeviceFailure("predictor pass: a stage input did not arrive within its bound");
+        }
         const int next = validated_token();
         Qwen3TtsCodecFrameResult r{};
         r.talker_position = pending_position_;
@@ -1199,8 +1209,71 @@ private:
         ++history_count_;
     }
 
+    // The persistent predictor pass runs the predictor at the geometry it is
+    // built for (the reference's: talker hidden 2048; predictor 1024 / 3072,
+    // 16 / 8 heads, 5 layers, 2048-entry codebooks) on a device where all
+    // its workgroups fit at once; QWEN3_TTS_DISABLE_PREDICTOR_CHAIN=1 keeps
+    // the per-kernel sequence.  Both give the same bits.
+    void setup_predictor_chain() {
+        const Dims& P = cfg_.predictor;
+        const char* off = std::getenv("QWEN3_TTS_DISABLE_PREDICTOR_CHAIN");
+        bool supported = false;
+        if (off != nullptr && std::strcmp(off, "1") == 0) return;
+        if (cfg_.talker.hidden != 2048 || P.hidden != 1024 || P.intermediate != 3072 || P.query_heads != 16 ||
+            P.key_value_heads != 8 || P.head_dimension != 128 || P.layers != 5 || cfg_.predictor_vocab != 2048) {
+            return;
+        }
+        check_hip(predictor_pass_supported(device_, &supported), "predictor pass support");
+        if (!supported) return;
+        pred_words_ = DeviceBuffer(predictor_pass_words() * sizeof(unsigned long long));
+        check_hip(hipMemset(pred_words_.as<void>(), 0, pred_words_.bytes()), "zero predictor words");
+        const int T2 = 2 * cfg_.talker.layers;
+        PredictorPassArgs& c = pass_;
+        c.s2m_w = m_.small_to_mtp_.data;
+        c.s2m_s = m_.small_to_mtp_.scales;
+        c.s2m_bias = m_.small_to_mtp_bias_;
+        for (int l = 0; l < P.layers; ++l) {
+            const Layer& L = m_.predictor_layers_[l];
+            PredLayerArgs& d = c.layer[l];
+            d.qkv_w = L.qkv.data;
+            d.qkv_s = L.qkv.scales;
+            d.o_w = L.o.data;
+            d.o_s = L.o.scales;
+            d.gu_w = L.gate_up.data;
+            d.gu_s = L.gate_up.scales;
+            d.d_w = L.down.data;
+            d.d_s = L.down.scales;
+            d.input_norm = L.input_norm;
+            d.post_norm = L.post_norm;
+            d.q_norm = L.q_norm;
+            d.k_norm = L.k_norm;
+            d.key_cache = host_bases_[T2 + l];
+            d.value_cache = host_bases_[T2 + P.layers + l];
+        }
+        c.final_norm = m_.predictor_norm_;
+        c.logits = logits_.as<bf16_t>();
+        c.rope_table = m_.rope_table_.as<bf16_t>();
+        c.words = pred_words_.as<unsigned long long>();
+        c.epoch = reinterpret_cast<unsigned*>(ints_.as<int>() + 41);
+        c.status = ints_.as<int>() + 40;
+        c.hidden = P.hidden;
+        c.intermediate = P.intermediate;
+        c.query_heads = P.query_heads;
+        c.key_value_heads = P.key_value_heads;
+        c.input_width = cfg_.talker.hidden;
+        c.vocabulary = cfg_.predictor_vocab;
+        c.layers = P.layers;
+        c.capacity = kCodebooks;
+        c.epsilon = cfg_.eps;
+        pred_chain_ = true;
+    }
+
     // Predictor: 16 positions (talker.cu:1153-1220).
     void enqueue_predictor(const SamplingParams& ps) {
+        if (pred_chain_) {
+            enqueue_predictor_chain(ps);
+            return;
+        }
         const int H = cfg_.talker.hidden;
         const int PH = cfg_.predictor.hidden;
         const int PV = cfg_.predictor_vocab;
@@ -1221,6 +1294,31 @@ private:
             if (p >= 1) {
                 Gemv(m_.predictor_heads_[p - 1], p_hidden_.as<bf16_t>(), PH, PV, kEpiStore)
                     .norm(m_.predictor_norm_, cfg_.eps).to(logits_.as<bf16_t>()).run(stream_, "predictor head");
+                check_hip(launch_sample_logits_ex(logits_.as<bf16_t>(), PV, false, cfg_.codec_eos, history_.as<int>(),
+                                                  history_count_ptr(), 0, ps.do_sample, ps.top_k, ps.top_p, ps.temperature,
+                                                  ps.penalty, random_state_.as<uint64_t>(), sampled_ptr(), frame_tokens(),
+                                                  nullptr, p, nullptr, nullptr, stream_),
+                          "predictor sample");
+            }
+        }
+        check_hip(launch_pack_frame_codes(frame_tokens(), codes_.as<uint16_t>(), kCodebooks, stream_), "pack frame codes");
+    }
+
+    // The same 16 passes, one persistent launch each (the inputs of
+    // small_to_mtp as above), each followed by its sampler.
+    void enqueue_predictor_chain(const SamplingParams& ps) {
+        const int PV = cfg_.predictor_vocab;
+        for (int p = 0; p < kCodebooks; ++p) {
+            PredictorPassArgs c = pass_;
+            c.input = p == 0 ? last_hidden_.as<bf16_t>() : p == 1 ? m_.codec_embedding_ : m_.predictor_embeddings_[p - 2];
+            c.input_row = p == 0 ? nullptr : frame_tokens() + (p == 1 ? 0 : p - 1);
+            c.position = pred_positions() + p;
+            if (p >= 1) {
+                c.head_w = m_.predictor_heads_[p - 1].data;
+                c.head_s = m_.predictor_heads_[p - 1].scales;
+            }
+            check_hip(launch_predictor_pass(c, stream_), "predictor pass");
+            if (p >= 1) {
                 check_hip(launch_sample_logits_ex(logits_.as<bf16_t>(), PV, false, cfg_.codec_eos, history_.as<int>(),
                                                   history_count_ptr(), 0, ps.do_sample, ps.top_k, ps.top_p, ps.temperature,
                                                   ps.penalty, random_state_.as<uint64_t>(), sampled_ptr(), frame_tokens(),
@@ -1276,8 +1374,13 @@ private:
     DeviceBuffer talker_k_, talker_v_, pred_k_, pred_v_;
     DeviceBuffer hidden_, p_hidden_, qkv_, attn_, attn_scratch_, act_, logits_, proj_, last_hidden_;
     DeviceBuffer ints_, history_, codes_, random_state_, kv_bases_;
+    // Persistent predictor pass (pred_chain.hip): its tagged words, and the
+    // static part of its arguments; ints_[40] status, ints_[41] epoch.
+    DeviceBuffer pred_words_;
+    PredictorPassArgs pass_{};
+    bool pred_chain_ = false;
     std::vector<bf16_t*> host_bases_;
-    int* pinned_ = nullptr;  // [0] sampled token, [1] text token, [8..] codes (u16)
+    int* pinned_ = nullptr;  // [0] sampled token, [1] text token, [8..] codes (u16), [20] predictor pass status
     Graph predictor_graph_, talker_graph_;
     PrefillBuffers prefill_;
     int position_ = 0;

@@ -144,6 +144,42 @@ def test_voicedesign_geometry_frames(hip, orc, full):
         hip.load().qwen3_tts_session_destroy(s)
 
 
+def test_voicedesign_geometry_predictor_pass_chain_matches_kernel_sequence(hip, full, monkeypatch):
+    """The persistent predictor pass (one launch per predictor step,
+    csrc/pred_chain.hip; the default at this geometry) against the
+    per-kernel sequence of the same steps (QWEN3_TTS_DISABLE_PREDICTOR_CHAIN=1
+    when the session is created): six frames, greedy and top-k, give the
+    same codes and next tokens bit for bit (the test above pins the chain
+    itself to the oracle)."""
+    model, _ = full
+    runs = []
+    for disable in ("0", "1"):
+        monkeypatch.setenv("QWEN3_TTS_DISABLE_PREDICTOR_CHAIN", disable)
+        s = session(hip, model, 7)
+        try:
+            text, codec = prompt(7)
+            pre = hip.PrefillResult()
+            hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                     codec.ctypes.data_as(C.POINTER(C.c_int32)), PROMPT, hip.SamplingConfig(*GREEDY), C.byref(pre))
+            sem, out = pre.first_semantic_token, []
+            for f, (ts, ps) in enumerate(SCHEDULE + SCHEDULE[2:]):
+                if sem == VOICEDESIGN["codec_eos_token"]:
+                    break
+                print(f"[geometry] predictor chain {disable} frame {f}", flush=True)
+                codes = (C.c_uint16 * 16)()
+                nxt = C.c_uint16()
+                info = hip.CodecFrameInfo()
+                hip.call("qwen3_tts_session_next_frame", s, sem, 200 + f, hip.SamplingConfig(*ts),
+                         hip.SamplingConfig(*ps), codes, 16, C.byref(nxt), C.byref(info))
+                out.append((list(codes), nxt.value))
+                sem = nxt.value
+            runs.append(out)
+        finally:
+            hip.load().qwen3_tts_session_destroy(s)
+    assert len(runs[0]) >= 2
+    assert runs[0] == runs[1]
+
+
 def test_voicedesign_geometry_batched_exact(hip, orc, full, monkeypatch):
     monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
     model, om = full
