@@ -258,8 +258,18 @@ __global__ __launch_bounds__(64) void conv_gemm_reduce_kernel(ConvGemmArgs g) {
     const size_t tiles = (size_t)gridDim.x * gridDim.y;
     const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
     floatx4 sum = *reinterpret_cast<const floatx4*>(partial_slot<TM, TN>(g, tiles, tile, 0, wave, i, j, lane));
-    for (int z = 1; z < g.splits; ++z)
-        sum += *reinterpret_cast<const floatx4*>(partial_slot<TM, TN>(g, tiles, tile, z, wave, i, j, lane));
+    // eight slices' loads in flight together, added in slice order
+    for (int z0 = 1; z0 < g.splits; z0 += 8) {
+        floatx4 v[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int z = min(z0 + d, g.splits - 1);
+            v[d] = *reinterpret_cast<const floatx4*>(partial_slot<TM, TN>(g, tiles, tile, z, wave, i, j, lane));
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+            if (z0 + d < g.splits) sum += v[d];
+    }
     subtile_epilogue<TM, TN, WM, WN>(g, sum, blockIdx.y, blockIdx.x, wave, i, j, lane);
 }
 
