@@ -595,6 +595,11 @@ public:
             for (int p = 0; p < kCodebooks; ++p) init[20 + p] = p;
             init[41] = 1;  // predictor pass epoch
             setup_predictor_chain();
+            // test switch: the predictor pass starts with its status word
+            // set, so every stage wait gives up at once (the frame then
+            // reports the failure); no wait is ever unbounded
+            const char* give_up = std::getenv("QWEN3_TTS_PREDICTOR_CHAIN_TEST_GIVE_UP");
+            if (pred_chain_ && give_up != nullptr && std::strcmp(give_up, "1") == 0) init[40] = 1;
             check_hip(hipMemcpy(ints_.as<void>(), init.data(), init.size() * sizeof(int), hipMemcpyHostToDevice), "init session ints");
             check_hip(hipHostMalloc(reinterpret_cast<void**>(&pinned_), 256, hipHostMallocDefault), "hipHostMalloc(session)");
             reset(seed);

@@ -180,6 +180,36 @@ def test_voicedesign_geometry_predictor_pass_chain_matches_kernel_sequence(hip, 
     assert runs[0] == runs[1]
 
 
+def test_voicedesign_geometry_predictor_pass_waits_are_bounded(hip, full, monkeypatch):
+    """Failure handling of the persistent predictor pass, forced from the
+    host: the session starts with the pass's status word set
+    (QWEN3_TTS_PREDICTOR_CHAIN_TEST_GIVE_UP=1), so every stage wait gives up
+    after its first round instead of waiting; the launches drain, and the
+    frame reports a device failure (QWEN3_TTS_TALKER_STATUS_CUDA) with the
+    pass named, after which the session refuses further frames."""
+    model, _ = full
+    monkeypatch.setenv("QWEN3_TTS_PREDICTOR_CHAIN_TEST_GIVE_UP", "1")
+    s = session(hip, model, 9)
+    try:
+        text, codec = prompt(9)
+        pre = hip.PrefillResult()
+        hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                 codec.ctypes.data_as(C.POINTER(C.c_int32)), PROMPT, hip.SamplingConfig(*GREEDY), C.byref(pre))
+        codes = (C.c_uint16 * 16)()
+        nxt = C.c_uint16()
+        info = hip.CodecFrameInfo()
+        print("[geometry] predictor pass with its waits forced to give up", flush=True)
+        with pytest.raises(hip.Qwen3TtsError) as e:
+            hip.call("qwen3_tts_session_next_frame", s, pre.first_semantic_token, 100, hip.SamplingConfig(*GREEDY),
+                     hip.SamplingConfig(*GREEDY), codes, 16, C.byref(nxt), C.byref(info))
+        assert e.value.status == -2 and "predictor pass" in str(e.value)
+        with pytest.raises(hip.Qwen3TtsError):
+            hip.call("qwen3_tts_session_next_frame", s, pre.first_semantic_token, 101, hip.SamplingConfig(*GREEDY),
+                     hip.SamplingConfig(*GREEDY), codes, 16, C.byref(nxt), C.byref(info))
+    finally:
+        hip.load().qwen3_tts_session_destroy(s)
+
+
 def test_voicedesign_geometry_batched_exact(hip, orc, full, monkeypatch):
     monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
     model, om = full
