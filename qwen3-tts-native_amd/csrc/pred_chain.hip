@@ -32,6 +32,8 @@
 //     reference's 256-thread order and apply the epilogues.
 // Every wait is bounded: a poll that sees no progress for ~0.1 s sets the
 // status word and every later poll gives up, so the grid always drains.
+#include <mutex>
+
 #include "chain_device.hpp"
 #include "short_attention.hpp"
 
@@ -589,6 +591,42 @@ hipError_t launch_predictor_pass(const PredictorPassArgs& c, hipStream_t stream)
     a.status = c.status;
     hipLaunchKernelGGL(predictor_pass_kernel, dim3(kGrid), dim3(kPassThreads), 0, stream, a);
     return hipGetLastError();
+}
+
+struct PassOrderSlot {
+    std::mutex lock;
+    hipEvent_t done = nullptr;  // after the device's last predictor launches
+    hipStream_t stream = nullptr;
+    bool recorded = false;
+};
+namespace {
+PassOrderSlot pass_order[64];
+}  // namespace
+
+PredictorPassOrder::PredictorPassOrder(int device, hipStream_t stream) : stream_(stream) {
+    if (device < 0 || device >= 64) {
+        status_ = hipErrorInvalidDevice;
+        return;
+    }
+    slot_ = &pass_order[device];
+    slot_->lock.lock();
+    if (slot_->done == nullptr) status_ = hipEventCreateWithFlags(&slot_->done, hipEventDisableTiming);
+    if (status_ == hipSuccess && slot_->recorded && slot_->stream != stream)
+        status_ = hipStreamWaitEvent(stream, slot_->done, 0);
+}
+
+hipError_t PredictorPassOrder::done() {
+    if (slot_ == nullptr || status_ != hipSuccess) return status_;
+    status_ = hipEventRecord(slot_->done, stream_);
+    if (status_ == hipSuccess) {
+        slot_->stream = stream_;
+        slot_->recorded = true;
+    }
+    return status_;
+}
+
+PredictorPassOrder::~PredictorPassOrder() {
+    if (slot_ != nullptr) slot_->lock.unlock();
 }
 
 hipError_t predictor_pass_supported(int device, bool* supported) {

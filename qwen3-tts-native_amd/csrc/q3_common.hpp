@@ -235,6 +235,25 @@ struct PredictorPassArgs {
 size_t predictor_pass_words();
 hipError_t launch_predictor_pass(const PredictorPassArgs& args, hipStream_t stream);
 hipError_t predictor_pass_supported(int device, bool* supported);
+// Orders the persistent predictor launches of every session on a device
+// (two of them side by side could each hold part of the CUs and wait for
+// workgroups that cannot start): constructed before a stream's predictor
+// launches, it makes the stream wait for the device's previous ones when
+// they were another stream's; done() after them records their end.  Holds
+// the device's lock from construction to destruction.
+class PredictorPassOrder {
+public:
+    PredictorPassOrder(int device, hipStream_t stream);
+    ~PredictorPassOrder();
+    PredictorPassOrder(const PredictorPassOrder&) = delete;
+    PredictorPassOrder& operator=(const PredictorPassOrder&) = delete;
+    hipError_t status() const { return status_; }
+    hipError_t done();
+private:
+    struct PassOrderSlot* slot_ = nullptr;
+    hipStream_t stream_ = nullptr;
+    hipError_t status_ = hipSuccess;
+};
 // Exact-order rows of a prompt (any count, no RMSNorm) in one launch.
 hipError_t launch_int8_gemv_prompt_rows(const GemvArgs& a, hipStream_t stream);
 

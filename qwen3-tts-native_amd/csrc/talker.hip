@@ -602,6 +602,7 @@ public:
             if (pred_chain_ && give_up != nullptr && std::strcmp(give_up, "1") == 0) init[40] = 1;
             check_hip(hipMemcpy(ints_.as<void>(), init.data(), init.size() * sizeof(int), hipMemcpyHostToDevice), "init session ints");
             check_hip(hipHostMalloc(reinterpret_cast<void**>(&pinned_), 256, hipHostMallocDefault), "hipHostMalloc(session)");
+            std::memset(pinned_, 0, 256);
             reset(seed);
         } catch (...) {
             release();
@@ -892,18 +893,31 @@ public:
         const uint64_t lease = next_lease_++;
         if (next_lease_ == 0) next_lease_ = 1;
         frame_in_flight_ = true;
+        pending_pass_status_ = false;
         pending_copy_ = copy_codes;
         pending_lease_ = lease;
         pending_position_ = static_cast<uint32_t>(position_);
         try {
             pinned_[1] = text_token;
             check_hip(hipMemcpyAsync(ints_.as<int>() + 3, &pinned_[1], sizeof(int), hipMemcpyHostToDevice, stream_), "upload text token");
-            check_hip(hipEventRecord(predictor_start_, stream_), "hipEventRecord(predictor start)");
-            launch_graph(predictor_graph_, ps, [&] { enqueue_predictor(ps); });
-            check_hip(hipEventRecord(predictor_stop_, stream_), "hipEventRecord(predictor stop)");
             if (pred_chain_) {
+                // The persistent passes need every CU at once: the passes of
+                // all sessions on the device run one after another (a
+                // per-device order of their launches; no wait when the last
+                // ones were this stream's own).
+                PredictorPassOrder order(device_, stream_);
+                check_hip(order.status(), "predictor pass order");
+                check_hip(hipEventRecord(predictor_start_, stream_), "hipEventRecord(predictor start)");
+                launch_graph(predictor_graph_, ps, [&] { enqueue_predictor(ps); });
+                check_hip(hipEventRecord(predictor_stop_, stream_), "hipEventRecord(predictor stop)");
+                check_hip(order.done(), "predictor pass order");
                 check_hip(hipMemcpyAsync(pinned_ + 20, ints_.as<int>() + 40, sizeof(int), hipMemcpyDeviceToHost, stream_),
                           "copy predictor pass status");
+                pending_pass_status_ = true;
+            } else {
+                check_hip(hipEventRecord(predictor_start_, stream_), "hipEventRecord(predictor start)");
+                launch_graph(predictor_graph_, ps, [&] { enqueue_predictor(ps); });
+                check_hip(hipEventRecord(predictor_stop_, stream_), "hipEventRecord(predictor stop)");
             }
             check_hip(hipEventRecord(codes_ready_, stream_), "hipEventRecord(codes ready)");
             if (copy_codes) {
@@ -939,7 +953,9 @@ public:
         }
         check_hip(hipEventSynchronize(semantic_ready_), "hipEventSynchronize(semantic ready)");
         ++host_syncs_;
-        if (pred_chain_ && pinned_[20] != 0) {
+        const bool pass_status = pending_pass_status_;  // this frame ran the persistent predictor passes
+        pending_pass_status_ = false;
+        if (pass_status && pinned_[20] != 0) {
             poisoned_ = true;
             throw DeviceFailure("predictor pass: a stage input did not arrive within its bound");
         }
@@ -1121,8 +1137,11 @@ private:
     };
 
     // Capture on the second use of a sampling configuration, replay after.
+    // The work runs on `exec` (default: the session's stream); a capture is
+    // always taken on the session's own stream.
     template <typename Enqueue>
-    void launch_graph(Graph& g, const SamplingParams& key, Enqueue&& enqueue) {
+    void launch_graph(Graph& g, const SamplingParams& key, Enqueue&& enqueue, hipStream_t exec = nullptr) {
+        if (exec == nullptr) exec = stream_;
         if (g.have_key && !(g.key == key)) {
             // the old graph may still be queued on the stream
             if (g.exec) check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize(replace graph)");
@@ -1133,11 +1152,19 @@ private:
         g.have_key = true;
         g.key = key;
         if (g.exec != nullptr) {
-            check_hip(hipGraphLaunch(g.exec, stream_), "hipGraphLaunch");
+            check_hip(hipGraphLaunch(g.exec, exec), "hipGraphLaunch");
             return;
         }
         if (g.eager_runs < 1 || !graphs_enabled()) {
-            enqueue();
+            const hipStream_t own = stream_;
+            stream_ = exec;  // the enqueue functions launch on stream_
+            try {
+                enqueue();
+            } catch (...) {
+                stream_ = own;
+                throw;
+            }
+            stream_ = own;
             ++g.eager_runs;
             return;
         }
@@ -1155,7 +1182,7 @@ private:
         const hipError_t inst = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         check_hip(inst, "hipGraphInstantiate");
-        check_hip(hipGraphLaunch(g.exec, stream_), "hipGraphLaunch");
+        check_hip(hipGraphLaunch(g.exec, exec), "hipGraphLaunch");
     }
 
     static bool graphs_enabled() {
@@ -1393,7 +1420,7 @@ private:
     uint64_t frames_ = 0, device_samples_ = 0, host_syncs_ = 0;
     uint16_t semantic_ = 0;
     Qwen3TtsTalkerPhase phase_ = QWEN3_TTS_TALKER_CREATED;
-    bool frame_in_flight_ = false, pending_copy_ = false, poisoned_ = false;
+    bool frame_in_flight_ = false, pending_copy_ = false, poisoned_ = false, pending_pass_status_ = false;
     uint64_t next_lease_ = 1, pending_lease_ = 0;
     uint32_t pending_position_ = 0;
 
@@ -1540,6 +1567,7 @@ public:
             const uint64_t lease = c->next_lease_++;
             if (c->next_lease_ == 0) c->next_lease_ = 1;
             c->frame_in_flight_ = true;
+            c->pending_pass_status_ = false;
             c->pending_copy_ = false;
             c->pending_lease_ = lease;
             c->pending_position_ = static_cast<uint32_t>(c->position_);

@@ -210,6 +210,66 @@ def test_voicedesign_geometry_predictor_pass_waits_are_bounded(hip, full, monkey
         hip.load().qwen3_tts_session_destroy(s)
 
 
+def test_voicedesign_geometry_predictor_passes_of_concurrent_sessions(hip, full):
+    """Two sessions with frames in flight at once (begin_v2 on both, then
+    finish both): their persistent predictor passes, each needing every CU,
+    are ordered one after the other across the two streams, so nothing
+    waits on a workgroup that cannot start; the codes equal those of the
+    same sessions run one frame at a time."""
+    model, _ = full
+
+    def start(seed):
+        s = session(hip, model, seed)
+        text, codec = prompt(seed)
+        pre = hip.PrefillResult()
+        hip.call("qwen3_tts_session_prefill", s, text.ctypes.data_as(C.POINTER(C.c_int32)),
+                 codec.ctypes.data_as(C.POINTER(C.c_int32)), PROMPT, hip.SamplingConfig(*GREEDY), C.byref(pre))
+        return s
+
+    ts, ps = hip.SamplingConfig(*TALKER_TOPK), hip.SamplingConfig(*PREDICTOR_TOPK)
+    seeds = (11, 12)
+    alone = {}
+    for seed in seeds:
+        s = start(seed)
+        try:
+            out = []
+            for f in range(3):
+                nxt = C.c_uint16()
+                info = hip.CodecFrameInfo()
+                view = hip.DeviceFrameViewV2()
+                view.struct_size = C.sizeof(hip.DeviceFrameViewV2)
+                hip.call("qwen3_tts_session_next_frame_begin_v2", s, 300 + f, ts, ps, C.byref(view))
+                hip.call("qwen3_tts_session_next_frame_finish_v2", s, view.lease_id, None, C.byref(nxt), C.byref(info))
+                got = np.zeros(16, np.uint16)
+                hip.call("qwen3_tts_device_memcpy", got.ctypes.data, view.device_codes, 32)
+                out.append((list(got), nxt.value))
+            alone[seed] = out
+        finally:
+            hip.load().qwen3_tts_session_destroy(s)
+    sessions = [start(seed) for seed in seeds]
+    try:
+        together = {seed: [] for seed in seeds}
+        for f in range(3):
+            print(f"[geometry] concurrent sessions frame {f}", flush=True)
+            views = []
+            for s in sessions:
+                view = hip.DeviceFrameViewV2()
+                view.struct_size = C.sizeof(hip.DeviceFrameViewV2)
+                hip.call("qwen3_tts_session_next_frame_begin_v2", s, 300 + f, ts, ps, C.byref(view))
+                views.append(view)
+            for seed, s, view in zip(seeds, sessions, views):
+                nxt = C.c_uint16()
+                info = hip.CodecFrameInfo()
+                hip.call("qwen3_tts_session_next_frame_finish_v2", s, view.lease_id, None, C.byref(nxt), C.byref(info))
+                got = np.zeros(16, np.uint16)
+                hip.call("qwen3_tts_device_memcpy", got.ctypes.data, view.device_codes, 32)
+                together[seed].append((list(got), nxt.value))
+        assert together == alone
+    finally:
+        for s in sessions:
+            hip.load().qwen3_tts_session_destroy(s)
+
+
 def test_voicedesign_geometry_batched_exact(hip, orc, full, monkeypatch):
     monkeypatch.setenv("QWEN3_TTS_BATCH_GEMV", "exact")
     model, om = full
