@@ -147,6 +147,7 @@ struct ChainLds {
     float y[48];               // scaled dot products of this workgroup's rows
     float residual[8];         // hidden rows 8b..8b+7 (fp32 of the bf16 value)
     CHAIN_TRACE(unsigned long long ts[8];)
+    CHAIN_TRACE(unsigned long long tw[4][8];)  // each compute wave's end of its dot products
 };
 
 __device__ __forceinline__ void compute_qkv(const QkvRegs& r, ChainLds& s) {
@@ -222,6 +223,7 @@ __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, con
     issue_down(rd, wl, sl, o);
     compute_qkv(rq, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[1] = wall_clock64();)
+    CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[0][threadIdx.x >> 6] = wall_clock64();)
     barrier();
     barrier();
     barrier();
@@ -230,6 +232,7 @@ __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, con
     if constexpr (!kLast) issue_qkv(rq, wn, sn, o);
     compute_o(ro, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[3] = wall_clock64();)
+    CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[1][threadIdx.x >> 6] = wall_clock64();)
     barrier();
     barrier();
     barrier();
@@ -238,6 +241,7 @@ __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, con
     if constexpr (!kLast) issue_o(ro, wn, sn, o);
     compute_gu(rg, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[5] = wall_clock64();)
+    CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[2][threadIdx.x >> 6] = wall_clock64();)
     barrier();
     barrier();
     barrier();
@@ -250,6 +254,7 @@ __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, con
     }
     compute_down(rd, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[7] = wall_clock64();)
+    CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[3][threadIdx.x >> 6] = wall_clock64();)
     barrier();
 }
 
@@ -362,7 +367,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 0 + 1] = wall_clock64();)
         norm_stage(s, pt, gq, a.epsilon, true);
         barrier();  // B2: QKV dot products
-        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 0 + 2] = s.ts[0]; a.trace[64 * layer + 8 * 0 + 3] = s.ts[1]; a.trace[64 * layer + 8 * 0 + 4] = wall_clock64(); })
+        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 0 + 2] = s.ts[0]; a.trace[64 * layer + 8 * 0 + 3] = s.ts[1]; a.trace[64 * layer + 8 * 0 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[0][w]); mn = min(mn, s.tw[0][w]); } a.trace[64 * layer + 8 * 0 + 5] = mx; a.trace[64 * layer + 8 * 0 + 6] = mn; })
         if (pt < 8) {
             const unsigned lo = f2bf(s.y[2 * pt]), hi = f2bf(s.y[2 * pt + 1]);
             publish(Q + 8 * b + pt, pack_word(lo, hi, t + 1));
@@ -377,7 +382,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 1 + 1] = wall_clock64();)
         norm_stage(s, pt, gq, a.epsilon, false);
         barrier();  // B2
-        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 1 + 2] = s.ts[2]; a.trace[64 * layer + 8 * 1 + 3] = s.ts[3]; a.trace[64 * layer + 8 * 1 + 4] = wall_clock64(); })
+        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 1 + 2] = s.ts[2]; a.trace[64 * layer + 8 * 1 + 3] = s.ts[3]; a.trace[64 * layer + 8 * 1 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[1][w]); mn = min(mn, s.tw[1][w]); } a.trace[64 * layer + 8 * 1 + 5] = mx; a.trace[64 * layer + 8 * 1 + 6] = mn; })
         if (pt < 4) {
             unsigned r[2];
 #pragma unroll
@@ -394,7 +399,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 2 + 1] = wall_clock64();)
         norm_stage(s, pt, gg, a.epsilon, true);
         barrier();  // B2
-        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 2 + 2] = s.ts[4]; a.trace[64 * layer + 8 * 2 + 3] = s.ts[5]; a.trace[64 * layer + 8 * 2 + 4] = wall_clock64(); })
+        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 2 + 2] = s.ts[4]; a.trace[64 * layer + 8 * 2 + 3] = s.ts[5]; a.trace[64 * layer + 8 * 2 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[2][w]); mn = min(mn, s.tw[2][w]); } a.trace[64 * layer + 8 * 2 + 5] = mx; a.trace[64 * layer + 8 * 2 + 6] = mn; })
         if (pt < 12) {
             unsigned r[2];
 #pragma unroll
@@ -414,7 +419,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 3 + 1] = wall_clock64();)
         norm_stage(s, pt, gg, a.epsilon, false);
         barrier();  // B2
-        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 3 + 2] = s.ts[6]; a.trace[64 * layer + 8 * 3 + 3] = s.ts[7]; a.trace[64 * layer + 8 * 3 + 4] = wall_clock64(); })
+        CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 3 + 2] = s.ts[6]; a.trace[64 * layer + 8 * 3 + 3] = s.ts[7]; a.trace[64 * layer + 8 * 3 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[3][w]); mn = min(mn, s.tw[3][w]); } a.trace[64 * layer + 8 * 3 + 5] = mx; a.trace[64 * layer + 8 * 3 + 6] = mn; })
         if (pt < 4) {
             unsigned r[2];
 #pragma unroll
