@@ -280,9 +280,8 @@ __device__ __forceinline__ void compute_layer(const PredArgs& a, PassLds& s, Com
     // QKV
     AttnOperandsGlobal g;
     if (b < kHeads && wave == 0) issue_attention(g, L, a, b);  // independent of this pass's QKV
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // input staged
+    barrier();  // input normalized
     {
         const float acc = dot_narrow(r.q.w, s.x);
         if (l == 0) s.y[hw] = acc * r.q.s;
@@ -303,9 +302,8 @@ __device__ __forceinline__ void compute_layer(const PredArgs& a, PassLds& s, Com
     if constexpr (kL + 1 < kLayers) issue_layer_o(r, a.layer[kL + 1], b, wave);
     barrier();
     // gate/up
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // input staged
+    barrier();  // input normalized
     if (hw < 12) {
         const int4 wg[2] = {r.gu.w[0], r.gu.w[1]};
         const int4 wu[2] = {r.gu.w[2], r.gu.w[3]};
@@ -360,7 +358,6 @@ __device__ __forceinline__ void compute_path(const PredArgs& a, PassLds& s) {
     if (with_head) {
         barrier();
         barrier();
-        barrier();
         if (hw < 8) {
             const float acc = dot_narrow(head.w, s.x);
             if (l == 0) s.y[hw] = acc * head.s;
@@ -371,23 +368,47 @@ __device__ __forceinline__ void compute_path(const PredArgs& a, PassLds& s) {
 
 // ------------------------------------------------------------- poller waves
 
-// RMSNorm of the staged 1024-wide input in place, the reference's 256-thread
-// order (talker_kernels.cu:14-48): thread t's partial is the fma chain of
-// x[t + 256 i], i = 0..3, the partials fold in the tree of
-// fold_partials256, then each thread normalizes elements 4t..4t+3 with the
-// gain chunk it loaded ahead.
-__device__ __forceinline__ void norm_stage(PassLds& s, int pt, const uint2& gain, float epsilon) {
-    barrier();  // B1a: input staged
-    {
-        float v[4];
+// RMSNorm input of 1024 values (512 words): poller thread q < 128 polls
+// words q + 128 i (i = 0..3), i.e. elements 2q + 256 i and 2q + 1 + 256 i,
+// exactly the inputs of the reference's 256-thread partials t = 2q and
+// t = 2q + 1 (talker_kernels.cu:14-48: thread t's partial is the fma chain
+// of x[t + 256 i], i = 0..3).  It stages the elements and writes both
+// partials, so no barrier separates staging from the partials.
+__device__ __forceinline__ void poll_norm_input(const unsigned long long* src, unsigned tag, PassLds& s, int pt,
+                                                int* status) {
+    if (pt >= 128) return;
+    unsigned long long v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = s.x[x_index<kPH>(pt + 256 * j)];
-        float sum = 0.0f;
+    for (int i = 0; i < 4; ++i) v[i] = read_word(src + pt + 128 * i);
+    unsigned long long t0 = 0;
+    int spins = 0;
+    while (true) {
+        bool stale = false;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sum = fmaf(v[j], v[j], sum);
-        s.partial[pt] = sum;
+        for (int i = 0; i < 4; ++i) stale |= static_cast<unsigned>(v[i] >> 32) != tag;
+        if (!stale) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (static_cast<unsigned>(v[i] >> 32) != tag) v[i] = read_word(src + pt + 128 * i);
+        if (give_up(spins, t0, status)) break;
     }
-    barrier();  // B1b: partials
+    float even = 0.0f, odd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t pair = static_cast<uint32_t>(v[i]);
+        const float lo = __uint_as_float(pair << 16), hi = __uint_as_float(pair & 0xffff0000u);
+        *reinterpret_cast<float2*>(s.x + x_index<kPH>(2 * pt + 256 * i)) = make_float2(lo, hi);
+        even = fmaf(lo, lo, even);
+        odd = fmaf(hi, hi, odd);
+    }
+    *reinterpret_cast<float2*>(s.partial + 2 * pt) = make_float2(even, odd);
+}
+
+// RMSNorm of the staged 1024-wide input in place, after poll_norm_input:
+// the partials fold in the tree of fold_partials256, then each thread
+// normalizes elements 4t..4t+3 with the gain chunk it loaded ahead.
+__device__ __forceinline__ void norm_stage(PassLds& s, int pt, const uint2& gain, float epsilon) {
+    barrier();  // B1a: input staged, partials written
     {
         const float inverse = fold_partials256(s.partial, kPH, epsilon);
         float4* c = reinterpret_cast<float4*>(s.x + x_index<kPH>(4 * pt));
@@ -463,7 +484,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
         const uint2 gq = reinterpret_cast<const uint2*>(L.input_norm)[pt];
         const uint2 gg = reinterpret_cast<const uint2*>(L.post_norm)[pt];
         // ---- QKV: x = hidden (RMSNorm)
-        poll_words<kWordsH>(HA, t - 1u, s.x, pt, a.status);
+        poll_norm_input(HA, t - 1u, s, pt, a.status);
         PRED_STAMP(2 + 10 * layer);
         norm_stage(s, pt, gq, a.epsilon);
         barrier();  // B2
@@ -495,7 +516,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
         residual_epilogue(s, HB, b, pt, t + 2u);
         PRED_STAMP(6 + 10 * layer);
         // ---- gate/up: x = hidden after O (RMSNorm), SiLU gate
-        poll_words<kWordsH>(HB, t + 2u, s.x, pt, a.status);
+        poll_norm_input(HB, t + 2u, s, pt, a.status);
         PRED_STAMP(7 + 10 * layer);
         norm_stage(s, pt, gg, a.epsilon);
         barrier();  // B2
@@ -523,7 +544,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
     // ---- head: final RMSNorm + codebook logits
     if (a.head_w != nullptr) {
         const uint2 gf = reinterpret_cast<const uint2*>(a.final_norm)[pt];
-        poll_words<kWordsH>(HA, base + 5u * kLayers, s.x, pt, a.status);
+        poll_norm_input(HA, base + 5u * kLayers, s, pt, a.status);
         PRED_STAMP(52);
         norm_stage(s, pt, gf, a.epsilon);
         barrier();  // B2
