@@ -81,6 +81,55 @@ __device__ __forceinline__ void poll_words(const unsigned long long* src, unsign
     }
 }
 
+// Stage one RMSNorm input element pair per word and write the reference's
+// 256-thread sum-of-squares partials (talker_kernels.cu:14-48: thread t's
+// partial is the fma chain of x[t + 256 i]^2 in i order).  Thread q < 128
+// holds words q + 128 i, i.e. elements 2q + 256 i and 2q + 1 + 256 i: the
+// inputs of partials t = 2q and t = 2q + 1, so no barrier separates the
+// staging from the partials.
+template <int kK>
+__device__ __forceinline__ void stage_norm_pairs(const uint32_t (&pairs)[kK / 256], float* x, float* partial,
+                                                 int q) {
+    float even = 0.0f, odd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kK / 256; ++i) {
+        const float lo = __uint_as_float(pairs[i] << 16), hi = __uint_as_float(pairs[i] & 0xffff0000u);
+        *reinterpret_cast<float2*>(x + x_index<kK>(2 * q + 256 * i)) = make_float2(lo, hi);
+        even = fmaf(lo, lo, even);
+        odd = fmaf(hi, hi, odd);
+    }
+    *reinterpret_cast<float2*>(partial + 2 * q) = make_float2(even, odd);
+}
+
+// poll_words for an RMSNorm input of kK values (kK / 2 words), staged with
+// its partials by stage_norm_pairs: poller threads 0-127 poll kK / 256 words
+// each, the others return at once.
+template <int kK>
+__device__ __forceinline__ void poll_norm_input(const unsigned long long* src, unsigned tag, float* x,
+                                                float* partial, int pt, int* status) {
+    constexpr int kPer = kK / 256;
+    if (pt >= 128) return;
+    unsigned long long v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = read_word(src + pt + 128 * i);
+    unsigned long long t0 = 0;
+    int spins = 0;
+    while (true) {
+        bool stale = false;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) stale |= static_cast<unsigned>(v[i] >> 32) != tag;
+        if (!stale) break;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (static_cast<unsigned>(v[i] >> 32) != tag) v[i] = read_word(src + pt + 128 * i);
+        if (give_up(spins, t0, status)) break;
+    }
+    uint32_t pairs[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) pairs[i] = static_cast<uint32_t>(v[i]);
+    stage_norm_pairs<kK>(pairs, x, partial, pt);
+}
+
 // One 16-byte weight vector against its 16 activations (fp32 in LDS, the
 // exact values of the bf16 inputs): the reference's fresh 16-term fmaf chain
 // (chain16, int8_gemv.cu:99-112).

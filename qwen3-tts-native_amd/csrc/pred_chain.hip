@@ -270,7 +270,7 @@ __device__ __forceinline__ void issue_layer_d(ComputeRegs& r, const PredLayerArg
     if (wave < 4) issue_wide3(r.d, L.d_w, L.d_s, 4 * b + wave);
 }
 
-// Barriers per stage, matched by the poller path: norm stages B1a, B1b, B1,
+// Barriers per stage, matched by the poller path: norm stages B1a, B1,
 // B2; plain stages B1, B2; the attention (workgroups 0-15) one more.
 template <int kL>
 __device__ __forceinline__ void compute_layer(const PredArgs& a, PassLds& s, ComputeRegs& r, int b, int wave, int hw,
@@ -368,43 +368,8 @@ __device__ __forceinline__ void compute_path(const PredArgs& a, PassLds& s) {
 
 // ------------------------------------------------------------- poller waves
 
-// RMSNorm input of 1024 values (512 words): poller thread q < 128 polls
-// words q + 128 i (i = 0..3), i.e. elements 2q + 256 i and 2q + 1 + 256 i,
-// exactly the inputs of the reference's 256-thread partials t = 2q and
-// t = 2q + 1 (talker_kernels.cu:14-48: thread t's partial is the fma chain
-// of x[t + 256 i], i = 0..3).  It stages the elements and writes both
-// partials, so no barrier separates staging from the partials.
-__device__ __forceinline__ void poll_norm_input(const unsigned long long* src, unsigned tag, PassLds& s, int pt,
-                                                int* status) {
-    if (pt >= 128) return;
-    unsigned long long v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = read_word(src + pt + 128 * i);
-    unsigned long long t0 = 0;
-    int spins = 0;
-    while (true) {
-        bool stale = false;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) stale |= static_cast<unsigned>(v[i] >> 32) != tag;
-        if (!stale) break;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (static_cast<unsigned>(v[i] >> 32) != tag) v[i] = read_word(src + pt + 128 * i);
-        if (give_up(spins, t0, status)) break;
-    }
-    float even = 0.0f, odd = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t pair = static_cast<uint32_t>(v[i]);
-        const float lo = __uint_as_float(pair << 16), hi = __uint_as_float(pair & 0xffff0000u);
-        *reinterpret_cast<float2*>(s.x + x_index<kPH>(2 * pt + 256 * i)) = make_float2(lo, hi);
-        even = fmaf(lo, lo, even);
-        odd = fmaf(hi, hi, odd);
-    }
-    *reinterpret_cast<float2*>(s.partial + 2 * pt) = make_float2(even, odd);
-}
-
-// RMSNorm of the staged 1024-wide input in place, after poll_norm_input:
+// RMSNorm of the staged 1024-wide input in place, after poll_norm_input
+// (input and partials staged):
 // the partials fold in the tree of fold_partials256, then each thread
 // normalizes elements 4t..4t+3 with the gain chunk it loaded ahead.
 __device__ __forceinline__ void norm_stage(PassLds& s, int pt, const uint2& gain, float epsilon) {
@@ -484,7 +449,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
         const uint2 gq = reinterpret_cast<const uint2*>(L.input_norm)[pt];
         const uint2 gg = reinterpret_cast<const uint2*>(L.post_norm)[pt];
         // ---- QKV: x = hidden (RMSNorm)
-        poll_norm_input(HA, t - 1u, s, pt, a.status);
+        poll_norm_input<kPH>(HA, t - 1u, s.x, s.partial, pt, a.status);
         PRED_STAMP(2 + 10 * layer);
         norm_stage(s, pt, gq, a.epsilon);
         barrier();  // B2
@@ -516,7 +481,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
         residual_epilogue(s, HB, b, pt, t + 2u);
         PRED_STAMP(6 + 10 * layer);
         // ---- gate/up: x = hidden after O (RMSNorm), SiLU gate
-        poll_norm_input(HB, t + 2u, s, pt, a.status);
+        poll_norm_input<kPH>(HB, t + 2u, s.x, s.partial, pt, a.status);
         PRED_STAMP(7 + 10 * layer);
         norm_stage(s, pt, gg, a.epsilon);
         barrier();  // B2
@@ -544,7 +509,7 @@ __device__ __forceinline__ void poll_path(const PredArgs& a, PassLds& s) {
     // ---- head: final RMSNorm + codebook logits
     if (a.head_w != nullptr) {
         const uint2 gf = reinterpret_cast<const uint2*>(a.final_norm)[pt];
-        poll_norm_input(HA, base + 5u * kLayers, s, pt, a.status);
+        poll_norm_input<kPH>(HA, base + 5u * kLayers, s.x, s.partial, pt, a.status);
         PRED_STAMP(52);
         norm_stage(s, pt, gf, a.epsilon);
         barrier();  // B2

@@ -96,6 +96,13 @@ __device__ __forceinline__ void poll_words(const unsigned long long* src, unsign
     chain_detail::poll_words<kWords>(src, tag, x, pt, status);
 }
 
+template <int kK>
+__device__ __forceinline__ void poll_norm_input(const unsigned long long* src, unsigned tag, float* x, float* partial,
+                                                int pt, int* status) {
+    CHAIN_TRACE(if (chain_nosync) return;)
+    chain_detail::poll_norm_input<kK>(src, tag, x, partial, pt, status);
+}
+
 // ------------------------------------------------------------ compute waves
 
 struct RowOffsets {
@@ -203,12 +210,13 @@ __device__ __forceinline__ void compute_down(const DownRegs& r, ChainLds& s) {
     if (lane == 0) s.y[threadIdx.x >> 6] = acc * r.s;
 }
 
-// Four barriers per GEMV on both paths: B1a (input staged), B1b (norm
-// partials), B1 (normalized input ready), B2 (dot products in LDS).
+// Barriers per GEMV on both paths: for the normalized inputs (QKV,
+// gate/up) B1a (input and norm partials staged), B1 (normalized input
+// ready), B2 (dot products in LDS); for O and down B1 (input staged), B2.
 __device__ __forceinline__ void barrier() { __syncthreads(); }
 
-// Per GEMV: B1a, B1b, B1 (input ready), the loads of the GEMV three ahead,
-// the dot products, B2.
+// Per GEMV: [B1a,] B1 (input ready), the loads of the GEMV three ahead, the
+// dot products, B2.
 template <bool kLast>
 __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, const RowOffsets& o, ChainLds& s,
                                               QkvRegs& rq, ORegs& ro, GuRegs& rg, DownRegs& rd) {
@@ -216,36 +224,30 @@ __device__ __forceinline__ void compute_layer(const ChainArgs& a, int layer, con
     const float* sl = a.scales + a.scale_layer_stride * layer;
     const int8_t* wn = wl + a.weight_layer_stride;
     const float* sn = sl + a.scale_layer_stride;
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // B1a
+    barrier();  // B1
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[0] = wall_clock64();)
     issue_down(rd, wl, sl, o);
     compute_qkv(rq, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[1] = wall_clock64();)
     CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[0][threadIdx.x >> 6] = wall_clock64();)
-    barrier();
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // B2
+    barrier();  // B1
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[2] = wall_clock64();)
     if constexpr (!kLast) issue_qkv(rq, wn, sn, o);
     compute_o(ro, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[3] = wall_clock64();)
     CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[1][threadIdx.x >> 6] = wall_clock64();)
-    barrier();
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // B2
+    barrier();  // B1a
+    barrier();  // B1
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[4] = wall_clock64();)
     if constexpr (!kLast) issue_o(ro, wn, sn, o);
     compute_gu(rg, s);
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[5] = wall_clock64();)
     CHAIN_TRACE(if ((threadIdx.x & 63) == 0) s.tw[2][threadIdx.x >> 6] = wall_clock64();)
-    barrier();
-    barrier();
-    barrier();
-    barrier();
+    barrier();  // B2
+    barrier();  // B1
     CHAIN_TRACE(if (threadIdx.x == 0) s.ts[6] = wall_clock64();)
     if constexpr (!kLast) {
         issue_gu<0>(rg, wn, sn, o);
@@ -290,24 +292,13 @@ __device__ __forceinline__ void compute_path(const ChainArgs& a, ChainLds& s) {
 
 // ------------------------------------------------------------- poller waves
 
-// RMSNorm of the staged input in place, the reference's 256-thread order
-// (talker_kernels.cu:14-48): poller thread t's partial is the fma chain of
-// x[t + 256 i]^2, i = 0..7 (block_partial_sq), the partials fold in the tree
-// of fold_partials256, then each thread normalizes its own 16-byte chunk
-// with the gain chunk it loaded ahead.
-__device__ __forceinline__ void norm_stage(ChainLds& s, int pt, const uint4& gain, float epsilon, bool norm) {
-    barrier();  // B1a: input staged
-    if (norm) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = s.x[x_index<kH>(pt + 256 * j)];
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sum = fmaf(v[j], v[j], sum);
-        s.partial[pt] = sum;
-    }
-    barrier();  // B1b: partials
-    if (norm) {
+// RMSNorm of the staged input in place, after poll_norm_input (input and the
+// reference's 256-thread partials staged, talker_kernels.cu:14-48): the
+// partials fold in the tree of fold_partials256, then each thread
+// normalizes its own 16-byte chunk with the gain chunk it loaded ahead.
+__device__ __forceinline__ void norm_stage(ChainLds& s, int pt, const uint4& gain, float epsilon) {
+    barrier();  // B1a: input and partials staged
+    {
         const float inverse = fold_partials256(s.partial, kH, epsilon);
         // elements 8pt..8pt+7: quarters 2(pt%2), 2(pt%2)+1 of vector pt/2
         float4* c0 = reinterpret_cast<float4*>(s.x + x_index<kH>(8 * pt));
@@ -345,15 +336,16 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         const uint4 gg = reinterpret_cast<const uint4*>(a.gain_gu + a.gain_layer_stride * layer)[pt];
         // ---- QKV: x = hidden
         if (layer == 0) {
-            const uint4 v = reinterpret_cast<const uint4*>(a.hidden)[pt];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            float4* chunk0 = reinterpret_cast<float4*>(s.x + x_index<kH>(8 * pt));
-            float4* chunk1 = reinterpret_cast<float4*>(s.x + x_index<kH>(8 * pt + 4));
-            *chunk0 = make_float4(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
-                                   __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u));
-            *chunk1 = make_float4(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u),
-                                   __uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u));
+            if (pt < 128) {
+                const uint32_t* row = reinterpret_cast<const uint32_t*>(a.hidden);
+                uint32_t pairs[kH / 256];
+#pragma unroll
+                for (int i = 0; i < kH / 256; ++i) pairs[i] = row[pt + 128 * i];
+                chain_detail::stage_norm_pairs<kH>(pairs, s.x, s.partial, pt);
+            }
             if (pt == b) {  // this workgroup's residual rows 8b..8b+7
+                const uint4 v = reinterpret_cast<const uint4*>(a.hidden)[b];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     s.residual[2 * i] = __uint_as_float(w[i] << 16);
@@ -362,10 +354,10 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
             }
         } else {
             CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 0 + 0] = wall_clock64();)
-            poll_words<kWordsH>(H, t, s.x, pt, a.status);
+            poll_norm_input<kH>(H, t, s.x, s.partial, pt, a.status);
         }
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 0 + 1] = wall_clock64();)
-        norm_stage(s, pt, gq, a.epsilon, true);
+        norm_stage(s, pt, gq, a.epsilon);
         barrier();  // B2: QKV dot products
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 0 + 2] = s.ts[0]; a.trace[64 * layer + 8 * 0 + 3] = s.ts[1]; a.trace[64 * layer + 8 * 0 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[0][w]); mn = min(mn, s.tw[0][w]); } a.trace[64 * layer + 8 * 0 + 5] = mx; a.trace[64 * layer + 8 * 0 + 6] = mn; })
         if (pt < 8) {
@@ -380,7 +372,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 1 + 0] = wall_clock64();)
         poll_words<kWordsH>(Q, t + 1, s.x, pt, a.status);
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 1 + 1] = wall_clock64();)
-        norm_stage(s, pt, gq, a.epsilon, false);
+        barrier();  // B1
         barrier();  // B2
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 1 + 2] = s.ts[2]; a.trace[64 * layer + 8 * 1 + 3] = s.ts[3]; a.trace[64 * layer + 8 * 1 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[1][w]); mn = min(mn, s.tw[1][w]); } a.trace[64 * layer + 8 * 1 + 5] = mx; a.trace[64 * layer + 8 * 1 + 6] = mn; })
         if (pt < 4) {
@@ -395,9 +387,9 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         }
         // ---- gate/up: x = hidden after O, RMSNorm, SiLU gate
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 2 + 0] = wall_clock64();)
-        poll_words<kWordsH>(H2, t + 2, s.x, pt, a.status);
+        poll_norm_input<kH>(H2, t + 2, s.x, s.partial, pt, a.status);
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 2 + 1] = wall_clock64();)
-        norm_stage(s, pt, gg, a.epsilon, true);
+        norm_stage(s, pt, gg, a.epsilon);
         barrier();  // B2
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 2 + 2] = s.ts[4]; a.trace[64 * layer + 8 * 2 + 3] = s.ts[5]; a.trace[64 * layer + 8 * 2 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[2][w]); mn = min(mn, s.tw[2][w]); } a.trace[64 * layer + 8 * 2 + 5] = mx; a.trace[64 * layer + 8 * 2 + 6] = mn; })
         if (pt < 12) {
@@ -417,7 +409,7 @@ __device__ __forceinline__ void poll_path(const ChainArgs& a, ChainLds& s) {
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 3 + 0] = wall_clock64();)
         poll_words<kWordsAct>(A, t + 3, s.x, pt, a.status);
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) a.trace[64 * layer + 8 * 3 + 1] = wall_clock64();)
-        norm_stage(s, pt, gg, a.epsilon, false);
+        barrier();  // B1
         barrier();  // B2
         CHAIN_TRACE(if (a.trace && b == 0 && pt == 0) { a.trace[64 * layer + 8 * 3 + 2] = s.ts[6]; a.trace[64 * layer + 8 * 3 + 3] = s.ts[7]; a.trace[64 * layer + 8 * 3 + 4] = wall_clock64(); unsigned long long mx = 0, mn = ~0ull; for (int w = 0; w < kComputeWaves; ++w) { mx = max(mx, s.tw[3][w]); mn = min(mn, s.tw[3][w]); } a.trace[64 * layer + 8 * 3 + 5] = mx; a.trace[64 * layer + 8 * 3 + 6] = mn; })
         if (pt < 4) {
