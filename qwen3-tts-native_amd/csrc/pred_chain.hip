@@ -238,7 +238,18 @@ __device__ __forceinline__ void run_attention(const AttnOperandsGlobal& g, const
     bf16_t* vrun0 = L.value_cache + (static_cast<size_t>(kvh) * 2 * 128 + lane) * 8;
     bf16_t* kdst = head % kGroup == 0 ? L.key_cache + static_cast<size_t>(position) * kKvW + kvh * 128 : nullptr;
     float acc0, acc1;
+#ifdef Q3_PRED_TRACE
+    const int trace_base = 64 + 8 * static_cast<int>((tag - 2u - *a.epoch) / 5u);
+    PRED_STAMP(trace_base);
+    struct Stamp {
+        int base;
+        __device__ void operator()(int k) const { PRED_STAMP(base + k); }
+    };
+    short_attn::core<true>(in, position, a.epsilon, a.scale, kdst, vrun0, vrun0 + 64 * 8, acc0, acc1,
+                           Stamp{trace_base});
+#else
     short_attn::core<true>(in, position, a.epsilon, a.scale, kdst, vrun0, vrun0 + 64 * 8, acc0, acc1);
+#endif
     // dimensions (lane, lane + 1) and (lane + 64, lane + 65) from the even lanes
     const unsigned b0 = f2bf(acc0), b1 = f2bf(acc1);
     const unsigned n0 = static_cast<unsigned>(__shfl_xor(static_cast<int>(b0), 1, 64));
@@ -248,6 +259,9 @@ __device__ __forceinline__ void run_attention(const AttnOperandsGlobal& g, const
         publish(att + lane / 2, pack_word(b0, n0, tag));
         publish(att + 32 + lane / 2, pack_word(b1, n1, tag));
     }
+#ifdef Q3_PRED_TRACE
+    PRED_STAMP(trace_base + 5);  // attention outputs published
+#endif
 }
 
 struct ComputeRegs {

@@ -46,9 +46,14 @@ struct Operands {
 // `position`) non-null: the normalized, rotated key is written there and the
 // value into the blocked value runs vrun0 / vrun1 (group 0 of dimensions
 // lane and lane + 64).  One wave; no barrier.
-template <bool kExact>
+// Stage hook of core (a diagnostic build's stamps); the default does nothing.
+struct NoHook {
+    __device__ void operator()(int) const {}
+};
+
+template <bool kExact, typename Hook = NoHook>
 __device__ __forceinline__ void core(const Operands& in, int position, float epsilon, float scale, bf16_t* key_dst,
-                                     bf16_t* vrun0, bf16_t* vrun1, float& acc0, float& acc1) {
+                                     bf16_t* vrun0, bf16_t* vrun1, float& acc0, float& acc1, Hook hook = Hook()) {
     __shared__ uint4 rows_lds[2][kCapacity][kDim / 8];  // rope, keys
     __shared__ uint4 head_lds[5][kDim / 8];             // q, k, v, q gain, k gain
     const int lane = threadIdx.x & 63;
@@ -96,6 +101,7 @@ __device__ __forceinline__ void core(const Operands& in, int position, float eps
         }
     }
 
+    hook(1);
     // 2. head norm + RoPE of the query head and the new key; the append
     bf16_t q0b, q1b, kn0, kn1;
     head_detail::norm_rope_from(q_in, epsilon, q0b, q1b);
@@ -121,6 +127,7 @@ __device__ __forceinline__ void core(const Operands& in, int position, float eps
         }
     }
 
+    hook(2);
     // 3. scores.  Lane L = 16 j + p works on position p and the tree's
     //    entries t = 8 j + i (i < 8) of level 32: it forms
     //    (P[t] + P[t+64]) + (P[t+32] + P[t+96]) itself (P = q*k), receives
@@ -196,6 +203,7 @@ __device__ __forceinline__ void core(const Operands& in, int position, float eps
     //    levels 128 and 64 only add zeros here (a wave shuffle-down tree),
     //    the value chains take the unnormalized exponentials, and the
     //    output is scaled by the inverse once.
+    hook(3);
     const float maximum = wave_max(score);
     const float e = live ? q3_expf(score - maximum) : 0.0f;
     float inverse;
@@ -215,6 +223,7 @@ __device__ __forceinline__ void core(const Operands& in, int position, float eps
 #pragma unroll
     for (int p = 0; p < kCapacity; ++p) pv[p] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prob), p));
 
+    hook(4);
     // 5. value chains for dimensions lane and lane + 64, positions in order.
     //    Past the current position the value is replaced by 0 (and its
     //    probability is 0): fmaf(0, 0, acc) == acc exactly, for every acc the

@@ -65,6 +65,10 @@ def main(frames: int = 40) -> None:
         o = 10 * layer
         print("%d | " % layer + " | ".join("%.2f" % us(i + o) for i in range(2, 11)))
     print("head in %.2f, logits written %.2f us" % (us(52), us(53)))
+    print("attention of head 0 | start | operands staged | norm + RoPE | scores | probabilities | published")
+    for layer in range(5):
+        o = 64 + 8 * layer
+        print("%d | " % layer + " | ".join("%.2f" % us(o + k) for k in range(6)))
 
 
 if __name__ == "__main__":
