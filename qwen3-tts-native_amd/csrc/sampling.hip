@@ -28,6 +28,20 @@ constexpr int kCandidateCap = 1024;
 // survivors ranked by eight lanes each (all 1024 threads)
 constexpr int kRankParallelCap = kSampleThreads / 8;
 
+// Build-time diagnostic: -DQ3_SAMPLE_TRACE records the wall-clock time of
+// the sampler's phases (thread 0 of block 0) in q3_sample_trace.
+#ifdef Q3_SAMPLE_TRACE
+__device__ unsigned long long q3_sample_trace[16];
+#define SAMPLE_STAMP(i)                                                         \
+    do {                                                                        \
+        if (blockIdx.x == 0 && threadIdx.x == 0) q3_sample_trace[i] = wall_clock64(); \
+    } while (0)
+#else
+#define SAMPLE_STAMP(i) \
+    do {                \
+    } while (0)
+#endif
+
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v);
@@ -105,6 +119,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
     // the generator state, requested now and used at the very end
     uint64_t random_state = (tid == 0 && a.random_state != nullptr) ? *a.random_state : 0ull;
     const bool penalize = a.suppress && a.penalty != 1.0f;
+    SAMPLE_STAMP(0);
 
     // The logits are requested first (they do not depend on the history).
     constexpr int kPerThread = kMaxVocabulary / kSampleThreads;
@@ -137,6 +152,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
         values[t] = value;
     }
     __syncthreads();
+    SAMPLE_STAMP(1);
 
     const bool direct = a.do_sample != 0 && a.top_k == 0 && a.top_p >= 1.0f;
     const int selections = a.do_sample == 0 ? 1 : (a.top_k == 0 ? V : min(a.top_k, V));
@@ -272,6 +288,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
             __syncthreads();
             if (s_total <= kRankParallelCap) break;  // block-uniform
         }
+        SAMPLE_STAMP(2);
         // keys >= threshold: the chosen bin's prefix with the unresolved
         // low bits zero
         const uint32_t threshold = s_prefix;
@@ -289,6 +306,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
         }
         __syncthreads();
         const int n = s_count;
+        SAMPLE_STAMP(3);
         // Rank counting over the survivors: exact total order.  The packed
         // key compares like (value desc, index asc) (order_key is monotone,
         // -0 == +0).
@@ -337,6 +355,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
             }
         }
         __syncthreads();
+        SAMPLE_STAMP(4);
         const float maximum = sorted_v[0] / a.temperature;
         // (entries selections .. 63 are 0 for the wave-0 sums below)
         const int weight_count = selections <= 64 ? 64 : selections;
@@ -344,6 +363,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
             weights[r] = r < selections ? exp(static_cast<double>(sorted_v[r] / a.temperature - maximum)) : 0.0;
         }
         __syncthreads();
+        SAMPLE_STAMP(5);
         if (selections <= 64) {
             // Wave 0.  Every running sum of the reference is a prefix sum in
             // rank order, so one sequential pass (all lanes, LDS broadcast
@@ -365,22 +385,36 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
                     }
                 }
                 const double denominator = running;
-                shares[lane] = lane < selections ? weights[lane] / denominator : 0.0;
-                __builtin_amdgcn_wave_barrier();
-                double share_running = 0.0;
-                for (int r0 = 0; r0 < steps; r0 += 8) {
+                // The top-p cut: the first r whose running sum of shares
+                // w_r / denominator reaches top_p.  With top_p >= 1 it can
+                // only fall on the last candidate (and then keeps them all)
+                // when the smallest weight exceeds 1e-12 of the denominator:
+                // for r below the last, the tail sum w_(r+1).. >= w_last, and
+                // the computed running share is at most (1 - w_last / W)(1 +
+                // 130 u) with W the exact weight sum and u = 2^-53 (the
+                // denominator's and the sum's rounding over <= 64 terms), which
+                // stays below 1.  Otherwise the running shares are formed in
+                // order as the reference does.
+                int retained = selections;
+                if (!(a.top_p >= 1.0f && weights[selections - 1] > 1e-12 * denominator)) {
+                    shares[lane] = lane < selections ? weights[lane] / denominator : 0.0;
+                    __builtin_amdgcn_wave_barrier();
+                    double share_running = 0.0;
+                    for (int r0 = 0; r0 < steps; r0 += 8) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        share_running += shares[r0 + u];
-                        cumulative_lds[r0 + u] = share_running;
+                        for (int u = 0; u < 8; ++u) {
+                            share_running += shares[r0 + u];
+                            cumulative_lds[r0 + u] = share_running;
+                        }
                     }
+                    __builtin_amdgcn_wave_barrier();
+                    const double share_mine = cumulative_lds[lane];
+                    const unsigned long long cut =
+                        __ballot(lane < selections && share_mine >= static_cast<double>(a.top_p));
+                    if (cut) retained = __ffsll(static_cast<long long>(cut));
                 }
                 __builtin_amdgcn_wave_barrier();
                 const double prefix_mine = prefix_lds[lane];
-                const double share_mine = cumulative_lds[lane];
-                const unsigned long long cut =
-                    __ballot(lane < selections && share_mine >= static_cast<double>(a.top_p));
-                const int retained = cut ? __ffsll(static_cast<long long>(cut)) : selections;
                 // sum of weights[0..retained) in order: prefix retained-1
                 const double retained_total =
                     __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(prefix_mine), retained - 1),
@@ -425,6 +459,7 @@ __device__ __forceinline__ void sample_one(const SampleArgs& a) {
         selected = s_best;
     }
 
+    SAMPLE_STAMP(6);
     if (tid == 0) {
         if (a.selected) *a.selected = selected;
         if (a.store_tokens) {

@@ -317,6 +317,27 @@ def test_sampler_topk_matches_oracle(hip, orc, top_k, top_p, vocab, suppress, pe
         state = rstate
 
 
+@pytest.mark.parametrize("top_p", [1.0, 0.999999])
+def test_sampler_topk_wide_spread_matches_oracle(hip, orc, top_p):
+    """Top-k 50 whose logits span ~75 units: the smallest kept weight is
+    below 1e-12 of their sum, so with top_p >= 1 the sampler cannot skip the
+    running-share pass (its shortcut needs a larger smallest weight) and
+    forms the shares in order; the token and the next RNG state equal the
+    oracle's."""
+    rng = np.random.default_rng(77)
+    state = 0x2468ACE
+    for trial in range(8):
+        raw = rng.standard_normal(2048).astype(np.float32) - 40.0
+        top = rng.choice(2048, 50, replace=False)
+        raw[top] = np.linspace(30.0, -45.0, 50, dtype=np.float32) + rng.standard_normal(50).astype(np.float32) * 0.1
+        logits = gen.bf16(raw)
+        cfg = hip.sampling(1, 50, top_p, 0.9, 1.0)
+        got, gstate = sample_gpu(hip, logits, False, [], cfg, state)
+        ref, rstate = orc.sample_logits(logits, False, 2150, [], 1, 50, top_p, 0.9, 1.0, state)
+        assert (got, gstate) == (ref, rstate), trial
+        state = rstate
+
+
 @pytest.mark.parametrize("pattern", ["all_nan", "half_nan", "nan_and_inf"])
 def test_sampler_nan_logits_select_in_range(hip, pattern):
     """Logits with NaNs (a diverged model) still yield a token inside the
